@@ -1,0 +1,138 @@
+"""Model forwards composed from oracle ops (TEST INFRASTRUCTURE ONLY).
+
+Composition follows the reference modules op by op:
+  Sequential          src/nn/sequential.hpp:18-25
+  Linear              src/nn/linear.hpp:28-34      (matmul then broadcast add)
+  Conv2d / MaxPool2d  src/nn/linear.hpp:59-61, src/nn/pooling.hpp:33
+  Flatten             src/nn/linear.hpp:66-73
+  GELU                src/nn/activations.hpp:31-38
+  LayerNorm           src/nn/normalization.hpp:29-34
+  MultiHeadAttention  src/nn/attention.hpp:34-104
+  TransformerBlock    demos/multigpu/gpt3_multi_gpu_demo.py:105-114 (pre-LN)
+  DecoderLM           demos/multigpu/gpt3_multi_gpu_demo.py:149-172 with the
+                      nn::Embedding gather path (src/nn/linear.hpp:95-128)
+The UNet (and its ConvTranspose2d) has no reference counterpart; its oracle is
+the brute-force definition below, using the reference's conv fallback
+convention for low precision (fp32 compute, one rounding at the output).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from munet_amd import models as mm
+from munet_amd import synth
+
+from . import CpuOracle
+
+
+def _dt(cfg):
+    return synth.DTYPE_CODES[cfg.get("dtype", "float32")]
+
+
+def conv_transpose2d(o: CpuOracle, x, w, b, stride, dt):
+    """Build-defined ConvTranspose2d with kernel == stride (no overlap):
+    out[b,oc,oh,ow] = bias[oc] + sum_ic x[b,ic,oh//s,ow//s] * w[ic,oc,oh%s,ow%s]
+    computed in float64 from the decoded operands, rounded once."""
+    xf = o.decode(x, dt).astype(np.float64)
+    wf = o.decode(w, dt).astype(np.float64)
+    bf = o.decode(b, dt).astype(np.float64)
+    B, iC, iH, iW = xf.shape
+    _, oC, k, _ = wf.shape
+    assert k == stride
+    out = np.einsum("bihw,iokl->bohkwl", xf, wf).reshape(B, oC, iH * k, iW * k)
+    out += bf[None, :, None, None]
+    return o.encode(out.astype(np.float32), dt)
+
+
+def block_forward(o: CpuOracle, cfg, p, x, prefix, causal):
+    dt = _dt(cfg)
+    eps = cfg.get("eps", 1e-5)
+    h = o.layer_norm(x, p[prefix + "ln1.weight"], p[prefix + "ln1.bias"], dt, eps)
+    a = o.mha(h, p, cfg["num_heads"], causal, dt, prefix=prefix + "attn.")
+    x = o.add(x, a, dt)
+    h2 = o.layer_norm(x, p[prefix + "ln2.weight"], p[prefix + "ln2.bias"], dt, eps)
+    f = o.linear(h2, p[prefix + "ff.0.weight"], p[prefix + "ff.0.bias"], dt)
+    f = o.gelu(f, dt)
+    f = o.linear(f, p[prefix + "ff.2.weight"], p[prefix + "ff.2.bias"], dt)
+    return o.add(x, f, dt)
+
+
+def decoder_embed(o: CpuOracle, cfg, p, ids):
+    dt = _dt(cfg)
+    B, T = ids.shape
+    tok = o.embedding(ids, p["token_embed.weight"], dt)
+    pos_ids = np.tile(np.arange(T, dtype=np.int32), (B, 1))
+    pos = o.embedding(pos_ids, p["pos_embed.weight"], dt)
+    return o.add(tok, pos, dt)
+
+
+def decoder_forward(o: CpuOracle, cfg, p, ids, layers=None):
+    dt = _dt(cfg)
+    x = decoder_embed(o, cfg, p, ids)
+    n = cfg["num_layers"] if layers is None else layers
+    for i in range(n):
+        x = block_forward(o, cfg, p, x, f"blocks.{i}.", True)
+    x = o.layer_norm(x, p["ln_f.weight"], p["ln_f.bias"], dt, cfg.get("eps", 1e-5))
+    return o.linear(x, p["head.weight"], p["head.bias"], dt)
+
+
+def unet_forward(o: CpuOracle, cfg, p, x):
+    dt = _dt(cfg)
+    skips = {}
+    L = len(cfg["channels"])
+    for name, kind, _ic, _oc, _k, s, pad in mm.unet_layers(cfg):
+        w, b = p[name + ".weight"], p[name + ".bias"]
+        if kind == "convt":
+            x = conv_transpose2d(o, x, w, b, s, dt)
+            lvl = int(name[2:])
+            x = o.concat([x, skips[lvl]], 1, dt)
+            continue
+        x = o.conv2d(x, w, b, s, pad, dt)
+        if name != "head":
+            x = o.relu(x, dt)
+        if name.startswith("enc") and name.endswith(".1"):
+            lvl = int(name[3:-2])
+            if lvl < L - 1:
+                skips[lvl] = x
+    return x
+
+
+def layer_forward(o: CpuOracle, layer, p, prefix, x, dt):
+    t = layer["type"]
+    if t == "Linear":
+        return o.linear(x, p[prefix + "weight"], p.get(prefix + "bias"), dt)
+    if t == "ReLU":
+        return o.relu(x, dt)
+    if t == "Sigmoid":
+        return o.sigmoid(x, dt)
+    if t == "GELU":
+        return o.gelu(x, dt)
+    if t == "Conv2d":
+        return o.conv2d(x, p[prefix + "weight"], p[prefix + "bias"], layer["stride"], layer["padding"], dt)
+    if t == "MaxPool2d":
+        return o.max_pool2d(x, layer["kernel_size"], layer["stride"], layer["padding"], dt)
+    if t == "Upsample":
+        return o.upsample2d(x, layer["scale_factor"], dt)
+    if t == "Flatten":
+        return x.reshape(x.shape[0], -1)
+    if t == "LayerNorm":
+        return o.layer_norm(x, p[prefix + "weight"], p[prefix + "bias"], dt, layer.get("eps", 1e-5))
+    if t == "MultiHeadAttention":
+        return o.mha(x, p, layer["num_heads"], layer.get("causal", True), dt, prefix=prefix)
+    raise ValueError(f"oracle: unsupported layer {t}")
+
+
+def forward(o: CpuOracle, cfg, p, x):
+    t = cfg["type"]
+    dt = _dt(cfg)
+    if t == "Sequential":
+        for i, layer in enumerate(cfg["layers"]):
+            x = layer_forward(o, layer, p, f"{i}.", x, dt)
+        return x
+    if t == "TransformerBlock":
+        return block_forward(o, cfg, p, x, "", cfg.get("causal", False))
+    if t == "DecoderLM":
+        return decoder_forward(o, cfg, p, x)
+    if t == "UNet":
+        return unet_forward(o, cfg, p, x)
+    return layer_forward(o, cfg, p, "", x, dt)
