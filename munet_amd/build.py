@@ -1,0 +1,86 @@
+"""Build the MI355X HIP backend libraries in-tree with hipcc (gfx950 only).
+
+Outputs (next to this file):
+  libmunet_hip.so             kernels + C ABI + engine (include/munet_hip.h,
+                              include/munet_hip_engine.h)
+  libmunet_backend_hip.so     MuNet plugin-probe library (5 discovery symbols,
+                              reference src/backend/plugin_loader.cpp:122-131)
+
+Run ``python -m munet_amd.build`` (or ``__graft_entry__.build()``).
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+BUILD = os.path.join(HERE, "_build")
+LIB = os.path.join(HERE, "libmunet_hip.so")
+PLUGIN = os.path.join(HERE, "libmunet_backend_hip.so")
+ARCH = "gfx950"
+
+KERNEL_SOURCES = ["gemm.hip", "attention.hip", "eltwise.hip", "norm.hip", "layout.hip"]
+HOST_SOURCES = ["capi.cpp", "engine.cpp", "backend.cpp"]
+PLUGIN_SOURCES = ["plugin.cpp"]
+
+
+def hipcc():
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (ROCm required to build the HIP backend)")
+
+
+def _flags():
+    return [
+        "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+        # packed fp32 ops stay off: some of their forms have produced wrong
+        # results on these machines
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-I", os.path.join(ROOT, "include"), "-I", CSRC,
+        "-Wno-unused-result",
+    ]
+
+
+def _compile(src: str) -> str:
+    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    cmd = [hipcc()] + _flags() + ["-c", os.path.join(CSRC, src), "-o", obj]
+    if src.endswith(".cpp"):
+        cmd = [hipcc()] + _flags() + ["-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stderr}")
+    return obj
+
+
+def build(verbose: bool = True) -> None:
+    os.makedirs(BUILD, exist_ok=True)
+    srcs = [s for s in KERNEL_SOURCES + HOST_SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        objs = list(ex.map(_compile, srcs))
+    tmp = LIB + ".tmp"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs + ["-lpthread"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stderr}")
+    os.replace(tmp, LIB)
+    psrc = [os.path.join(CSRC, s) for s in PLUGIN_SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    if psrc:
+        tmp = PLUGIN + ".tmp"
+        cmd = ["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-o", tmp] + psrc + ["-ldl"]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"plugin build failed: {' '.join(cmd)}\n{res.stderr}")
+        os.replace(tmp, PLUGIN)
+    if verbose:
+        print(f"built {LIB}" + (f" and {PLUGIN}" if psrc else ""))
+
+
+if __name__ == "__main__":
+    build()
+    sys.exit(0)

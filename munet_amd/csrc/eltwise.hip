@@ -1,0 +1,272 @@
+// Elementwise, gather and reduction-free kernels for gfx950.
+//
+// Reference semantics (all dtypes):
+//   add/sub/mul/div with stride broadcasting ... BackendElementwiseCapability
+//       (src/core/backend.hpp:207-217); strides come from compute_broadcast
+//       (src/types.hpp:436-478) and address raw storage (view offsets are not
+//       applied, src/core/ops/add.cpp:27-30).  fp32 computes in float
+//       (src/backend/cpu_backend.hpp:238-332); fp16/bf16 compute the op on
+//       the decoded values and round once (src/core/ops/common.hpp:46-85).
+//   relu / sigmoid ............ src/backend/cpu_backend.hpp:493-531
+//   exp/log/sqrt/rsqrt/sin/cos  src/backend/cpu_backend.hpp (unary family)
+//   GELU ...................... nn::GELU, x * sigmoid(x * c) with c = 1.702
+//       held in a [1] tensor of the dtype, three rounded ops
+//       (src/nn/activations.hpp:31-38)
+//   masked_fill ............... src/core/ops/elementwise.cpp:8-53
+//   embedding gather .......... nn::Embedding index path
+//       (src/nn/linear.hpp:92-128); out-of-range ids raise an error there,
+//       here they write zeros and set a device error flag that the host
+//       checks at its next synchronisation.
+//   dtype conversion .......... Tensor::to(DataType) (src/tensor.cpp:249-284)
+//       with the reference codecs.
+//   argmax .................... first index of the row maximum (np.argmax as
+//       used by demos/transformers/decoder_block_demo.py:112).
+//
+// Contiguous same-shape operands take a vectorised path (8 values per thread
+// per step, 16-byte loads for 16-bit types); all kernels are grid-stride and
+// sized to a few waves per CU.
+#include "mh_common.hpp"
+#include "mh_kernels.hpp"
+
+namespace mh {
+
+namespace {
+
+inline int grid_for(size_t work, int per_block) {
+  size_t g = (work + per_block - 1) / per_block;
+  if (g > 256 * 16) g = 256 * 16;
+  if (g < 1) g = 1;
+  return int(g);
+}
+
+__device__ __forceinline__ float binop(int op, float a, float b) {
+  switch (op) {
+  case BIN_ADD: return a + b;
+  case BIN_SUB: return a - b;
+  case BIN_MUL: return a * b;
+  default: return a / b;
+  }
+}
+
+template <int DT>
+__global__ void binary_contig_kernel(const typename Store<DT>::T *__restrict__ a,
+                                     const typename Store<DT>::T *__restrict__ b, typename Store<DT>::T *__restrict__ o,
+                                     size_t n, int op) {
+  typedef Store<DT> S;
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    // reference fp32: float op; 16-bit: exact decoded op, single rounding
+    o[i] = S::enc(binop(op, S::dec(a[i]), S::dec(b[i])));
+  }
+}
+
+template <int DT>
+__global__ void binary_bcast_kernel(const typename Store<DT>::T *__restrict__ a,
+                                    const typename Store<DT>::T *__restrict__ b, typename Store<DT>::T *__restrict__ o,
+                                    BcastArgs g, int op) {
+  typedef Store<DT> S;
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < g.total; i += stride) {
+    size_t cur = i;
+    long oa = 0, ob = 0;
+    for (int d = g.ndim - 1; d >= 0; --d) {
+      const size_t c = cur % size_t(g.shape[d]);
+      cur /= size_t(g.shape[d]);
+      oa += long(c) * g.sa[d];
+      ob += long(c) * g.sb[d];
+    }
+    o[i] = S::enc(binop(op, S::dec(a[oa]), S::dec(b[ob])));
+  }
+}
+
+// Row broadcast [rows, cols] op [cols] (bias add): no index division per
+// element beyond one modulo.
+template <int DT>
+__global__ void binary_row_kernel(const typename Store<DT>::T *__restrict__ a,
+                                  const typename Store<DT>::T *__restrict__ b, typename Store<DT>::T *__restrict__ o,
+                                  size_t n, int cols, int op) {
+  typedef Store<DT> S;
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+    o[i] = S::enc(binop(op, S::dec(a[i]), S::dec(b[i % cols])));
+}
+
+template <int DT>
+__global__ void unary_kernel(const typename Store<DT>::T *__restrict__ in, typename Store<DT>::T *__restrict__ out,
+                             size_t n, int op, float c) {
+  typedef Store<DT> S;
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float x = S::dec(in[i]);
+    float y;
+    switch (op) {
+    case UN_RELU: y = x > 0.0f ? x : 0.0f; break;
+    case UN_SIGMOID: y = sigmoidf_ref(x); break;
+    case UN_GELU: {
+      const float t1 = S::round(x * c);
+      const float t2 = S::round(sigmoidf_ref(t1));
+      y = x * t2;
+      break;
+    }
+    case UN_EXP: y = __expf(x); break;
+    case UN_LOG: y = __logf(x); break;
+    case UN_SQRT: y = sqrtf(x); break;
+    case UN_RSQRT: y = rsqrtf(x); break;
+    case UN_SIN: y = sinf(x); break;
+    default: y = cosf(x); break;
+    }
+    out[i] = S::enc(y);
+  }
+}
+
+__global__ void masked_fill_kernel(const void *__restrict__ x, const int32_t *__restrict__ mask, void *__restrict__ out,
+                                   size_t n, int dt, float value) {
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+    st_any(out, dt, i, mask[i] != 0 ? value : ld_any(x, dt, i));
+}
+
+__global__ void convert_kernel(const void *__restrict__ in, int sdt, void *__restrict__ out, int ddt, size_t n) {
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+    st_any(out, ddt, i, ld_any(in, sdt, i));
+}
+
+// One wave per token row; 16-bit rows of D values copied in 8-byte units.
+// With `pos` set, adds the positional row (t = row % T) and rounds once, the
+// fused form of token_embed(ids) + pos_embed(arange(T)).
+template <int DT>
+__global__ void __launch_bounds__(256)
+embedding_kernel(const int32_t *__restrict__ ids, const typename Store<DT>::T *__restrict__ w,
+                 const typename Store<DT>::T *__restrict__ pos, typename Store<DT>::T *__restrict__ out, int n, int V,
+                 int D, int T, int *__restrict__ err) {
+  typedef Store<DT> S;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= n) return;
+  const int tok = ids[row];
+  const bool ok = tok >= 0 && tok < V;
+  if (!ok && lane == 0) atomicOr(err, 1);
+  const typename Store<DT>::T *src = w + long(ok ? tok : 0) * D;
+  const typename Store<DT>::T *prow = pos ? pos + long(row % T) * D : nullptr;
+  typename Store<DT>::T *dst = out + long(row) * D;
+  for (int d = lane; d < D; d += 64) {
+    float v = ok ? S::dec(src[d]) : 0.0f;
+    if (prow) v = S::dec(prow[d]) + (ok ? v : 0.0f);
+    dst[d] = S::enc(v);
+  }
+}
+
+// One wave per row: first index of the maximum (NaN never wins).
+template <int DT>
+__global__ void __launch_bounds__(256)
+argmax_kernel(const typename Store<DT>::T *__restrict__ x, int32_t *__restrict__ out, int rows, int cols) {
+  typedef Store<DT> S;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const typename Store<DT>::T *p = x + long(row) * cols;
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int c = lane; c < cols; c += 64) {
+    const float v = S::dec(p[c]);
+    if (v > best || (bi == 0x7fffffff && v == best)) { best = v; bi = c; }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ob = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
+  }
+  if (lane == 0) out[row] = bi == 0x7fffffff ? 0 : bi;
+}
+
+}  // namespace
+
+hipError_t binary(int dt, int op, const void *a, const void *b, void *out, const BcastArgs &g, hipStream_t st) {
+  if (g.total == 0) return hipSuccess;
+  // classify: same contiguous shape, [rows, cols] + [cols], or general
+  bool contig = true, row_bcast = g.ndim >= 1;
+  long s = 1;
+  for (int d = g.ndim - 1; d >= 0; --d) {
+    if (g.sa[d] != s || g.sb[d] != s) contig = false;
+    if (g.sa[d] != s) row_bcast = false;
+    if (d == g.ndim - 1) { if (g.sb[d] != 1) row_bcast = false; }
+    else if (g.sb[d] != 0) row_bcast = false;
+    s *= g.shape[d];
+  }
+  const int blocks = grid_for(g.total, 256);
+  const int cols = g.ndim ? g.shape[g.ndim - 1] : 1;
+#define MH_BIN(DTV)                                                                                          \
+  {                                                                                                          \
+    typedef typename Store<DTV>::T T;                                                                        \
+    if (contig)                                                                                              \
+      hipLaunchKernelGGL(binary_contig_kernel<DTV>, dim3(blocks), dim3(256), 0, st, (const T *)a, (const T *)b, \
+                         (T *)out, g.total, op);                                                             \
+    else if (row_bcast)                                                                                      \
+      hipLaunchKernelGGL(binary_row_kernel<DTV>, dim3(blocks), dim3(256), 0, st, (const T *)a, (const T *)b,    \
+                         (T *)out, g.total, cols, op);                                                       \
+    else                                                                                                     \
+      hipLaunchKernelGGL(binary_bcast_kernel<DTV>, dim3(blocks), dim3(256), 0, st, (const T *)a, (const T *)b,  \
+                         (T *)out, g, op);                                                                   \
+  }
+  switch (dt) {
+  case F32: MH_BIN(F32); break;
+  case F16: MH_BIN(F16); break;
+  case BF16: MH_BIN(BF16); break;
+  default: return hipErrorInvalidValue;
+  }
+#undef MH_BIN
+  return hipGetLastError();
+}
+
+hipError_t unary(int dt, int op, const void *in, void *out, size_t n, float c, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  const int blocks = grid_for(n, 256);
+  switch (dt) {
+  case F32: hipLaunchKernelGGL(unary_kernel<F32>, dim3(blocks), dim3(256), 0, st, (const float *)in, (float *)out, n, op, c); break;
+  case F16: hipLaunchKernelGGL(unary_kernel<F16>, dim3(blocks), dim3(256), 0, st, (const uint16_t *)in, (uint16_t *)out, n, op, c); break;
+  case BF16: hipLaunchKernelGGL(unary_kernel<BF16>, dim3(blocks), dim3(256), 0, st, (const uint16_t *)in, (uint16_t *)out, n, op, c); break;
+  default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t masked_fill(int dt, const void *x, const int32_t *mask, void *out, size_t n, float value, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(masked_fill_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, x, mask, out, n, dt, value);
+  return hipGetLastError();
+}
+
+hipError_t convert(int sdt, const void *in, int ddt, void *out, size_t n, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(convert_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, in, sdt, out, ddt, n);
+  return hipGetLastError();
+}
+
+hipError_t embedding(int dt, const int32_t *ids, const void *w, const void *pos, void *out, int n, int V, int D,
+                     int T, int *err, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  dim3 grid((n + 3) / 4);
+  switch (dt) {
+  case F32: hipLaunchKernelGGL(embedding_kernel<F32>, grid, dim3(256), 0, st, ids, (const float *)w, (const float *)pos, (float *)out, n, V, D, T, err); break;
+  case F16: hipLaunchKernelGGL(embedding_kernel<F16>, grid, dim3(256), 0, st, ids, (const uint16_t *)w, (const uint16_t *)pos, (uint16_t *)out, n, V, D, T, err); break;
+  case BF16: hipLaunchKernelGGL(embedding_kernel<BF16>, grid, dim3(256), 0, st, ids, (const uint16_t *)w, (const uint16_t *)pos, (uint16_t *)out, n, V, D, T, err); break;
+  default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t argmax_rows(int dt, const void *x, int32_t *out, int rows, int cols, hipStream_t st) {
+  if (rows <= 0) return hipSuccess;
+  dim3 grid((rows + 3) / 4);
+  switch (dt) {
+  case F32: hipLaunchKernelGGL(argmax_kernel<F32>, grid, dim3(256), 0, st, (const float *)x, out, rows, cols); break;
+  case F16: hipLaunchKernelGGL(argmax_kernel<F16>, grid, dim3(256), 0, st, (const uint16_t *)x, out, rows, cols); break;
+  case BF16: hipLaunchKernelGGL(argmax_kernel<BF16>, grid, dim3(256), 0, st, (const uint16_t *)x, out, rows, cols); break;
+  default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace mh

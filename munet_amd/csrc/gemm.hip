@@ -1,0 +1,414 @@
+// MFMA GEMM for gfx950: C[M,N] = A[M,K] * Bt[N,K]^T with a fused epilogue.
+//
+// This is the compute behind BackendBlasCapability::matmul / batched_matmul
+// (reference src/core/backend.hpp:250-260, CPU semantics in
+// src/backend/cpu_backend.hpp:334-414) and behind nn::Linear
+// (src/nn/linear.hpp:28-34: y = x.matmul(W) + b, W stored [in, out]).
+//
+// Design (CDNA4-first, not derived from any CUDA kernel):
+//   * 256 threads = 4 wave64s in a WGM x WGN grid; block tile BM x BN; every
+//     K step stages a 128-byte-deep slab of A and Bt through LDS (64 bf16/fp16
+//     or 32 fp32 values per row), double buffered, one barrier per step.
+//   * Both operands are K-contiguous in LDS, split in 16-byte chunks with an
+//     XOR swizzle (chunk c of row r lives at c ^ (r & 7)) so the 16-byte
+//     fragment reads of 8 consecutive rows hit distinct banks.
+//   * 16-bit types use v_mfma_f32_16x16x32_{bf16,f16}; fp32 uses four
+//     v_mfma_f32_16x16x4_f32 per 16-byte chunk (full fp32 precision).
+//   * Operands are fed "swapped" (Bt fragment as the MFMA A operand) so each
+//     lane ends up holding 4 consecutive output columns of one row, which
+//     makes the epilogue a single 8/16-byte store per fragment.
+//   * Epilogue reproduces the reference's per-op rounding chain in registers:
+//     round(matmul) -> round(+bias) -> activation -> round(+residual), with
+//     GELU as the reference's three rounded ops x*sigmoid(round(x*c))
+//     (src/nn/activations.hpp:31-38).  Optional head-split output writes
+//     q/k/v straight into the [B,H,T,hd] layout that MultiHeadAttention
+//     produces with permute+contiguous (src/nn/attention.hpp:51-62).
+//   * Grid order: workgroups are dealt round-robin to the 8 XCDs; the tile
+//     index is remapped so each XCD walks a contiguous band of tiles, then
+//     grouped along M so consecutive tiles share Bt panels in that XCD's L2.
+#include "mh_common.hpp"
+#include "mh_kernels.hpp"
+
+namespace mh {
+
+namespace {
+
+constexpr int kThreads = 256;
+
+template <int DT> struct Mfma;
+template <> struct Mfma<BF16> {
+  static constexpr int kElems = 8;  // elements per 16-byte chunk
+  static __device__ __forceinline__ void step(f32x4 &acc, uint4 a, uint4 b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                  __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
+  }
+};
+template <> struct Mfma<F16> {
+  static constexpr int kElems = 8;
+  static __device__ __forceinline__ void step(f32x4 &acc, uint4 a, uint4 b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                 __builtin_bit_cast(f16x8, b), acc, 0, 0, 0);
+  }
+};
+template <> struct Mfma<F32> {
+  static constexpr int kElems = 4;
+  static __device__ __forceinline__ void step(f32x4 &acc, uint4 a, uint4 b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.x), __uint_as_float(b.x), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.y), __uint_as_float(b.y), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.z), __uint_as_float(b.z), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.w), __uint_as_float(b.w), acc, 0, 0, 0);
+  }
+};
+
+// Load one 16-byte chunk (kElems values starting at column k of row `row`),
+// zero-filling whatever lies outside [0,rows) x [0,K).
+template <int DT, bool VEC>
+__device__ __forceinline__ uint4 load_chunk(const typename Store<DT>::T *__restrict__ p, long ld, int row,
+                                            int rows, int k, int K) {
+  constexpr int E = Mfma<DT>::kElems;
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (row >= rows) return v;
+  const typename Store<DT>::T *src = p + long(row) * ld + k;
+  if (VEC && k + E <= K) return *reinterpret_cast<const uint4 *>(src);
+  typename Store<DT>::T tmp[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) tmp[e] = (k + e < K) ? src[e] : typename Store<DT>::T(0);
+  __builtin_memcpy(&v, tmp, 16);
+  return v;
+}
+
+template <int DT>
+__device__ __forceinline__ void epi_store4(const EpiArgs &ep, int m, int n, int N, float v[4]) {
+  typedef Store<DT> S;
+  typedef typename S::T T;
+  // reference rounding chain, one op at a time
+  if (ep.bias && ep.bias_first) {
+    // conv: the reference initialises the float accumulator with the bias and
+    // rounds once (src/core/ops/conv2d.cpp:51-72 fallback converts to fp32)
+    const T *b = static_cast<const T *>(ep.bias);
+    const int nb = ep.mode == EPI_CONVT ? ep.convt_oc : 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = S::round(v[i] + (n + i < N ? S::dec(b[(n + i) % nb]) : 0.0f));
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = S::round(v[i]);
+    if (ep.bias) {
+      const T *b = static_cast<const T *>(ep.bias);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = S::round(v[i] + (n + i < N ? S::dec(b[n + i]) : 0.0f));
+    }
+  }
+  if (ep.act == ACT_RELU) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = v[i] > 0.0f ? v[i] : 0.0f;
+  } else if (ep.act == ACT_GELU) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float t1 = S::round(v[i] * ep.gelu_c);
+      const float t2 = S::round(sigmoidf_ref(t1));
+      v[i] = S::round(v[i] * t2);
+    }
+  }
+  T *out;
+  long idx;
+  if (ep.mode == EPI_HEADSPLIT) {
+    const int which = n / ep.E, e = n - which * ep.E;
+    const int h = e / ep.hd, dd = e - h * ep.hd;
+    const int b = m / ep.T, t = m - b * ep.T;
+    out = static_cast<T *>(ep.outs[which]);
+    idx = ((long(b) * ep.H + h) * ep.T + t) * ep.hd + dd;
+  } else if (ep.mode == EPI_CONVT) {
+    // column n = (kh*k + kw)*oC + oc of input pixel m = (b, ih, iw) lands on
+    // output pixel (b, ih*k + kh, iw*k + kw) of an NHWC tensor (row stride ldc)
+    const int oc = n % ep.convt_oc, ph = n / ep.convt_oc;
+    const int kh = ph / ep.convt_k, kw = ph - kh * ep.convt_k;
+    const int iw = m % ep.convt_iw, rest = m / ep.convt_iw;
+    const int ih = rest % ep.convt_ih, b = rest / ep.convt_ih;
+    const long opix = (long(b) * ep.convt_ih * ep.convt_k + ih * ep.convt_k + kh) * (long(ep.convt_iw) * ep.convt_k) +
+                      iw * ep.convt_k + kw;
+    out = static_cast<T *>(ep.out);
+    idx = opix * ep.ldc + oc;
+  } else {
+    out = static_cast<T *>(ep.out);
+    idx = long(m) * ep.ldc + n;
+  }
+  if (ep.resid) {
+    const T *r = static_cast<const T *>(ep.resid) + long(m) * ep.ldr + n;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = S::round((n + i < N ? S::dec(r[i]) : 0.0f) + v[i]);
+  }
+  const bool full = (n + 4 <= N) && (((uintptr_t)(out + idx) & (sizeof(T) * 4 - 1)) == 0);
+  if (full) {
+    if (DT == F32) {
+      *reinterpret_cast<float4 *>(out + idx) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      u16x4 w;
+      w.x = S::enc(v[0]); w.y = S::enc(v[1]); w.z = S::enc(v[2]); w.w = S::enc(v[3]);
+      *reinterpret_cast<u16x4 *>(out + idx) = w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (n + i < N) out[idx + i] = S::enc(v[i]);
+  }
+}
+
+// im2col chunk from an NHWC activation: GEMM row m = output pixel
+// (b, oh, ow), column k = (kh*kW + kw)*iC + ic.  Rows are pre-decoded into
+// (pixel base, ih0, iw0) once per thread.
+template <int DT, bool VEC>
+__device__ __forceinline__ uint4 load_im2col(const typename Store<DT>::T *__restrict__ x, const ConvArgs &cv, bool rowok,
+                                             long pixbase, int ih0, int iw0, int k, int K) {
+  typedef typename Store<DT>::T T;
+  constexpr int E = Mfma<DT>::kElems;
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (!rowok) return v;
+  const int kk = k / cv.iC, ic0 = k - kk * cv.iC;
+  if (VEC && k + E <= K) {
+    const int kh = kk / cv.kW, kw = kk - kh * cv.kW;
+    const int ih = ih0 + kh, iw = iw0 + kw;
+    if (ih >= 0 && ih < cv.iH && iw >= 0 && iw < cv.iW)
+      v = *reinterpret_cast<const uint4 *>(x + (pixbase + long(ih) * cv.iW + iw) * cv.ldx + ic0);
+    return v;
+  }
+  T tmp[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    tmp[e] = T(0);
+    const int ke = k + e;
+    if (ke < K) {
+      const int q = ke / cv.iC, ic = ke - q * cv.iC;
+      const int kh = q / cv.kW, kw = q - kh * cv.kW;
+      const int ih = ih0 + kh, iw = iw0 + kw;
+      if (ih >= 0 && ih < cv.iH && iw >= 0 && iw < cv.iW) tmp[e] = x[(pixbase + long(ih) * cv.iW + iw) * cv.ldx + ic];
+    }
+  }
+  __builtin_memcpy(&v, tmp, 16);
+  return v;
+}
+
+template <int DT, int BM, int BN, int WGM, int WGN, bool VEC, bool CONV>
+__global__ void __launch_bounds__(kThreads)
+gemm_nt_kernel(const typename Store<DT>::T *__restrict__ A, const typename Store<DT>::T *__restrict__ Bt,
+               int M, int N, int K, long lda, long ldb, long sa, long sb, long sc, EpiArgs ep, ConvArgs cv) {
+  typedef typename Store<DT>::T T;
+  constexpr int E = Mfma<DT>::kElems;
+  constexpr int BK = 8 * E;  // 8 chunks of 16 bytes per row
+  constexpr int WTM = BM / WGM, WTN = BN / WGN;
+  constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int ACH = BM * 8 / kThreads, BCH = BN * 8 / kThreads;
+  static_assert(WGM * WGN == 4, "4 waves");
+  static_assert(ACH >= 1 && BCH >= 1, "tile too small");
+
+  extern __shared__ uint4 smem[];
+  uint4 *As = smem;                 // [2][BM*8]
+  uint4 *Bs = smem + 2 * BM * 8;    // [2][BN*8]
+
+  // ---- tile scheduling (XCD band + group-M swizzle) ----
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int ntiles = tiles_m * tiles_n;
+  int pid = blockIdx.x;
+  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+  constexpr int GROUP = 8;
+  const int group_span = GROUP * tiles_n;
+  const int gid = pid / group_span;
+  const int first_m = gid * GROUP;
+  const int gsize = min(tiles_m - first_m, GROUP);
+  const int tm = first_m + (pid % group_span) % gsize;
+  const int tn = (pid % group_span) / gsize;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int z = blockIdx.z;
+  A += z * sa;
+  Bt += z * sb;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+
+  uint4 ra[ACH], rb[BCH];
+  long pixbase[CONV ? ACH : 1];
+  int ih0[CONV ? ACH : 1], iw0[CONV ? ACH : 1];
+  if (CONV) {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int m = m0 + ((tid + i * kThreads) >> 3);
+      const int ow = m % cv.oW, t2 = m / cv.oW, oh = t2 % cv.oH, b = t2 / cv.oH;
+      pixbase[i] = long(b) * cv.iH * cv.iW;
+      ih0[i] = oh * cv.s - cv.p;
+      iw0[i] = ow * cv.s - cv.p;
+    }
+  }
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int id = tid + i * kThreads, r = id >> 3, c = id & 7;
+      if (CONV)
+        ra[i] = load_im2col<DT, VEC>(A, cv, m0 + r < M, pixbase[i], ih0[i], iw0[i], k0 + c * E, K);
+      else
+        ra[i] = load_chunk<DT, VEC>(A, lda, m0 + r, M, k0 + c * E, K);
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      const int id = tid + i * kThreads, r = id >> 3, c = id & 7;
+      rb[i] = load_chunk<DT, VEC>(Bt, ldb, n0 + r, N, k0 + c * E, K);
+    }
+  };
+  auto sstore = [&](int buf) {
+    uint4 *as = As + buf * BM * 8, *bs = Bs + buf * BN * 8;
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int id = tid + i * kThreads, r = id >> 3, c = id & 7;
+      as[r * 8 + (c ^ (r & 7))] = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      const int id = tid + i * kThreads, r = id >> 3, c = id & 7;
+      bs[r * 8 + (c ^ (r & 7))] = rb[i];
+    }
+  };
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int KT = (K + BK - 1) / BK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+
+  const int lrow = lane & 15, lgrp = lane >> 4;
+  for (int kt = 0; kt < KT; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < KT) gload((kt + 1) * BK);
+    const uint4 *as = As + buf * BM * 8, *bs = Bs + buf * BN * 8;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int c = ks * 4 + lgrp;
+      uint4 af[FM], bf[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int r = wm * WTM + i * 16 + lrow;
+        af[i] = as[r * 8 + (c ^ (r & 7))];
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int r = wn * WTN + j * 16 + lrow;
+        bf[j] = bs[r * 8 + (c ^ (r & 7))];
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) Mfma<DT>::step(acc[i][j], bf[j], af[i]);
+    }
+    if (kt + 1 < KT) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds C[m][n..n+3] ----
+  EpiArgs e2 = ep;
+  if (ep.mode == EPI_ROWMAJOR) e2.out = static_cast<T *>(ep.out) + z * sc;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int m = m0 + wm * WTM + i * 16 + lrow;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = n0 + wn * WTN + j * 16 + lgrp * 4;
+      if (n >= N) continue;
+      float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+      epi_store4<DT>(e2, m, n, N, v);
+    }
+  }
+}
+
+template <int DT, int BM, int BN, int WGM, int WGN, bool VEC, bool CONV>
+void launch_one(dim3 grid, size_t lds, hipStream_t st, const void *A, const void *Bt, int M, int N, int K, long lda,
+                long ldb, long sa, long sb, long sc, const EpiArgs &ep, const ConvArgs &cv) {
+  typedef typename Store<DT>::T T;
+  auto kfn = gemm_nt_kernel<DT, BM, BN, WGM, WGN, VEC, CONV>;
+  if (lds > 65536) (void)hipFuncSetAttribute((const void *)kfn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+  hipLaunchKernelGGL(kfn, grid, dim3(kThreads), lds, st, (const T *)A, (const T *)Bt, M, N, K, lda, ldb, sa, sb, sc,
+                     ep, cv);
+}
+
+template <int DT, int BM, int BN, int WGM, int WGN>
+hipError_t launch_cfg(const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch,
+                      long sa, long sb, long sc, const EpiArgs &ep, const ConvArgs *cv, hipStream_t st) {
+  constexpr int E = Mfma<DT>::kElems;
+  const size_t lds = size_t(2) * (BM + BN) * 8 * 16;
+  const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  bool vec = (ldb % E == 0) && (sb % E == 0) && ((uintptr_t)A % 16 == 0) && ((uintptr_t)Bt % 16 == 0);
+  if (cv) vec = vec && (cv->iC % E == 0) && (cv->ldx % E == 0);
+  else vec = vec && (lda % E == 0) && (sa % E == 0);
+  dim3 grid(tiles, 1, batch);
+  const ConvArgs none{};
+  if (cv) {
+    if (vec) launch_one<DT, BM, BN, WGM, WGN, true, true>(grid, lds, st, A, Bt, M, N, K, lda, ldb, sa, sb, sc, ep, *cv);
+    else launch_one<DT, BM, BN, WGM, WGN, false, true>(grid, lds, st, A, Bt, M, N, K, lda, ldb, sa, sb, sc, ep, *cv);
+  } else {
+    if (vec) launch_one<DT, BM, BN, WGM, WGN, true, false>(grid, lds, st, A, Bt, M, N, K, lda, ldb, sa, sb, sc, ep, none);
+    else launch_one<DT, BM, BN, WGM, WGN, false, false>(grid, lds, st, A, Bt, M, N, K, lda, ldb, sa, sb, sc, ep, none);
+  }
+  return hipGetLastError();
+}
+
+// Choose the block tile that minimises (waves of tiles) x (tile cost) on 256
+// CUs, preferring larger tiles for operand reuse when the wave count ties.
+template <int DT>
+hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch, long sa,
+                     long sb, long sc, const EpiArgs &ep, const ConvArgs *cv, int tile_hint, hipStream_t st) {
+  struct Cand { int bm, bn; double cost; };
+  const int kCU = 256;
+  Cand cands[5] = {{256, 256, 4.0}, {256, 128, 2.0}, {128, 128, 1.0}, {128, 64, 0.55}, {64, 64, 0.3}};
+  int best = 2;
+  if (tile_hint >= 0 && tile_hint < 5) {
+    best = tile_hint;
+  } else {
+    double best_t = 1e30;
+    for (int c = 0; c < 5; ++c) {
+      const long tiles = long((M + cands[c].bm - 1) / cands[c].bm) * ((N + cands[c].bn - 1) / cands[c].bn) * batch;
+      const long waves = (tiles + kCU - 1) / kCU;
+      // per-tile cost grows with the tile area, discounted for better reuse
+      const double t = double(waves) * cands[c].cost;
+      if (t < best_t * 0.999) { best_t = t; best = c; }
+    }
+  }
+  switch (best) {
+  case 0: return launch_cfg<DT, 256, 256, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, cv, st);
+  case 1: return launch_cfg<DT, 256, 128, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, cv, st);
+  case 2: return launch_cfg<DT, 128, 128, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, cv, st);
+  case 3: return launch_cfg<DT, 128, 64, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, cv, st);
+  default: return launch_cfg<DT, 64, 64, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, cv, st);
+  }
+}
+
+}  // namespace
+
+hipError_t gemm_nt(int dt, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch,
+                   long sa, long sb, long sc, const EpiArgs &ep, int tile_hint, hipStream_t st) {
+  if (M <= 0 || N <= 0 || batch <= 0) return hipSuccess;
+  switch (dt) {
+  case F32: return launch_dt<F32>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, nullptr, tile_hint, st);
+  case F16: return launch_dt<F16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, nullptr, tile_hint, st);
+  case BF16: return launch_dt<BF16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, nullptr, tile_hint, st);
+  default: return hipErrorInvalidValue;
+  }
+}
+
+// Implicit-GEMM convolution on an NHWC activation with OHWI-packed weights:
+// M = B*oH*oW output pixels, N = oC, K = kH*kW*iC.  Output row m, column oc.
+hipError_t conv_nhwc(int dt, const void *x, const void *w_ohwi, const ConvArgs &cv, int oC, const EpiArgs &ep,
+                     int tile_hint, hipStream_t st) {
+  const int M = cv.B * cv.oH * cv.oW, K = cv.kH * cv.kW * cv.iC;
+  if (M <= 0 || oC <= 0) return hipSuccess;
+  switch (dt) {
+  case F32: return launch_dt<F32>(x, w_ohwi, M, oC, K, 0, K, 1, 0, 0, 0, ep, &cv, tile_hint, st);
+  case F16: return launch_dt<F16>(x, w_ohwi, M, oC, K, 0, K, 1, 0, 0, 0, ep, &cv, tile_hint, st);
+  case BF16: return launch_dt<BF16>(x, w_ohwi, M, oC, K, 0, K, 1, 0, 0, 0, ep, &cv, tile_hint, st);
+  default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace mh

@@ -1,0 +1,124 @@
+// Shared device-side definitions for the MI355X (gfx950) kernels of the
+// MuNet HIP backend: storage dtypes, the reference's rounding codecs, vector
+// types for MFMA operands and small launch helpers.
+//
+// Storage formats follow MuNet (src/types.hpp:16-30): float32, float16 and
+// bfloat16 are stored as 4/2/2-byte values, int32 for indices.  Rounding to a
+// 16-bit storage type uses the reference's own codecs so that every op
+// boundary rounds exactly like MuNet's CPU backend:
+//   * fp16: round half away from zero on the magnitude
+//     (src/types.hpp:239-278 adds half an ulp to the truncated mantissa);
+//   * bf16: round to nearest even on the raw bits, with no NaN special case
+//     (src/types.hpp:311-317).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mh {
+
+enum DType : int { F32 = 0, F16 = 1, BF16 = 2, I32 = 3 };
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+
+// ---- codecs ----------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(uint32_t(h) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t b = __float_as_uint(f);
+  b += 0x7fffu + ((b >> 16) & 1u);
+  return uint16_t(b >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  _Float16 v = __builtin_bit_cast(_Float16, h);
+  return float(v);
+}
+
+// fp16 encode with the reference's rounding: truncate the 23-bit mantissa to
+// 10 bits after adding 0x1000 (half of the dropped 13-bit field), carrying into
+// the exponent; subnormal results shift the implicit-one mantissa first and
+// round the same way; overflow saturates to infinity; NaN becomes 0x7e00.
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  const uint32_t bits = __float_as_uint(f);
+  const uint32_t sign = (bits >> 16) & 0x8000u;
+  const uint32_t raw_exp = (bits >> 23) & 0xffu;
+  uint32_t man = bits & 0x7fffffu;
+  int e = int(raw_exp) - 112;  // rebias 127 -> 15
+  if (raw_exp == 0xffu) return uint16_t(sign | (man ? 0x7e00u : 0x7c00u));
+  if (e <= 0) {
+    if (e < -10) return uint16_t(sign);
+    man |= 0x800000u;
+    const uint32_t sh = man >> uint32_t(1 - e);
+    return uint16_t(sign | ((sh + 0x1000u) >> 13));
+  }
+  // normal: the carry out of the mantissa bumps the exponent naturally
+  const uint32_t v = (uint32_t(e) << 10) + ((man + 0x1000u) >> 13);
+  if (v >= 0x7c00u) return uint16_t(sign | 0x7c00u);
+  return uint16_t(sign | v);
+}
+
+template <int DT> struct Store;
+template <> struct Store<F32> {
+  typedef float T;
+  static __device__ __forceinline__ float load(const float *p, size_t i) { return p[i]; }
+  static __device__ __forceinline__ float enc(float v) { return v; }
+  static __device__ __forceinline__ float round(float v) { return v; }
+  static __device__ __forceinline__ float dec(float v) { return v; }
+};
+template <> struct Store<F16> {
+  typedef uint16_t T;
+  static __device__ __forceinline__ float load(const uint16_t *p, size_t i) { return f16_to_f32(p[i]); }
+  static __device__ __forceinline__ uint16_t enc(float v) { return f32_to_f16(v); }
+  static __device__ __forceinline__ float round(float v) { return f16_to_f32(f32_to_f16(v)); }
+  static __device__ __forceinline__ float dec(uint16_t v) { return f16_to_f32(v); }
+};
+template <> struct Store<BF16> {
+  typedef uint16_t T;
+  static __device__ __forceinline__ float load(const uint16_t *p, size_t i) { return bf16_to_f32(p[i]); }
+  static __device__ __forceinline__ uint16_t enc(float v) { return f32_to_bf16(v); }
+  static __device__ __forceinline__ float round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+  static __device__ __forceinline__ float dec(uint16_t v) { return bf16_to_f32(v); }
+};
+
+// Generic (runtime dtype) scalar access for the cold paths.
+__device__ __forceinline__ float ld_any(const void *p, int dt, size_t i) {
+  if (dt == F32) return static_cast<const float *>(p)[i];
+  if (dt == F16) return f16_to_f32(static_cast<const uint16_t *>(p)[i]);
+  if (dt == BF16) return bf16_to_f32(static_cast<const uint16_t *>(p)[i]);
+  return float(static_cast<const int32_t *>(p)[i]);
+}
+
+__device__ __forceinline__ void st_any(void *p, int dt, size_t i, float v) {
+  if (dt == F32) static_cast<float *>(p)[i] = v;
+  else if (dt == F16) static_cast<uint16_t *>(p)[i] = f32_to_f16(v);
+  else if (dt == BF16) static_cast<uint16_t *>(p)[i] = f32_to_bf16(v);
+  else static_cast<int32_t *>(p)[i] = int32_t(v);
+}
+
+// Sigmoid in float: 1 / (1 + e^-x), as the reference's fp32 kernel writes it
+// (src/backend/cpu_backend.hpp:509-531).
+__device__ __forceinline__ float sigmoidf_ref(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// Wavefront (64-lane) reductions via cross-lane shuffles.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+inline size_t dtype_size(int dt) { return (dt == F16 || dt == BF16) ? 2 : 4; }
+
+}  // namespace mh

@@ -1,0 +1,104 @@
+// Internal launcher declarations shared by the kernel translation units and
+// the C-ABI layer.  Every launcher enqueues on the given stream and returns
+// the launch status; shapes have been validated by the caller.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace mh {
+
+enum Act : int { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2 };
+enum EpiMode : int { EPI_ROWMAJOR = 0, EPI_HEADSPLIT = 1, EPI_CONVT = 2 };
+enum BinOp : int { BIN_ADD = 0, BIN_SUB = 1, BIN_MUL = 2, BIN_DIV = 3 };
+enum UnOp : int {
+  UN_RELU = 0, UN_SIGMOID = 1, UN_GELU = 2, UN_EXP = 3, UN_LOG = 4,
+  UN_SQRT = 5, UN_RSQRT = 6, UN_SIN = 7, UN_COS = 8
+};
+
+constexpr int kMaxDims = 6;
+
+// Fused GEMM epilogue.
+//   row-major : out[m*ldc + n]
+//   head split: column n of a [M, nsplit*E] product goes to outs[n / E] in
+//               [B, H, T, hd] order with m = b*T + t and n % E = h*hd + d
+//   convT     : column n = (kh*k + kw)*oC + oc of input pixel m = (b, ih, iw)
+//               goes to NHWC pixel (b, ih*k+kh, iw*k+kw), channel oc
+// bias_first adds the bias to the fp32 accumulator before the single output
+// rounding (convolution semantics); otherwise the Linear chain
+// round(round(acc) + bias) is applied.
+struct EpiArgs {
+  void *out = nullptr;
+  long ldc = 0;
+  const void *bias = nullptr;   // [N] (or [oC] for convT) in the storage dtype
+  int bias_first = 0;
+  const void *resid = nullptr;  // [M, ldr] added after the activation
+  long ldr = 0;
+  int act = ACT_NONE;
+  float gelu_c = 1.702f;        // GELU constant already rounded to the dtype
+  int mode = EPI_ROWMAJOR;
+  void *outs[3] = {nullptr, nullptr, nullptr};
+  int T = 1, H = 1, hd = 1, E = 1;
+  int convt_oc = 1, convt_k = 1, convt_ih = 1, convt_iw = 1;
+};
+
+// Implicit-GEMM convolution geometry (NHWC activation, ldx = pixel stride).
+struct ConvArgs {
+  int B = 0, iC = 0, iH = 0, iW = 0, kH = 1, kW = 1, s = 1, p = 0, oH = 0, oW = 0;
+  long ldx = 0;
+};
+
+struct BcastArgs {
+  int ndim = 0;
+  int shape[kMaxDims] = {};
+  long sa[kMaxDims] = {};
+  long sb[kMaxDims] = {};
+  size_t total = 0;
+};
+
+struct StridedArgs {
+  int ndim = 0;
+  int shape[kMaxDims] = {};
+  long strides[kMaxDims] = {};
+  long offset = 0;
+  size_t total = 0;
+};
+
+// C = A[M,K] (row stride lda) * Bt[N,K]^T (row stride ldb), batch slices at
+// element strides sa/sb/sc (sb = 0 broadcasts one weight).  tile_hint < 0
+// picks the block tile automatically.
+hipError_t gemm_nt(int dt, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch,
+                   long sa, long sb, long sc, const EpiArgs &ep, int tile_hint, hipStream_t st);
+hipError_t conv_nhwc(int dt, const void *x, const void *w_ohwi, const ConvArgs &cv, int oC, const EpiArgs &ep,
+                     int tile_hint, hipStream_t st);
+
+hipError_t attention(int dt, const void *q, const void *k, const void *v, void *ctx, int B, int H, int T, int hd,
+                     int causal, float scale, int force_generic, hipStream_t st);
+
+hipError_t binary(int dt, int op, const void *a, const void *b, void *out, const BcastArgs &g, hipStream_t st);
+hipError_t unary(int dt, int op, const void *in, void *out, size_t n, float c, hipStream_t st);
+hipError_t masked_fill(int dt, const void *x, const int32_t *mask, void *out, size_t n, float value, hipStream_t st);
+hipError_t convert(int sdt, const void *in, int ddt, void *out, size_t n, hipStream_t st);
+hipError_t embedding(int dt, const int32_t *ids, const void *w, const void *pos, void *out, int n, int V, int D,
+                     int T, int *err, hipStream_t st);
+hipError_t argmax_rows(int dt, const void *x, int32_t *out, int rows, int cols, hipStream_t st);
+
+hipError_t layernorm(int dt, const void *x, const void *w, const void *b, void *y, int rows, int cols, float eps,
+                     hipStream_t st);
+hipError_t softmax_rows(int dt, const void *x, void *y, int rows, int cols, hipStream_t st);
+
+hipError_t to_contiguous(int dt, const void *src, void *dst, const StridedArgs &g, hipStream_t st);
+hipError_t transpose2d(int dt, const void *in, void *out, int batch, int rows, int cols, hipStream_t st);
+hipError_t concat_part(int dt, const void *src, void *dst, size_t outer, size_t len, size_t out_len, size_t off,
+                       hipStream_t st);
+hipError_t max_pool2d(int dt, int nhwc, const void *in, void *out, int B, int C, int iH, int iW, int k, int s, int p,
+                      hipStream_t st);
+hipError_t upsample2d(int dt, int nhwc, const void *in, void *out, int B, int C, int iH, int iW, int scale,
+                      hipStream_t st);
+hipError_t nchw_to_nhwc(int dt, const void *in, void *out, int B, int C, int HW, hipStream_t st);
+hipError_t nhwc_to_nchw(int dt, const void *in, void *out, int B, int C, int HW, hipStream_t st);
+
+inline size_t dt_size(int dt) { return (dt == 1 || dt == 2) ? 2 : 4; }
+
+}  // namespace mh

@@ -1,0 +1,140 @@
+// Row-wise normalisation kernels for gfx950: LayerNorm and softmax.
+//
+// LayerNorm follows ops::layer_norm (src/core/ops/normalization.cpp:125-224):
+// per row mean, biased variance, (x - mean) / sqrt(var + eps) * w + b, output
+// rounded to the storage dtype.  The reference evaluates it in double on the
+// host; here one wave owns a row, keeps the row in registers, and reduces in
+// fp32 with cross-lane shuffles (two passes over registers, one HBM read and
+// one HBM write per element).
+//
+// Softmax follows CPUBackend::softmax (src/backend/cpu_backend.hpp:587-611):
+// float row max, double sum of exp(x - max), y = exp(x - max) / sum; the
+// fp16/bf16 fallback (src/core/ops/activations.cpp:208-243) is the same
+// arithmetic on decoded values with one rounding at the output.
+#include "mh_common.hpp"
+#include "mh_kernels.hpp"
+
+namespace mh {
+
+namespace {
+
+// VPL values per lane held in registers (row length <= 64*VPL).
+template <int DT, int VPL>
+__global__ void __launch_bounds__(256)
+layernorm_kernel(const typename Store<DT>::T *__restrict__ x, const typename Store<DT>::T *__restrict__ w,
+                 const typename Store<DT>::T *__restrict__ b, typename Store<DT>::T *__restrict__ y, int rows, int cols,
+                 float eps) {
+  typedef Store<DT> S;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const typename Store<DT>::T *xr = x + long(row) * cols;
+  float v[VPL];
+  float sum = 0.f;
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int c = k * 64 + lane;
+    v[k] = c < cols ? S::dec(xr[c]) : 0.f;
+    sum += v[k];
+  }
+  const float mean = wave_sum(sum) / float(cols);
+  float var = 0.f;
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int c = k * 64 + lane;
+    const float d = c < cols ? v[k] - mean : 0.f;
+    var += d * d;
+  }
+  var = wave_sum(var) / float(cols);
+  const float inv = 1.0f / sqrtf(var + eps);
+  typename Store<DT>::T *yr = y + long(row) * cols;
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int c = k * 64 + lane;
+    if (c < cols) yr[c] = S::enc((v[k] - mean) * inv * S::dec(w[c]) + S::dec(b[c]));
+  }
+}
+
+// Long rows: three streaming passes (mean, variance, normalise).
+template <int DT>
+__global__ void __launch_bounds__(256)
+layernorm_long_kernel(const typename Store<DT>::T *__restrict__ x, const typename Store<DT>::T *__restrict__ w,
+                      const typename Store<DT>::T *__restrict__ b, typename Store<DT>::T *__restrict__ y, int rows,
+                      int cols, float eps) {
+  typedef Store<DT> S;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const typename Store<DT>::T *xr = x + long(row) * cols;
+  float sum = 0.f;
+  for (int c = lane; c < cols; c += 64) sum += S::dec(xr[c]);
+  const float mean = wave_sum(sum) / float(cols);
+  float var = 0.f;
+  for (int c = lane; c < cols; c += 64) {
+    const float d = S::dec(xr[c]) - mean;
+    var += d * d;
+  }
+  var = wave_sum(var) / float(cols);
+  const float inv = 1.0f / sqrtf(var + eps);
+  typename Store<DT>::T *yr = y + long(row) * cols;
+  for (int c = lane; c < cols; c += 64) yr[c] = S::enc((S::dec(xr[c]) - mean) * inv * S::dec(w[c]) + S::dec(b[c]));
+}
+
+template <int DT>
+__global__ void __launch_bounds__(256)
+softmax_kernel(const typename Store<DT>::T *__restrict__ x, typename Store<DT>::T *__restrict__ y, int rows, int cols) {
+  typedef Store<DT> S;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const typename Store<DT>::T *xr = x + long(row) * cols;
+  float mx = -INFINITY;
+  for (int c = lane; c < cols; c += 64) mx = fmaxf(mx, S::dec(xr[c]));
+  mx = wave_max(mx);
+  double sum = 0.0;
+  for (int c = lane; c < cols; c += 64) sum += exp(double(S::dec(xr[c])) - double(mx));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  typename Store<DT>::T *yr = y + long(row) * cols;
+  for (int c = lane; c < cols; c += 64) yr[c] = S::enc(float(exp(double(S::dec(xr[c])) - double(mx)) / sum));
+}
+
+template <int DT>
+hipError_t ln_dt(const void *x, const void *w, const void *b, void *y, int rows, int cols, float eps, hipStream_t st) {
+  typedef typename Store<DT>::T T;
+  dim3 grid((rows + 3) / 4), block(256);
+  const T *X = (const T *)x, *W = (const T *)w, *B = (const T *)b;
+  T *Y = (T *)y;
+  if (cols <= 64 * 4) hipLaunchKernelGGL((layernorm_kernel<DT, 4>), grid, block, 0, st, X, W, B, Y, rows, cols, eps);
+  else if (cols <= 64 * 8) hipLaunchKernelGGL((layernorm_kernel<DT, 8>), grid, block, 0, st, X, W, B, Y, rows, cols, eps);
+  else if (cols <= 64 * 16) hipLaunchKernelGGL((layernorm_kernel<DT, 16>), grid, block, 0, st, X, W, B, Y, rows, cols, eps);
+  else hipLaunchKernelGGL((layernorm_long_kernel<DT>), grid, block, 0, st, X, W, B, Y, rows, cols, eps);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t layernorm(int dt, const void *x, const void *w, const void *b, void *y, int rows, int cols, float eps,
+                     hipStream_t st) {
+  if (rows <= 0 || cols <= 0) return hipSuccess;
+  switch (dt) {
+  case F32: return ln_dt<F32>(x, w, b, y, rows, cols, eps, st);
+  case F16: return ln_dt<F16>(x, w, b, y, rows, cols, eps, st);
+  case BF16: return ln_dt<BF16>(x, w, b, y, rows, cols, eps, st);
+  default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t softmax_rows(int dt, const void *x, void *y, int rows, int cols, hipStream_t st) {
+  if (rows <= 0 || cols <= 0) return hipSuccess;
+  dim3 grid((rows + 3) / 4), block(256);
+  switch (dt) {
+  case F32: hipLaunchKernelGGL(softmax_kernel<F32>, grid, block, 0, st, (const float *)x, (float *)y, rows, cols); break;
+  case F16: hipLaunchKernelGGL(softmax_kernel<F16>, grid, block, 0, st, (const uint16_t *)x, (uint16_t *)y, rows, cols); break;
+  case BF16: hipLaunchKernelGGL(softmax_kernel<BF16>, grid, block, 0, st, (const uint16_t *)x, (uint16_t *)y, rows, cols); break;
+  default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace mh

@@ -1,0 +1,318 @@
+"""Op-level parity: every HIP entry point against the CPU restatement of
+MuNet's CPU backend (oracle/munet_cpu_ref.cpp) on the same seeded inputs.
+
+Tolerances: normwise rel 1e-4 for fp32, 2e-2 for
+fp16/bf16; data movement, indexing and argmax bit-exact.
+"""
+import numpy as np
+import pytest
+
+from munet_amd import synth
+from munet_amd.backend import BroadcastInfo, compute_broadcast, contiguous_strides, empty, to_device, to_host
+from oracle import ADD, DIV, MUL, SUB
+from util import assert_close, dec, rand
+
+pytestmark = pytest.mark.gpu
+
+F32, F16, BF16, I32 = synth.F32, synth.F16, synth.BF16, synth.I32
+DTS = [F32, F16, BF16]
+
+
+def _mm_operand(shape_mk, trans, dt, seed):
+    m, k = shape_mk
+    x = rand((m, k), dt, seed)
+    return np.ascontiguousarray(x.T) if trans else x
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("M,K,N", [(64, 784, 256), (37, 53, 29), (128, 256, 10), (1, 8, 1), (300, 200, 130)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_matmul(hip, orc, dt, M, K, N, ta, tb):
+    a = rand((M, K), dt, 1)
+    b = rand((K, N), dt, 2)
+    a_st = np.ascontiguousarray(synth.decode(a, dt).T) if ta else synth.decode(a, dt)
+    b_st = np.ascontiguousarray(synth.decode(b, dt).T) if tb else synth.decode(b, dt)
+    a_st, b_st = synth.encode(a_st, dt), synth.encode(b_st, dt)
+    out = empty((M, N), dt)
+    hip.matmul(to_device(a_st, dt), to_device(b_st, dt), out, M, K, N, bool(ta), bool(tb))
+    ref = orc.matmul(a, b, dt)
+    assert_close(to_host(out, dt), ref, dt, what=f"matmul {M}x{K}x{N} t{ta}{tb}")
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("bcast_b", [True, False])
+def test_batched_matmul(hip, orc, dt, bcast_b):
+    batch, M, K, N = 3, 33, 40, 24
+    a = rand((batch, M, K), dt, 3)
+    b = rand((batch, K, N) if not bcast_b else (K, N), dt, 4)
+    out = empty((batch, M, N), dt)
+    hip.batched_matmul(to_device(a, dt), to_device(b, dt), out, batch, M, K, N, False, False, M * K,
+                       0 if bcast_b else K * N, M * N)
+    ref = orc.matmul(a, b, dt)
+    assert_close(to_host(out, dt), ref, dt, what="batched_matmul")
+
+
+def test_matmul_closed_form(hip):
+    """all-ones known answer (reference tests/unified_tests.cpp:50-64): every entry == K."""
+    for dt in DTS:
+        M, K, N = 17, 96, 33
+        a, b = synth.encode(np.ones((M, K)), dt), synth.encode(np.ones((K, N)), dt)
+        out = empty((M, N), dt)
+        hip.matmul(to_device(a, dt), to_device(b, dt), out, M, K, N)
+        assert np.all(dec(to_host(out, dt), dt) == K)
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("act", [0, 1, 2])
+@pytest.mark.parametrize("resid", [False, True])
+def test_linear_fused(hip, orc, dt, act, resid):
+    M, K, N = 96, 160, 72
+    x, w, bias = rand((M, K), dt, 5), rand((K, N), dt, 6, 0.2), rand((N,), dt, 7)
+    r = rand((M, N), dt, 8)
+    ref = orc.linear(x, w, bias, dt)
+    if act == 1:
+        ref = orc.relu(ref, dt)
+    elif act == 2:
+        ref = orc.gelu(ref, dt)
+    if resid:
+        ref = orc.add(r, ref, dt)
+    wd = to_device(w, dt)
+    wt = empty((N, K), dt)
+    hip.pack_linear_weight(wd, wt, K, N)
+    out = empty((M, N), dt)
+    hip.linear(to_device(x, dt), wt, to_device(bias, dt), out, M, K, N, act, to_device(r, dt) if resid else None)
+    assert_close(to_host(out, dt), ref, dt, what=f"linear act={act} resid={resid}")
+
+
+def _mha_params(E, dt, seed):
+    p = {}
+    for i, n in enumerate(("q_proj", "k_proj", "v_proj", "out_proj")):
+        p[n + ".weight"] = rand((E, E), dt, seed + i, 1.0 / np.sqrt(E))
+        p[n + ".bias"] = rand((E,), dt, seed + 10 + i, 0.1)
+    return p
+
+
+@pytest.mark.parametrize("dt", [F16, BF16, F32])
+@pytest.mark.parametrize("B,T,H,hd", [(2, 64, 2, 64), (1, 200, 3, 64), (2, 40, 2, 32), (1, 3, 2, 4)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_core(hip, orc, dt, B, T, H, hd, causal):
+    """q/k/v projection (fused head split) + fused attention vs the reference
+    MHA core, including MuNet's K-reinterpretation."""
+    E = H * hd
+    x = rand((B * T, E), dt, 20)
+    p = _mha_params(E, dt, 30)
+    q2 = orc.linear(x, p["q_proj.weight"], p["q_proj.bias"], dt)
+    k2 = orc.linear(x, p["k_proj.weight"], p["k_proj.bias"], dt)
+    v2 = orc.linear(x, p["v_proj.weight"], p["v_proj.bias"], dt)
+    ref = orc.mha_core(q2, k2, v2, B, T, H, causal, dt)
+    # device: packed [3E, E] weight, head-split projection, attention
+    w_cat = np.concatenate([p["q_proj.weight"], p["k_proj.weight"], p["v_proj.weight"]], axis=1)  # [E, 3E]
+    b_cat = np.concatenate([p["q_proj.bias"], p["k_proj.bias"], p["v_proj.bias"]])
+    wd = to_device(w_cat, dt)
+    wt = empty((3 * E, E), dt)
+    hip.pack_linear_weight(wd, wt, E, 3 * E)
+    q, k, v = (empty((B * H * T * hd,), dt) for _ in range(3))
+    hip.qkv_projection(to_device(x, dt), wt, to_device(b_cat, dt), q, k, v, B, T, E, H)
+    ctx = empty((B * T, E), dt)
+    hip.attention(q, k, v, ctx, B, H, T, hd, causal)
+    assert_close(to_host(ctx, dt), ref, dt, what="attention")
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("rows,cols", [(64, 768), (33, 512), (5, 100), (3, 2000)])
+def test_layer_norm(hip, orc, dt, rows, cols):
+    x, w, b = rand((rows, cols), dt, 40, 3.0), rand((cols,), dt, 41), rand((cols,), dt, 42)
+    out = empty((rows, cols), dt)
+    hip.layer_norm(to_device(x, dt), to_device(w, dt), to_device(b, dt), out, rows, cols, 1e-5)
+    assert_close(to_host(out, dt), orc.layer_norm(x, w, b, dt), dt, what="layer_norm")
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("rows,cols", [(64, 10), (17, 1000), (4, 3)])
+def test_softmax(hip, orc, dt, rows, cols):
+    x = rand((rows, cols), dt, 50, 4.0)
+    out = empty((rows, cols), dt)
+    hip.softmax(to_device(x, dt), out, rows, cols)
+    assert_close(to_host(out, dt), orc.softmax(x, dt), dt, what="softmax")
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("op", [ADD, SUB, MUL, DIV])
+@pytest.mark.parametrize("sa,sb", [((4, 5, 6), (4, 5, 6)), ((7, 9), (9,)), ((3, 1, 5), (1, 4, 1)), ((6,), (2, 3, 6))])
+def test_binary_broadcast(hip, orc, dt, op, sa, sb):
+    a = rand(sa, dt, 60)
+    b = rand(sb, dt, 61)
+    if op == DIV:
+        b = synth.encode(np.abs(dec(b, dt)) + 0.5, dt)
+    out_shape, stra, strb = compute_broadcast(sa, contiguous_strides(sa), sb, contiguous_strides(sb))
+    out = empty(out_shape, dt)
+    fn = {ADD: hip.add, SUB: hip.sub, MUL: hip.mul, DIV: hip.div}[op]
+    fn(to_device(a, dt), to_device(b, dt), out, BroadcastInfo(out_shape, stra, strb))
+    assert_close(to_host(out, dt), orc.binary(op, a, b, dt), dt, what=f"binary op={op}")
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_unary(hip, orc, dt):
+    x = rand((1000,), dt, 70, 3.0)
+    for name in ("relu", "sigmoid", "gelu"):
+        out = empty((1000,), dt)
+        getattr(hip, name)(to_device(x, dt), out, 1000)
+        ref = getattr(orc, name)(x, dt)
+        if name == "relu":
+            assert np.array_equal(to_host(out, dt), ref)
+        else:
+            assert_close(to_host(out, dt), ref, dt, what=name)
+
+
+def test_gelu_known_values(hip):
+    """x*sigmoid(1.702x) at -2, 0, 2 (reference tests/test_nn.cpp:385-402)."""
+    x = synth.encode(np.array([-2.0, 0.0, 2.0]), F32)
+    out = empty((3,), F32)
+    hip.gelu(to_device(x, F32), out, 3)
+    np.testing.assert_allclose(to_host(out, F32), [-0.0643, 0.0, 1.9357], atol=5e-3)
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_masked_fill(hip, orc, dt):
+    n = 513
+    x = rand((n,), dt, 80)
+    mask = (np.arange(n) % 3 == 0).astype(np.int32)
+    out = empty((n,), dt)
+    hip.masked_fill(to_device(x, dt), to_device(mask, I32), out, n, -1e9)
+    ref = np.where(mask != 0, synth.encode(np.full(n, -1e9), dt), x)
+    assert np.array_equal(to_host(out, dt), ref)
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_embedding(hip, orc, dt):
+    V, D, B, T = 50, 24, 3, 7
+    w = rand((V, D), dt, 90)
+    ids = np.random.default_rng(1).integers(0, V, (B, T)).astype(np.int32)
+    out = empty((B * T, D), dt)
+    hip.embedding(to_device(ids, I32), to_device(w, dt), out, B * T, V, D)
+    assert np.array_equal(to_host(out, dt).reshape(B, T, D), orc.embedding(ids, w, dt))
+    # fused token + position embedding == gather + gather + add
+    pos = rand((T, D), dt, 91)
+    out2 = empty((B * T, D), dt)
+    hip.embedding_pos(to_device(ids, I32), to_device(w, dt), to_device(pos, dt), out2, B * T, V, D, T)
+    ref = orc.add(orc.embedding(ids, w, dt), orc.embedding(np.tile(np.arange(T, dtype=np.int32), (B, 1)), pos, dt), dt)
+    assert np.array_equal(to_host(out2, dt).reshape(B, T, D), ref)
+
+
+def test_embedding_out_of_range(hip):
+    from munet_amd._lib import HipError
+    w = rand((10, 8), F32, 92)
+    ids = np.array([1, 10, 3], dtype=np.int32)
+    out = empty((3, 8), F32)
+    hip.embedding(to_device(ids, I32), to_device(w, F32), out, 3, 10, 8)
+    with pytest.raises(HipError, match="Embedding index out of range"):
+        hip.check_device_errors()
+    hip.check_device_errors()  # flag cleared
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_argmax(hip, dt):
+    rows, cols = 40, 3000
+    x = rand((rows, cols), dt, 93)
+    x[5, 17] = x[5, 2000] = synth.encode(np.array([50.0]), dt)[0]  # tie -> first index
+    out = empty((rows,), I32)
+    hip.argmax(to_device(x, dt), out, rows, cols)
+    assert np.array_equal(to_host(out, I32), np.argmax(dec(x, dt), axis=1))
+
+
+@pytest.mark.parametrize("dt", DTS)
+@pytest.mark.parametrize("B,iC,H,W,oC,k,s,p", [(2, 3, 9, 9, 4, 3, 1, 1), (2, 3, 9, 9, 4, 3, 2, 1),
+                                               (1, 16, 12, 10, 32, 3, 1, 1), (2, 8, 8, 8, 16, 1, 1, 0),
+                                               (1, 32, 16, 16, 16, 3, 2, 1)])
+def test_conv2d(hip, orc, dt, B, iC, H, W, oC, k, s, p):
+    x = rand((B, iC, H, W), dt, 100)
+    w = rand((oC, iC, k, k), dt, 101, np.sqrt(2.0 / (iC * k * k)))
+    b = rand((oC,), dt, 102, 0.1)
+    ref = orc.conv2d(x, w, b, s, p, dt)
+    out = empty(ref.shape, dt)
+    hip.conv2d(to_device(x, dt), to_device(w, dt), to_device(b, dt), out, B, iC, H, W, oC, k, k, s, p)
+    assert_close(to_host(out, dt), ref, dt, what="conv2d")
+
+
+def test_conv2d_closed_form(hip):
+    """all-ones 3x3 conv, pad 0: every output == iC*9 (unified_tests.cpp:66-82)."""
+    B, iC, H, W, oC = 1, 4, 6, 6, 8
+    x = synth.encode(np.ones((B, iC, H, W)), F32)
+    w = synth.encode(np.ones((oC, iC, 3, 3)), F32)
+    out = empty((B, oC, 4, 4), F32)
+    hip.conv2d(to_device(x, F32), to_device(w, F32), None, out, B, iC, H, W, oC, 3, 3, 1, 0)
+    assert np.all(to_host(out, F32) == iC * 9)
+
+
+@pytest.mark.parametrize("dt", [F16, BF16, F32])
+def test_conv_transpose2d(hip, orc, dt):
+    from oracle.models import conv_transpose2d
+    B, iC, H, W, oC = 2, 16, 5, 6, 8
+    x = rand((B, iC, H, W), dt, 110)
+    w = rand((iC, oC, 2, 2), dt, 111, 0.3)
+    b = rand((oC,), dt, 112, 0.1)
+    ref = conv_transpose2d(orc, x, w, b, 2, dt)
+    xd = to_device(x, dt)
+    xn = empty((B, H, W, iC), dt)
+    hip.nchw_to_nhwc(xd, xn, B, iC, H * W)
+    wp = empty((4 * oC, iC), dt)
+    hip.pack_convt_weight(to_device(w, dt), wp, iC, oC, 2)
+    on = empty((B, 2 * H, 2 * W, oC), dt)
+    hip.conv_transpose2d_nhwc(xn, wp, to_device(b, dt), on, B, iC, H, W, oC, 2)
+    out = empty((B, oC, 2 * H, 2 * W), dt)
+    hip.nhwc_to_nchw(on, out, B, oC, 4 * H * W)
+    assert_close(to_host(out, dt), ref, dt, what="conv_transpose2d")
+
+
+@pytest.mark.parametrize("dt", DTS)
+def test_pool_upsample_concat(hip, orc, dt):
+    B, C, H, W = 2, 3, 8, 6
+    x = rand((B, C, H, W), dt, 120)
+    xd = to_device(x, dt)
+    out = empty((B, C, 4, 3), dt)
+    hip.max_pool2d(xd, out, B, C, H, W, 2, 2, 0)
+    assert np.array_equal(to_host(out, dt), orc.max_pool2d(x, 2, 2, 0, dt))
+    out = empty((B, C, 3, 2), dt)
+    hip.max_pool2d(xd, out, B, C, H, W, 3, 3, 1)
+    assert np.array_equal(to_host(out, dt), orc.max_pool2d(x, 3, 3, 1, dt))
+    up = empty((B, C, 2 * H, 2 * W), dt)
+    hip.upsample2d(xd, up, B, C, H, W, 2)
+    assert np.array_equal(to_host(up, dt), orc.upsample2d(x, 2, dt))
+    y = rand((B, 5, H, W), dt, 121)
+    cat = empty((B, C + 5, H, W), dt)
+    hip.concat([xd, to_device(y, dt)], cat, 1, [x.shape, y.shape])
+    assert np.array_equal(to_host(cat, dt), np.concatenate([x, y], axis=1))
+    # NHWC variants agree with NCHW after a layout change
+    xn = empty((B, H, W, C), dt)
+    hip.nchw_to_nhwc(xd, xn, B, C, H * W)
+    pn = empty((B, 4, 3, C), dt)
+    hip.max_pool2d_nhwc(xn, pn, B, C, H, W, 2, 2, 0)
+    assert np.array_equal(to_host(pn, dt).transpose(0, 3, 1, 2), orc.max_pool2d(x, 2, 2, 0, dt))
+    un = empty((B, 2 * H, 2 * W, C), dt)
+    hip.upsample2d_nhwc(xn, un, B, C, H, W, 2)
+    assert np.array_equal(to_host(un, dt).transpose(0, 3, 1, 2), orc.upsample2d(x, 2, dt))
+
+
+@pytest.mark.parametrize("dt", DTS + [I32])
+def test_to_contiguous(hip, dt):
+    x = rand((4, 5, 6), dt, 130) if dt != I32 else np.arange(120, dtype=np.int32).reshape(4, 5, 6)
+    xd = to_device(x, dt)
+    out = empty((6, 4, 5), dt)
+    # permute(2,0,1) view of the contiguous [4,5,6] storage, offset 0
+    hip.to_contiguous(xd, out, [6, 4, 5], [1, 30, 6], 0)
+    assert np.array_equal(to_host(out, dt), np.ascontiguousarray(x.transpose(2, 0, 1)))
+    out2 = empty((3, 5), dt)
+    hip.to_contiguous(xd, out2, [3, 5], [30, 6], 7)  # narrow with an offset
+    flat = x.reshape(-1)
+    ref = np.array([[flat[7 + 30 * i + 6 * j] for j in range(5)] for i in range(3)])
+    assert np.array_equal(to_host(out2, dt), ref)
+
+
+def test_convert_codecs(hip, orc):
+    vals = np.random.default_rng(5).standard_normal(4096).astype(np.float32) * 1000
+    vals[:6] = [65519.0, 65520.0, 1e-8, -1e9, 0.5 + 2 ** -12, 3.0e-5]
+    xd = to_device(vals, F32)
+    for dt in (F16, BF16):
+        out = empty((4096,), dt)
+        hip.convert(xd, out, 4096)
+        assert np.array_equal(to_host(out, dt), orc.encode(vals, dt))
