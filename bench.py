@@ -1,0 +1,206 @@
+"""Benchmark: 12-layer GPT decoder prefill on the MI355X HIP engine.
+
+BASELINE.json metric "decoder inference tokens/s at 1 GPU" on configs[4]
+(GPT-style decoder bf16: 12 layers, d_model 768, 12 heads, FFN 3072 GELU,
+vocab 32000, causal, batch 4, seq 1024, full prefill forward to logits),
+with seeded uniform token ids and N(0, 0.02) weights.
+
+One step = one compiled forward (one hipGraph launch) over the resident
+[4, 1024] ids already in HBM.  W untimed warm-up steps, then exactly K timed
+steps bracketed by torch.cuda.synchronize() on both sides.
+
+Roofline: every kernel of the forward is also timed on its own with HIP
+events (eager launches on torch's current stream, the stream they are
+enqueued on); the kernel with the largest time per forward is reported
+against the bf16 MFMA peak (GEMM / attention: algorithmic 2*M*N*K FLOPs) or
+the HBM peak (LayerNorm: unique bytes).  CPU baseline: the C++ restatement
+of MuNet's CPU backend (oracle/, "port") on a bounded sample of the same
+forward, timed on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16 = 2.5e15      # dense bf16 MFMA, FLOP/s
+PEAK_HBM = 8.0e12       # HBM3E, B/s
+
+CFG = dict(vocab=32000, ctx=1024, d_model=768, num_heads=12, num_layers=12, ffn=3072, dtype="bfloat16")
+B, T = 4, 1024
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def kernel_table(hip, torch):
+    """Per-kernel event timing of every distinct kernel of the forward."""
+    from munet_amd.backend import empty
+    d, H, F, V = CFG["d_model"], CFG["num_heads"], CFG["ffn"], CFG["vocab"]
+    M, hd, L = B * T, d // H, CFG["num_layers"]
+    bf = torch.bfloat16
+    g = torch.Generator(device="cuda").manual_seed(0)
+
+    def rnd(*s, scale=1.0):
+        return (torch.randn(*s, device="cuda", generator=g) * scale).to(bf)
+
+    x, w = rnd(M, d), rnd(M, F)
+    rows = []
+
+    def timeit(name, fn, count, flops=0.0, bytes_=0.0, reps=20):
+        fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        t = s.elapsed_time(e) / reps * 1e-3
+        rows.append(dict(name=name, t=t, count=count, flops=flops, bytes=bytes_))
+
+    for (name, K_, N_, act, resid) in [("ffn_up_gelu", d, F, 2, False), ("ffn_down_resid", F, d, 0, True),
+                                        ("attn_out_resid", d, d, 0, True), ("lm_head", d, V, 0, False)]:
+        a = x if K_ == d else w
+        wt = rnd(N_, K_, scale=0.02)
+        bias = torch.zeros(N_, device="cuda", dtype=bf)
+        out = empty((M, N_), 2)
+        r = rnd(M, N_) if resid else None
+        timeit(name, lambda: hip.linear(a, wt, bias, out, M, K_, N_, act, r), 1 if name == "lm_head" else L,
+               flops=2.0 * M * N_ * K_)
+    wqkv = rnd(3 * d, d, scale=0.02)
+    bq = torch.zeros(3 * d, device="cuda", dtype=bf)
+    q, k, v = (empty((M * d,), 2) for _ in range(3))
+    timeit("qkv_headsplit", lambda: hip.qkv_projection(x, wqkv, bq, q, k, v, B, T, d, H), L, flops=2.0 * M * 3 * d * d)
+    ctx = empty((M, d), 2)
+    timeit("attention_causal", lambda: hip.attention(q, k, v, ctx, B, H, T, hd, True), L,
+           flops=4.0 * B * H * T * T * hd / 2)
+    lw, lb, ly = rnd(d), rnd(d), empty((M, d), 2)
+    timeit("layer_norm", lambda: hip.layer_norm(x, lw, lb, ly, M, d), 2 * L + 1, bytes_=2.0 * M * d * 2 + 2 * d * 2)
+    return rows
+
+
+def cpu_baseline():
+    """Oracle restatement on a bounded sample: 1 of the 12 decoder layers plus
+    final LayerNorm + LM head for 1 of the 4 sequences (1024 tokens), the
+    forward time extrapolated to 12 layers."""
+    from munet_amd import models, synth
+    from oracle import CpuOracle
+    from oracle import models as om
+    orc = CpuOracle("restatement")
+    cfg = models.decoder_config(**{**CFG, "num_layers": 1})
+    params = models.init_params(cfg, "gpt", scope="cpu")
+    ids = models.make_input(cfg, (1, T), "gpt", scope="cpu_in")
+    dt = synth.BF16
+    t0 = time.perf_counter()
+    x = om.decoder_embed(orc, cfg, params, ids)
+    t1 = time.perf_counter()
+    x = om.block_forward(orc, cfg, params, x, "blocks.0.", True)
+    t2 = time.perf_counter()
+    x = orc.layer_norm(x, params["ln_f.weight"], params["ln_f.bias"], dt)
+    orc.linear(x, params["head.weight"], params["head.bias"], dt)
+    t3 = time.perf_counter()
+    fwd = (t1 - t0) + CFG["num_layers"] * (t2 - t1) + (t3 - t2)
+    return dict(value=T / fwd, unit="tokens/s", cores=orc.threads(), kind="port",
+                sample=(f"1 of 12 decoder layers + ln_f + LM head on 1 sequence x {T} tokens "
+                        f"({t3 - t0:.1f} s measured: embed {t1 - t0:.2f}s, layer {t2 - t1:.2f}s, "
+                        f"head {t3 - t2:.2f}s), extrapolated to 12 layers"))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the single-GPU design and how the path would shard are in DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from munet_amd import models
+    from munet_amd.backend import HipBackend
+    from munet_amd.engine import Engine
+
+    hip = HipBackend(0)
+    cfg = models.decoder_config(**CFG)
+    log("bench: initialising weights")
+    params = models.init_params(cfg, "gpt", scope="bench")
+    ids = models.make_input(cfg, (B, T), "gpt", scope="bench_in")
+    log("bench: compiling engine")
+    eng = Engine(0).load(cfg, params).compile((B, T))
+    del params
+    logits = eng.run(ids)  # places the ids in the engine's input buffer (HBM)
+    assert np.isfinite(logits[:, :8].astype(np.float32)).all()
+
+    for _ in range(args.warmup):
+        eng.launch()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        eng.launch()
+    torch.cuda.synchronize()
+    dt_s = time.perf_counter() - t0
+    ms = dt_s / args.steps * 1e3
+    tokens_s = B * T * args.steps / dt_s
+    log(f"bench: {ms:.3f} ms/forward, {tokens_s:,.0f} tokens/s")
+
+    rows = kernel_table(hip, torch)
+    for r in rows:
+        r["per_fwd"] = r["t"] * r["count"]
+    dom = max(rows, key=lambda r: r["per_fwd"])
+    if dom["flops"]:
+        ach = dom["flops"] / dom["t"]
+        roof = dict(bound="mfma", achieved=ach / 1e12, peak=PEAK_BF16 / 1e12, unit="TFLOP/s", frac=ach / PEAK_BF16)
+    else:
+        ach = dom["bytes"] / dom["t"]
+        roof = dict(bound="hbm", achieved=ach / 1e9, peak=PEAK_HBM / 1e9, unit="GB/s", frac=ach / PEAK_HBM)
+    roof.update(kernel=dom["name"], avg_us=dom["t"] * 1e6, traffic=None)
+    gemm = [r for r in rows if r["flops"] and r["name"] != "attention_causal"]
+    gemm_frac = sum(r["flops"] * r["count"] for r in gemm) / sum(r["per_fwd"] for r in gemm) / PEAK_BF16
+    ln = next(r for r in rows if r["name"] == "layer_norm")
+    kernels = {r["name"]: dict(avg_us=round(r["t"] * 1e6, 2), per_forward=r["count"],
+                               tflops=round(r["flops"] / r["t"] / 1e12, 1) if r["flops"] else None,
+                               gbs=round(r["bytes"] / r["t"] / 1e9, 1) if r["bytes"] else None) for r in rows}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("bench: timing the CPU baseline sample")
+        cpu = cpu_baseline()
+    line = {
+        "metric": "decoder inference tokens/s at 1 GPU",
+        "value": tokens_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded uniform token ids [4,1024], N(0,0.02) weights (random init)",
+        "config": {"workload": "gpt_decoder_prefill (BASELINE configs[4])", "layers": 12, "d_model": 768,
+                   "heads": 12, "ffn": 3072, "vocab": 32000, "batch": B, "seq_len": T, "causal": True,
+                   "tokens_per_step": B * T},
+        "roofline": roof,
+        "gemm_mfma_frac": gemm_frac,
+        "layernorm_hbm_frac": (ln["bytes"] / ln["t"]) / PEAK_HBM,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,67 @@
+/* C ABI of the compiled inference executor in libmunet_hip.so.
+ *
+ * Mirrors inference::Engine (reference src/inference.hpp:292-801):
+ *   load    -> mh_engine_create (module config) + mh_engine_set_param
+ *              (reference Engine::load(module) / load_serialized,
+ *              src/inference.hpp:389-444, src/inference_serialization.cpp:1086)
+ *   compile -> mh_engine_compile (reference Engine::compile,
+ *              src/inference.hpp:446-537: shape contract + warm-up forward).
+ *              Here compile also traces the module tree into an op list,
+ *              fuses epilogues (bias, ReLU/GELU, residual, head split,
+ *              zero-copy concat), plans every activation into one hipMalloc
+ *              arena by liveness, and captures the forward as a hipGraph.
+ *   run     -> mh_engine_run (reference Engine::run, src/inference.hpp:
+ *              541-610): H2D of the input, one graph launch, D2H of the output.
+ *   stats   -> mh_engine_stats (EngineStats, src/inference.hpp:43-66) as JSON.
+ *
+ * Config JSON uses the reference's serialized module schema
+ * (src/inference_serialization.cpp:762-860: Sequential, Linear, Conv2d,
+ * MaxPool2d, Upsample, ReLU, Sigmoid, GELU, Softmax, Flatten, LayerNorm,
+ * Embedding, MultiHeadAttention) plus the composite TransformerBlock,
+ * DecoderLM and UNet workloads; "dtype" is float32 / float16 / bfloat16.
+ * Parameter names follow Module::named_parameters (src/core/module.hpp:95-107).
+ *
+ * device < 0 creates a plan-only engine: compile traces, fuses and plans but
+ * touches no GPU (used to test the planner on hosts without a GPU). */
+#ifndef MUNET_HIP_ENGINE_H
+#define MUNET_HIP_ENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mh_engine mh_engine;
+
+int mh_engine_create(mh_engine **engine, const char *config_json, int device);
+int mh_engine_destroy(mh_engine *engine);
+/* Copy one parameter (host storage bits of `dtype`, MuNet layout) into the
+ * engine; weights are packed for the kernels at compile time. */
+int mh_engine_set_param(mh_engine *engine, const char *name, const void *host_data, size_t bytes, int dtype);
+/* Compile for one input shape (exact shape contract). */
+int mh_engine_compile(mh_engine *engine, const int *input_shape, int ndim);
+/* Device address of the input / output buffers inside the arena. */
+int mh_engine_input_ptr(mh_engine *engine, void **ptr);
+int mh_engine_output_ptr(mh_engine *engine, void **ptr);
+/* Output shape (ndim written to *ndim, dims to shape[0..ndim)). */
+int mh_engine_output_shape(mh_engine *engine, int *shape, int *ndim);
+/* Host-to-host forward: input/output are host buffers in storage format. */
+int mh_engine_run(mh_engine *engine, const void *host_input, void *host_output);
+/* Forward on the device-resident input buffer; waits for completion. */
+int mh_engine_run_device(mh_engine *engine);
+/* Enqueue one forward (graph launch) on the engine stream without waiting. */
+int mh_engine_launch(mh_engine *engine);
+/* The engine's HIP stream. */
+int mh_engine_stream(mh_engine *engine, void **stream);
+/* EngineStats as a JSON object. */
+int mh_engine_stats(mh_engine *engine, char *buf, size_t len);
+/* The compiled plan (ops, fused epilogues, arena offsets) as JSON. */
+int mh_engine_plan(mh_engine *engine, char *buf, size_t len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MUNET_HIP_ENGINE_H */

@@ -115,6 +115,14 @@ def load():
             raise ImportError(
                 f"{LIB_PATH} is missing: build the HIP backend with `python -m munet_amd.build` "
                 "(there is no CPU fallback)")
+        # One HIP runtime per process: torch ships its own libamdhip64 (same
+        # SONAME, different file).  Loading torch first makes this library's
+        # NEEDED libamdhip64.so.7 bind to the runtime torch already loaded;
+        # the other order would start a second HIP/HSA runtime in the process.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         lib = ctypes.CDLL(LIB_PATH)
         for name, argt in _SIGS.items():
             fn = getattr(lib, name, None)

@@ -1,0 +1,859 @@
+// Compiled inference executor for the HIP backend (C ABI in
+// include/munet_hip_engine.h).
+//
+// The reference's inference::Engine (src/inference.hpp:292-801) runs the
+// module tree eagerly op by op; its compile() is a shape contract plus warm-up
+// forwards (src/inference.hpp:446-537) and every op output is a fresh
+// allocation (src/backend/cpu_backend.hpp:188-209).  This executor keeps the
+// same load / compile / run contract and, at compile time:
+//   1. traces the module tree (reference nn:: semantics per module) into a
+//      linear op list over SSA values;
+//   2. fuses: GEMM + bias + ReLU/GELU (+ residual) epilogues, conv + bias +
+//      ReLU, q/k/v projections into one head-splitting GEMM, token + position
+//      embedding + add, and UNet skip concats into zero-copy channel slices;
+//   3. plans every activation into one device arena by liveness intervals
+//      (greedy best-offset placement, largest first); weights live in a
+//      second arena packed into the kernels' K-contiguous layouts;
+//   4. captures the whole forward into a hipGraph on one stream.
+// run() is then one H2D copy, one graph launch and one D2H copy.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "../../include/munet_hip.h"
+#include "../../include/munet_hip_engine.h"
+#include "host_codec.hpp"
+#include "json.hpp"
+#include "mh_kernels.hpp"
+#include "mh_runtime.hpp"
+
+namespace mh {
+namespace {
+
+using Shape = std::vector<int>;
+
+size_t numel(const Shape &s) {
+  size_t n = 1;
+  for (int d : s) n *= size_t(d);
+  return n;
+}
+
+std::string shape_str(const Shape &s) {
+  std::string r = "[";
+  for (size_t i = 0; i < s.size(); ++i) r += (i ? "," : "") + std::to_string(s[i]);
+  return r + "]";
+}
+
+enum Layout { ROWMAJOR = 0, NHWC = 1 };
+
+struct Val {
+  Shape shape;   // logical shape (NCHW order for 4-D tensors even when stored NHWC)
+  int dt = F32;
+  int layout = ROWMAJOR;
+  int alias_of = -1;   // value whose buffer this one lives in
+  long alias_off = 0;  // element offset inside that buffer
+  long row_stride = 0; // NHWC channel-slice views: elements between pixels
+  int def = -1, last = -1;
+  long offset = -1;    // byte offset in the arena (resolved through aliases)
+  size_t bytes() const { return numel(shape) * dt_size(dt); }
+};
+
+enum OpKind {
+  OP_GEMM, OP_QKV, OP_ATTN, OP_LN, OP_EMBED, OP_EMBED_POS, OP_CONV, OP_CONVT, OP_POOL, OP_UPSAMPLE,
+  OP_UNARY, OP_BINARY, OP_SOFTMAX, OP_TO_NHWC, OP_TO_NCHW
+};
+
+const char *op_name(int k) {
+  static const char *n[] = {"gemm", "qkv_gemm", "attention", "layer_norm", "embedding", "embedding_pos", "conv2d",
+                            "conv_transpose2d", "max_pool2d", "upsample2d", "unary", "binary", "softmax",
+                            "nchw_to_nhwc", "nhwc_to_nchw"};
+  return n[k];
+}
+
+struct Op {
+  int kind;
+  std::string name;
+  std::vector<int> in, out;
+  // integer attributes (meaning per kind)
+  long a[12] = {0};
+  float f = 0.f;
+  const void *w = nullptr, *b = nullptr, *w2 = nullptr;
+  int act = ACT_NONE;
+  int resid = -1;  // residual value id (GEMM)
+};
+
+struct Param {
+  std::vector<uint8_t> host;
+  int dt = F32;
+  Shape shape;  // informational
+};
+
+}  // namespace
+
+struct EngineImpl {
+  json::Value cfg;
+  int device = 0;
+  bool plan_only = false;
+  int dt = F32;
+  std::map<std::string, Param> params;
+
+  std::vector<Val> vals;
+  std::vector<Op> ops;
+  int input = -1, output = -1;
+  Shape in_shape;
+
+  // device state
+  hipStream_t stream = nullptr;
+  char *arena = nullptr;
+  size_t arena_bytes = 0;
+  char *wbuf = nullptr;
+  size_t wbytes = 0;
+  std::vector<std::pair<std::vector<uint8_t>, size_t>> wpending;  // host bytes -> offset
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  bool compiled = false;
+
+  // stats
+  double compile_ms = 0, last_run_ms = 0, last_gpu_ms = 0, load_ms = 0;
+  size_t runs = 0, fused_epilogues = 0, zero_copy_concats = 0;
+
+  ~EngineImpl() {
+    if (plan_only) return;
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    if (arena) (void)hipFree(arena);
+    if (wbuf) (void)hipFree(wbuf);
+    if (ev0) (void)hipEventDestroy(ev0);
+    if (ev1) (void)hipEventDestroy(ev1);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+
+  // ---------------------------------------------------------------- values
+  int new_val(const Shape &s, int vdt, int layout = ROWMAJOR) {
+    Val v;
+    v.shape = s;
+    v.dt = vdt;
+    v.layout = layout;
+    vals.push_back(v);
+    return int(vals.size()) - 1;
+  }
+  int alias(int base, const Shape &s, long off = 0, int layout = ROWMAJOR, long row_stride = 0) {
+    int id = new_val(s, vals[base].dt, layout);
+    vals[id].alias_of = base;
+    vals[id].alias_off = off;
+    vals[id].row_stride = row_stride;
+    return id;
+  }
+  int root(int v) const {
+    while (vals[v].alias_of >= 0) v = vals[v].alias_of;
+    return v;
+  }
+  long elem_off(int v) const {
+    long off = 0;
+    while (vals[v].alias_of >= 0) {
+      off += vals[v].alias_off;
+      v = vals[v].alias_of;
+    }
+    return off;
+  }
+  Op &emit(int kind, const std::string &name, std::vector<int> in, std::vector<int> out) {
+    Op o;
+    o.kind = kind;
+    o.name = name;
+    o.in = std::move(in);
+    o.out = std::move(out);
+    ops.push_back(o);
+    return ops.back();
+  }
+
+  // ---------------------------------------------------------------- params
+  const Param &param(const std::string &n) const {
+    auto it = params.find(n);
+    if (it == params.end()) throw Error("missing parameter '" + n + "'");
+    if (it->second.dt != dt) throw Error("parameter '" + n + "' has the wrong dtype");
+    return it->second;
+  }
+  // Pending device upload of host bytes into the weights arena.
+  const void *upload(std::vector<uint8_t> bytes) {
+    const size_t off = wbytes;
+    wbytes += (bytes.size() + 255) & ~size_t(255);
+    wpending.emplace_back(std::move(bytes), off);
+    return reinterpret_cast<const void *>(off + 1);  // resolved after allocation (+1: never null)
+  }
+  // Linear weight [in, out] -> [out, in] (K-contiguous panels).
+  std::vector<uint8_t> pack_linear(const Param &p, int in_f, int out_f) const {
+    const size_t es = dt_size(dt);
+    if (p.host.size() != size_t(in_f) * out_f * es) throw Error("linear weight has the wrong size");
+    std::vector<uint8_t> t(p.host.size());
+    for (int i = 0; i < in_f; ++i)
+      for (int o = 0; o < out_f; ++o)
+        std::memcpy(&t[(size_t(o) * in_f + i) * es], &p.host[(size_t(i) * out_f + o) * es], es);
+    return t;
+  }
+  // Conv weight OIHW -> OHWI.
+  std::vector<uint8_t> pack_conv(const Param &p, int oC, int iC, int k) const {
+    const size_t es = dt_size(dt);
+    if (p.host.size() != size_t(oC) * iC * k * k * es) throw Error("conv weight has the wrong size");
+    std::vector<uint8_t> t(p.host.size());
+    for (int o = 0; o < oC; ++o)
+      for (int c = 0; c < iC; ++c)
+        for (int q = 0; q < k * k; ++q)
+          std::memcpy(&t[((size_t(o) * k * k + q) * iC + c) * es], &p.host[((size_t(o) * iC + c) * k * k + q) * es], es);
+    return t;
+  }
+  // ConvTranspose weight [iC, oC, k, k] -> [k, k, oC, iC].
+  std::vector<uint8_t> pack_convt(const Param &p, int iC, int oC, int k) const {
+    const size_t es = dt_size(dt);
+    if (p.host.size() != size_t(oC) * iC * k * k * es) throw Error("conv_transpose weight has the wrong size");
+    std::vector<uint8_t> t(p.host.size());
+    for (int c = 0; c < iC; ++c)
+      for (int o = 0; o < oC; ++o)
+        for (int q = 0; q < k * k; ++q)
+          std::memcpy(&t[((size_t(q) * oC + o) * iC + c) * es], &p.host[((size_t(c) * oC + o) * k * k + q) * es], es);
+    return t;
+  }
+  const void *bias_or_zero(const std::string &n, int len) {
+    auto it = params.find(n);
+    if (it != params.end()) return upload(it->second.host);
+    return upload(std::vector<uint8_t>(size_t(len) * dt_size(dt), 0));
+  }
+
+  // ---------------------------------------------------------------- lowering
+  int to_rowmajor4(int x, const std::string &name) {
+    if (vals[x].layout != NHWC) return x;
+    const Shape s = vals[x].shape;
+    int y = new_val(s, vals[x].dt, ROWMAJOR);
+    Op &o = emit(OP_TO_NCHW, name + ".to_nchw", {x}, {y});
+    o.a[0] = s[0]; o.a[1] = s[1]; o.a[2] = s[2] * s[3];
+    return y;
+  }
+  int to_nhwc(int x, const std::string &name) {
+    if (vals[x].layout == NHWC) return x;
+    const Shape s = vals[x].shape;
+    if (s.size() != 4) throw Error(name + ": expected a 4-D [B,C,H,W] input");
+    int y = new_val(s, vals[x].dt, NHWC);
+    Op &o = emit(OP_TO_NHWC, name + ".to_nhwc", {x}, {y});
+    o.a[0] = s[0]; o.a[1] = s[1]; o.a[2] = s[2] * s[3];
+    return y;
+  }
+
+  // y = act(x W + b) (+ resid); x [..., in]
+  int linear(int x, const std::string &pfx, int in_f, int out_f, bool has_bias, int act = ACT_NONE, int resid = -1,
+             int out_val = -1) {
+    x = to_rowmajor4(x, pfx);
+    const Shape s = vals[x].shape;
+    if (s.empty() || s.back() != in_f) throw Error(pfx + ": input " + shape_str(s) + " does not end in " + std::to_string(in_f));
+    Shape os = s;
+    os.back() = out_f;
+    const int y = out_val >= 0 ? out_val : new_val(os, dt);
+    Op &o = emit(OP_GEMM, pfx.empty() ? "linear" : pfx.substr(0, pfx.size() - 1), {x}, {y});
+    o.a[0] = long(numel(s) / in_f);  // M
+    o.a[1] = out_f;                  // N
+    o.a[2] = in_f;                   // K
+    o.w = upload(pack_linear(param(pfx + "weight"), in_f, out_f));
+    o.b = has_bias ? bias_or_zero(pfx + "bias", out_f) : nullptr;
+    o.act = act;
+    if (resid >= 0) {
+      o.resid = resid;
+      o.in.push_back(resid);
+    }
+    if (act != ACT_NONE || resid >= 0) ++fused_epilogues;
+    return y;
+  }
+
+  int conv(int x, const std::string &pfx, int iC, int oC, int k, int s, int p, int act, int out_view = -1) {
+    x = to_nhwc(x, pfx);
+    const Shape xs = vals[x].shape;
+    if (xs[1] != iC) throw Error(pfx + ": channel mismatch");
+    const int oH = (xs[2] + 2 * p - k) / s + 1, oW = (xs[3] + 2 * p - k) / s + 1;
+    const int y = out_view >= 0 ? out_view : new_val({xs[0], oC, oH, oW}, dt, NHWC);
+    Op &o = emit(OP_CONV, pfx.substr(0, pfx.size() - 1), {x}, {y});
+    o.a[0] = xs[0]; o.a[1] = iC; o.a[2] = xs[2]; o.a[3] = xs[3]; o.a[4] = oC; o.a[5] = k; o.a[6] = s; o.a[7] = p;
+    o.w = upload(pack_conv(param(pfx + "weight"), oC, iC, k));
+    o.b = bias_or_zero(pfx + "bias", oC);
+    o.act = act;
+    if (act != ACT_NONE) ++fused_epilogues;
+    return y;
+  }
+
+  int unary(int x, int op, const std::string &name) {
+    // fusion: fold ReLU / GELU into the producing GEMM / conv epilogue when
+    // this op is its only consumer
+    if (!ops.empty() && (op == UN_RELU || op == UN_GELU)) {
+      Op &prev = ops.back();
+      const bool producer = prev.out.size() == 1 && prev.out[0] == x;
+      const bool gemm_ok = prev.kind == OP_GEMM && prev.resid < 0;
+      const bool conv_ok = prev.kind == OP_CONV && op == UN_RELU;
+      if (producer && (gemm_ok || conv_ok) && prev.act == ACT_NONE) {
+        prev.act = op == UN_RELU ? ACT_RELU : ACT_GELU;
+        prev.name += op == UN_RELU ? "+relu" : "+gelu";
+        ++fused_epilogues;
+        return x;
+      }
+    }
+    int y = new_val(vals[x].shape, dt, vals[x].layout);
+    Op &o = emit(OP_UNARY, name, {x}, {y});
+    o.a[0] = op;
+    o.a[1] = long(numel(vals[x].shape));
+    o.f = host_round(dt, 1.702f);
+    return y;
+  }
+
+  int layer_norm(int x, const std::string &pfx, int d, float eps) {
+    x = to_rowmajor4(x, pfx);
+    if (vals[x].shape.back() != d) throw Error(pfx + ": normalized_shape mismatch");
+    int y = new_val(vals[x].shape, dt);
+    Op &o = emit(OP_LN, pfx.substr(0, pfx.size() - 1), {x}, {y});
+    o.a[0] = long(numel(vals[x].shape) / d);
+    o.a[1] = d;
+    o.f = eps;
+    o.w = upload(param(pfx + "weight").host);
+    o.b = upload(param(pfx + "bias").host);
+    return y;
+  }
+
+  // nn::MultiHeadAttention (src/nn/attention.hpp:34-104) on x [B,T,E]; the
+  // out-projection optionally adds a residual in its epilogue.
+  int mha(int x, const std::string &pfx, int E, int H, bool causal, int resid = -1) {
+    const Shape s = vals[x].shape;
+    if (s.size() != 3 || s[2] != E) throw Error(pfx + ": MultiHeadAttention expects [B,T,E]");
+    const int B = s[0], T = s[1], hd = E / H;
+    if (E % H) throw Error(pfx + ": embed_dim must be divisible by num_heads");
+    // fused q/k/v projection: weights [E,3E] -> [3E,E], biases [3E]
+    std::vector<uint8_t> wcat, bcat;
+    for (const char *p : {"q_proj.", "k_proj.", "v_proj."}) {
+      auto w = pack_linear(param(pfx + p + "weight"), E, E);
+      wcat.insert(wcat.end(), w.begin(), w.end());
+      const auto &b = param(pfx + p + "bias").host;
+      bcat.insert(bcat.end(), b.begin(), b.end());
+    }
+    const int q = new_val({B * H, T, hd}, dt), k = new_val({B * H, T, hd}, dt), v = new_val({B * H, T, hd}, dt);
+    Op &o = emit(OP_QKV, pfx + "qkv_proj", {x}, {q, k, v});
+    o.a[0] = B; o.a[1] = T; o.a[2] = E; o.a[3] = H;
+    o.w = upload(std::move(wcat));
+    o.b = upload(std::move(bcat));
+    const int ctx = new_val({B, T, E}, dt);
+    Op &a = emit(OP_ATTN, pfx + "attention", {q, k, v}, {ctx});
+    a.a[0] = B; a.a[1] = H; a.a[2] = T; a.a[3] = hd; a.a[4] = causal ? 1 : 0;
+    a.f = host_round(dt, 1.0f / std::sqrt(float(hd)));
+    return linear(ctx, pfx + "out_proj.", E, E, true, ACT_NONE, resid);
+  }
+
+  // Pre-LN transformer block: x + attn(ln1(x)), then x + ff(ln2(x))
+  // (demos/multigpu/gpt3_multi_gpu_demo.py:105-114).
+  int block(int x, const std::string &pfx, int d, int H, int ffn, bool causal, float eps) {
+    int h = layer_norm(x, pfx + "ln1.", d, eps);
+    int x2 = mha(h, pfx + "attn.", d, H, causal, x);
+    int h2 = layer_norm(x2, pfx + "ln2.", d, eps);
+    int f = linear(h2, pfx + "ff.0.", d, ffn, true, ACT_GELU);
+    return linear(f, pfx + "ff.2.", ffn, d, true, ACT_NONE, x2);
+  }
+
+  int lower(const json::Value &m, int x, const std::string &pfx) {
+    const std::string t = m.at("type").as_str();
+    if (t == "Sequential") {
+      const auto &layers = m.at("layers").arr;
+      for (size_t i = 0; i < layers.size(); ++i) x = lower(layers[i], x, pfx + std::to_string(i) + ".");
+      return x;
+    }
+    if (t == "Linear")
+      return linear(x, pfx, m.at("in_features").as_int(), m.at("out_features").as_int(), m.get_bool("bias", true));
+    if (t == "ReLU") return unary(x, UN_RELU, pfx + "relu");
+    if (t == "Sigmoid") return unary(x, UN_SIGMOID, pfx + "sigmoid");
+    if (t == "GELU") return unary(x, UN_GELU, pfx + "gelu");
+    if (t == "Dropout" || t == "Identity") return x;  // eval mode
+    if (t == "Softmax") {
+      x = to_rowmajor4(x, pfx);
+      int y = new_val(vals[x].shape, dt);
+      Op &o = emit(OP_SOFTMAX, pfx + "softmax", {x}, {y});
+      o.a[1] = vals[x].shape.back();
+      o.a[0] = long(numel(vals[x].shape) / o.a[1]);
+      return y;
+    }
+    if (t == "Conv2d")
+      return conv(x, pfx, m.at("in_channels").as_int(), m.at("out_channels").as_int(), m.at("kernel_size").as_int(),
+                  m.get_int("stride", 1), m.get_int("padding", 0), ACT_NONE);
+    if (t == "MaxPool2d" || t == "Upsample") {
+      const Shape xs = vals[x].shape;
+      if (xs.size() != 4) throw Error(pfx + t + ": expected [B,C,H,W]");
+      const bool pool = t == "MaxPool2d";
+      const int k = pool ? m.at("kernel_size").as_int() : m.at("scale_factor").as_int();
+      const int s = pool ? m.get_int("stride", k) : 1, p = pool ? m.get_int("padding", 0) : 0;
+      Shape os = pool ? Shape{xs[0], xs[1], (xs[2] + 2 * p - k) / s + 1, (xs[3] + 2 * p - k) / s + 1}
+                      : Shape{xs[0], xs[1], xs[2] * k, xs[3] * k};
+      int y = new_val(os, dt, vals[x].layout);
+      Op &o = emit(pool ? OP_POOL : OP_UPSAMPLE, pfx + (pool ? "max_pool2d" : "upsample2d"), {x}, {y});
+      o.a[0] = xs[0]; o.a[1] = xs[1]; o.a[2] = xs[2]; o.a[3] = xs[3]; o.a[4] = k; o.a[5] = s; o.a[6] = p;
+      o.a[7] = vals[x].layout == NHWC;
+      return y;
+    }
+    if (t == "Flatten") {
+      x = to_rowmajor4(x, pfx);
+      const Shape xs = vals[x].shape;
+      return alias(x, {xs[0], int(numel(xs) / xs[0])});
+    }
+    if (t == "LayerNorm") return layer_norm(x, pfx, m.at("normalized_shape").as_int(), float(m.get_num("eps", 1e-5)));
+    if (t == "MultiHeadAttention")
+      return mha(x, pfx, m.at("embed_dim").as_int(), m.at("num_heads").as_int(), m.get_bool("causal", true));
+    if (t == "Embedding") {
+      const Shape xs = vals[x].shape;
+      const int V = m.at("num_embeddings").as_int(), D = m.at("embedding_dim").as_int();
+      if (vals[x].dt != I32 || xs.size() != 2) throw Error(pfx + "Embedding: expects int32 [B,T] ids");
+      int y = new_val({xs[0], xs[1], D}, dt);
+      Op &o = emit(OP_EMBED, pfx + "embedding", {x}, {y});
+      o.a[0] = long(numel(xs)); o.a[1] = V; o.a[2] = D; o.a[3] = 1;
+      o.w = upload(param(pfx + "weight").host);
+      return y;
+    }
+    if (t == "TransformerBlock")
+      return block(x, pfx, m.at("d_model").as_int(), m.at("num_heads").as_int(), m.at("ffn").as_int(),
+                   m.get_bool("causal", false), float(m.get_num("eps", 1e-5)));
+    if (t == "DecoderLM") {
+      const Shape xs = vals[x].shape;
+      const int V = m.at("vocab").as_int(), C = m.at("ctx").as_int(), d = m.at("d_model").as_int();
+      if (vals[x].dt != I32 || xs.size() != 2) throw Error("DecoderLM: expects int32 [B,T] ids");
+      if (xs[1] > C) throw Error("DecoderLM: sequence longer than the position table");
+      // token + position gathers and their add, one rounding
+      int h = new_val({xs[0], xs[1], d}, dt);
+      Op &o = emit(OP_EMBED_POS, pfx + "embed", {x}, {h});
+      o.a[0] = long(numel(xs)); o.a[1] = V; o.a[2] = d; o.a[3] = xs[1];
+      o.w = upload(param(pfx + "token_embed.weight").host);
+      o.w2 = upload(param(pfx + "pos_embed.weight").host);
+      const int L = m.at("num_layers").as_int(), H = m.at("num_heads").as_int(), ffn = m.at("ffn").as_int();
+      const float eps = float(m.get_num("eps", 1e-5));
+      for (int i = 0; i < L; ++i) h = block(h, pfx + "blocks." + std::to_string(i) + ".", d, H, ffn, true, eps);
+      h = layer_norm(h, pfx + "ln_f.", d, eps);
+      return linear(h, pfx + "head.", d, V, true);
+    }
+    if (t == "UNet") return unet(m, x, pfx);
+    throw Error("unsupported module type '" + t + "'");
+  }
+
+  // Build-defined UNet (the reference has no transposed conv): per level two
+  // conv3x3+ReLU and a stride-2 conv3x3+ReLU downsample; decoder levels
+  // ConvTranspose2d(2,2) then cat([up, skip]) and two conv3x3+ReLU; 1x1 head.
+  // The skip conv writes straight into the right half of its level's concat
+  // buffer and the transposed conv into the left half (zero-copy concat).
+  int unet(const json::Value &m, int x, const std::string &pfx) {
+    std::vector<int> ch;
+    for (const auto &c : m.at("channels").arr) ch.push_back(c.as_int());
+    const int L = int(ch.size());
+    int prev = m.at("in_channels").as_int();
+    x = to_nhwc(x, pfx + "input");
+    std::vector<int> cat(L, -1);
+    for (int l = 0; l < L; ++l) {
+      const int c = ch[l];
+      x = conv(x, pfx + "enc" + std::to_string(l) + ".0.", prev, c, 3, 1, 1, ACT_RELU);
+      if (l < L - 1) {
+        const Shape xs = vals[x].shape;
+        cat[l] = new_val({xs[0], 2 * c, xs[2], xs[3]}, dt, NHWC);
+        const int skip = alias(cat[l], {xs[0], c, xs[2], xs[3]}, c, NHWC, 2 * c);
+        x = conv(x, pfx + "enc" + std::to_string(l) + ".1.", c, c, 3, 1, 1, ACT_RELU, skip);
+        ++zero_copy_concats;
+        x = conv(x, pfx + "down" + std::to_string(l) + ".", c, c, 3, 2, 1, ACT_RELU);
+      } else {
+        x = conv(x, pfx + "enc" + std::to_string(l) + ".1.", c, c, 3, 1, 1, ACT_RELU);
+      }
+      prev = c;
+    }
+    for (int l = L - 2; l >= 0; --l) {
+      const int c = ch[l];
+      const Shape xs = vals[x].shape;
+      const int up = alias(cat[l], {xs[0], c, xs[2] * 2, xs[3] * 2}, 0, NHWC, 2 * c);
+      Op &o = emit(OP_CONVT, pfx + "up" + std::to_string(l), {x}, {up});
+      o.a[0] = xs[0]; o.a[1] = ch[l + 1]; o.a[2] = xs[2]; o.a[3] = xs[3]; o.a[4] = c; o.a[5] = 2;
+      o.w = upload(pack_convt(param(pfx + "up" + std::to_string(l) + ".weight"), ch[l + 1], c, 2));
+      o.b = bias_or_zero(pfx + "up" + std::to_string(l) + ".bias", c);
+      x = conv(cat[l], pfx + "dec" + std::to_string(l) + ".0.", 2 * c, c, 3, 1, 1, ACT_RELU);
+      x = conv(x, pfx + "dec" + std::to_string(l) + ".1.", c, c, 3, 1, 1, ACT_RELU);
+    }
+    return conv(x, pfx + "head.", ch[0], m.at("out_channels").as_int(), 1, 1, 0, ACT_NONE);
+  }
+
+  // ---------------------------------------------------------------- planner
+  void plan() {
+    const int n = int(vals.size());
+    const int kUnset = 1 << 30;
+    for (auto &v : vals) { v.def = kUnset; v.last = -2; }
+    auto touch = [&](int v, int t) {
+      const int r = root(v);
+      vals[r].def = std::min(vals[r].def, t);
+      vals[r].last = std::max(vals[r].last, t);
+    };
+    touch(input, -1);
+    for (int i = 0; i < int(ops.size()); ++i) {
+      for (int v : ops[i].out) touch(v, i);
+      for (int v : ops[i].in) touch(v, i);
+    }
+    touch(output, int(ops.size()));
+    // roots ordered by size, placed at the lowest offset free for their interval
+    std::vector<int> order;
+    for (int v = 0; v < n; ++v)
+      if (vals[v].alias_of < 0 && vals[v].last >= -1) order.push_back(v);
+    std::sort(order.begin(), order.end(), [&](int a, int b) { return vals[a].bytes() > vals[b].bytes(); });
+    std::vector<int> placed;
+    arena_bytes = 0;
+    for (int v : order) {
+      const size_t sz = (vals[v].bytes() + 255) & ~size_t(255);
+      std::vector<std::pair<long, long>> busy;
+      for (int u : placed)
+        if (!(vals[u].last < vals[v].def || vals[v].last < vals[u].def))
+          busy.push_back({vals[u].offset, vals[u].offset + long((vals[u].bytes() + 255) & ~size_t(255))});
+      std::sort(busy.begin(), busy.end());
+      long off = 0;
+      for (auto &b : busy) {
+        if (off + long(sz) <= b.first) break;
+        off = std::max(off, b.second);
+      }
+      vals[v].offset = off;
+      arena_bytes = std::max(arena_bytes, size_t(off) + sz);
+      placed.push_back(v);
+    }
+    for (int v = 0; v < n; ++v)
+      if (vals[v].alias_of >= 0) vals[v].offset = vals[root(v)].offset + elem_off(v) * long(dt_size(vals[v].dt));
+  }
+
+  // ---------------------------------------------------------------- execution
+  void *dptr(int v) const { return arena + vals[v].offset; }
+  const void *wptr(const void *tag) const {
+    return tag ? static_cast<const void *>(wbuf + (reinterpret_cast<uintptr_t>(tag) - 1)) : nullptr;
+  }
+
+  void enqueue(const Op &o) {
+    hipStream_t st = stream;
+    switch (o.kind) {
+    case OP_GEMM: {
+      EpiArgs ep;
+      ep.out = dptr(o.out[0]);
+      ep.ldc = o.a[1];
+      ep.bias = wptr(o.b);
+      ep.act = o.act;
+      ep.gelu_c = host_round(dt, 1.702f);
+      if (o.resid >= 0) {
+        ep.resid = dptr(o.resid);
+        ep.ldr = o.a[1];
+      }
+      hip_check(gemm_nt(dt, dptr(o.in[0]), wptr(o.w), int(o.a[0]), int(o.a[1]), int(o.a[2]), o.a[2], o.a[2], 1, 0,
+                        0, 0, ep, -1, st),
+                o.name.c_str());
+      break;
+    }
+    case OP_QKV: {
+      const int B = int(o.a[0]), T = int(o.a[1]), E = int(o.a[2]), H = int(o.a[3]);
+      EpiArgs ep;
+      ep.mode = EPI_HEADSPLIT;
+      ep.outs[0] = dptr(o.out[0]);
+      ep.outs[1] = dptr(o.out[1]);
+      ep.outs[2] = dptr(o.out[2]);
+      ep.bias = wptr(o.b);
+      ep.T = T; ep.H = H; ep.hd = E / H; ep.E = E;
+      hip_check(gemm_nt(dt, dptr(o.in[0]), wptr(o.w), B * T, 3 * E, E, E, E, 1, 0, 0, 0, ep, -1, st), o.name.c_str());
+      break;
+    }
+    case OP_ATTN:
+      hip_check(attention(dt, dptr(o.in[0]), dptr(o.in[1]), dptr(o.in[2]), dptr(o.out[0]), int(o.a[0]), int(o.a[1]),
+                          int(o.a[2]), int(o.a[3]), int(o.a[4]), o.f, 0, st),
+                o.name.c_str());
+      break;
+    case OP_LN:
+      hip_check(layernorm(dt, dptr(o.in[0]), wptr(o.w), wptr(o.b), dptr(o.out[0]), int(o.a[0]), int(o.a[1]), o.f, st),
+                o.name.c_str());
+      break;
+    case OP_EMBED:
+    case OP_EMBED_POS:
+      hip_check(embedding(dt, static_cast<const int32_t *>(dptr(o.in[0])), wptr(o.w),
+                          o.kind == OP_EMBED_POS ? wptr(o.w2) : nullptr, dptr(o.out[0]), int(o.a[0]), int(o.a[1]),
+                          int(o.a[2]), int(o.a[3]), device_error_flag(), st),
+                o.name.c_str());
+      break;
+    case OP_CONV: {
+      ConvArgs cv;
+      cv.B = int(o.a[0]); cv.iC = int(o.a[1]); cv.iH = int(o.a[2]); cv.iW = int(o.a[3]);
+      cv.kH = cv.kW = int(o.a[5]); cv.s = int(o.a[6]); cv.p = int(o.a[7]);
+      cv.oH = (cv.iH + 2 * cv.p - cv.kH) / cv.s + 1;
+      cv.oW = (cv.iW + 2 * cv.p - cv.kW) / cv.s + 1;
+      const Val &xi = vals[o.in[0]];
+      cv.ldx = xi.row_stride ? xi.row_stride : cv.iC;
+      const Val &yo = vals[o.out[0]];
+      EpiArgs ep;
+      ep.out = dptr(o.out[0]);
+      ep.ldc = yo.row_stride ? yo.row_stride : o.a[4];
+      ep.bias = wptr(o.b);
+      ep.bias_first = 1;
+      ep.act = o.act;
+      hip_check(conv_nhwc(dt, dptr(o.in[0]), wptr(o.w), cv, int(o.a[4]), ep, -1, st), o.name.c_str());
+      break;
+    }
+    case OP_CONVT: {
+      const int B = int(o.a[0]), iC = int(o.a[1]), iH = int(o.a[2]), iW = int(o.a[3]), oC = int(o.a[4]),
+                k = int(o.a[5]);
+      const Val &yo = vals[o.out[0]];
+      EpiArgs ep;
+      ep.mode = EPI_CONVT;
+      ep.out = dptr(o.out[0]);
+      ep.ldc = yo.row_stride ? yo.row_stride : oC;
+      ep.bias = wptr(o.b);
+      ep.bias_first = 1;
+      ep.convt_oc = oC; ep.convt_k = k; ep.convt_ih = iH; ep.convt_iw = iW;
+      hip_check(gemm_nt(dt, dptr(o.in[0]), wptr(o.w), B * iH * iW, k * k * oC, iC, iC, iC, 1, 0, 0, 0, ep, -1, st),
+                o.name.c_str());
+      break;
+    }
+    case OP_POOL:
+      hip_check(max_pool2d(dt, int(o.a[7]), dptr(o.in[0]), dptr(o.out[0]), int(o.a[0]), int(o.a[1]), int(o.a[2]),
+                           int(o.a[3]), int(o.a[4]), int(o.a[5]), int(o.a[6]), st),
+                o.name.c_str());
+      break;
+    case OP_UPSAMPLE:
+      hip_check(upsample2d(dt, int(o.a[7]), dptr(o.in[0]), dptr(o.out[0]), int(o.a[0]), int(o.a[1]), int(o.a[2]),
+                           int(o.a[3]), int(o.a[4]), st),
+                o.name.c_str());
+      break;
+    case OP_UNARY:
+      hip_check(mh::unary(dt, int(o.a[0]), dptr(o.in[0]), dptr(o.out[0]), size_t(o.a[1]), o.f, st), o.name.c_str());
+      break;
+    case OP_SOFTMAX:
+      hip_check(softmax_rows(dt, dptr(o.in[0]), dptr(o.out[0]), int(o.a[0]), int(o.a[1]), st), o.name.c_str());
+      break;
+    case OP_TO_NHWC:
+      hip_check(nchw_to_nhwc(vals[o.in[0]].dt, dptr(o.in[0]), dptr(o.out[0]), int(o.a[0]), int(o.a[1]), int(o.a[2]), st),
+                o.name.c_str());
+      break;
+    case OP_TO_NCHW:
+      hip_check(nhwc_to_nchw(vals[o.in[0]].dt, dptr(o.in[0]), dptr(o.out[0]), int(o.a[0]), int(o.a[1]), int(o.a[2]), st),
+                o.name.c_str());
+      break;
+    default:
+      throw Error("engine: op kind not executable");
+    }
+  }
+
+  void compile(const Shape &ishape) {
+    const auto t0 = std::chrono::steady_clock::now();
+    if (compiled) throw Error("engine already compiled");
+    in_shape = ishape;
+    vals.clear();
+    ops.clear();
+    wbytes = 0;
+    wpending.clear();
+    const std::string t = cfg.at("type").as_str();
+    const bool ids = t == "DecoderLM" || t == "Embedding";
+    input = new_val(ishape, ids ? I32 : dt, ROWMAJOR);
+    int y = lower(cfg, input, "");
+    y = to_rowmajor4(y, "output");
+    output = y;
+    plan();
+    if (!plan_only) {
+      hip_check(hipSetDevice(device), "hipSetDevice");
+      hip_check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
+      hip_check(hipEventCreate(&ev0), "hipEventCreate");
+      hip_check(hipEventCreate(&ev1), "hipEventCreate");
+      hip_check(hipMalloc(&arena, std::max<size_t>(arena_bytes, 256)), "hipMalloc(arena)");
+      hip_check(hipMalloc(&wbuf, std::max<size_t>(wbytes, 256)), "hipMalloc(weights)");
+      for (auto &p : wpending)
+        hip_check(hipMemcpy(wbuf + p.second, p.first.data(), p.first.size(), hipMemcpyHostToDevice), "upload weights");
+      wpending.clear();
+      wpending.shrink_to_fit();
+      (void)device_error_flag();
+      // zero the arena once so the warm-up reads defined memory
+      hip_check(hipMemset(arena, 0, arena_bytes), "hipMemset(arena)");
+      // warm-up eager forward (sets kernel attributes outside capture)
+      for (const Op &o : ops) enqueue(o);
+      hip_check(hipStreamSynchronize(stream), "warm-up forward");
+      hip_check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+      try {
+        for (const Op &o : ops) enqueue(o);
+      } catch (...) {
+        hipGraph_t g = nullptr;
+        (void)hipStreamEndCapture(stream, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+      }
+      hip_check(hipStreamEndCapture(stream, &graph), "hipStreamEndCapture");
+      hip_check(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+    }
+    compiled = true;
+    compile_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  }
+
+  void require_device() const {
+    if (!compiled) throw Error("engine is not compiled");
+    if (plan_only) throw Error("plan-only engine cannot run");
+  }
+
+  void launch() {
+    require_device();
+    hip_check(hipGraphLaunch(exec, stream), "hipGraphLaunch");
+  }
+
+  void run_device() {
+    require_device();
+    hip_check(hipEventRecord(ev0, stream), "hipEventRecord");
+    hip_check(hipGraphLaunch(exec, stream), "hipGraphLaunch");
+    hip_check(hipEventRecord(ev1, stream), "hipEventRecord");
+    hip_check(hipStreamSynchronize(stream), "forward");
+    float ms = 0.f;
+    hip_check(hipEventElapsedTime(&ms, ev0, ev1), "hipEventElapsedTime");
+    last_gpu_ms = ms;
+    set_last_kernel_time_us(double(ms) * 1000.0);
+    ++runs;
+  }
+
+  void run(const void *hin, void *hout) {
+    require_device();
+    const auto t0 = std::chrono::steady_clock::now();
+    hip_check(hipMemcpyAsync(dptr(input), hin, vals[input].bytes(), hipMemcpyHostToDevice, stream), "input H2D");
+    run_device();
+    hip_check(hipMemcpyAsync(hout, dptr(output), vals[output].bytes(), hipMemcpyDeviceToHost, stream), "output D2H");
+    hip_check(hipStreamSynchronize(stream), "output D2H");
+    int flag = 0;
+    hip_check(hipMemcpy(&flag, device_error_flag(), sizeof(int), hipMemcpyDeviceToHost), "error flag");
+    if (flag) {
+      hip_check(hipMemset(device_error_flag(), 0, sizeof(int)), "clear error flag");
+      throw Error("Embedding index out of range");
+    }
+    last_run_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  }
+
+  std::string stats_json() const {
+    std::ostringstream s;
+    s << "{\"runs\":" << runs << ",\"compile_ms\":" << compile_ms << ",\"last_run_ms\":" << last_run_ms
+      << ",\"last_forward_gpu_ms\":" << last_gpu_ms << ",\"compiled_input_shape\":" << shape_str(in_shape)
+      << ",\"compiled_output_shape\":" << (output >= 0 ? shape_str(vals[output].shape) : "[]")
+      << ",\"arena_bytes\":" << arena_bytes << ",\"weight_bytes\":" << wbytes << ",\"ops\":" << ops.size()
+      << ",\"fused_epilogues\":" << fused_epilogues << ",\"zero_copy_concats\":" << zero_copy_concats
+      << ",\"current_memory_bytes\":" << (arena_bytes + wbytes) << ",\"peak_memory_bytes\":" << (arena_bytes + wbytes)
+      << "}";
+    return s.str();
+  }
+
+  std::string plan_json() const {
+    std::ostringstream s;
+    s << "{\"arena_bytes\":" << arena_bytes << ",\"input\":" << input << ",\"output\":" << output << ",\"ops\":[";
+    for (size_t i = 0; i < ops.size(); ++i) {
+      const Op &o = ops[i];
+      s << (i ? "," : "") << "{\"kind\":\"" << op_name(o.kind) << "\",\"name\":\"" << o.name << "\",\"act\":" << o.act
+        << ",\"resid\":" << o.resid << ",\"in\":[";
+      for (size_t j = 0; j < o.in.size(); ++j) s << (j ? "," : "") << o.in[j];
+      s << "],\"out\":[";
+      for (size_t j = 0; j < o.out.size(); ++j) s << (j ? "," : "") << o.out[j];
+      s << "]}";
+    }
+    s << "],\"values\":[";
+    for (size_t v = 0; v < vals.size(); ++v) {
+      const Val &x = vals[v];
+      s << (v ? "," : "") << "{\"shape\":" << shape_str(x.shape) << ",\"dtype\":" << x.dt << ",\"bytes\":" << x.bytes()
+        << ",\"offset\":" << x.offset << ",\"alias_of\":" << x.alias_of << ",\"def\":" << vals[root(int(v))].def
+        << ",\"last\":" << vals[root(int(v))].last << ",\"layout\":" << x.layout << "}";
+    }
+    s << "]}";
+    return s.str();
+  }
+};
+
+}  // namespace mh
+
+struct mh_engine {
+  mh::EngineImpl impl;
+};
+
+using mh::Error;
+
+#define ENG_TRY(...)                   \
+  try {                                \
+    __VA_ARGS__;                       \
+    return 0;                          \
+  } catch (const std::exception &e) {  \
+    mh::set_last_error(e.what());      \
+    return 1;                          \
+  }
+
+static void put_str(const std::string &s, char *buf, size_t len) {
+  if (!buf || !len) throw Error("null buffer");
+  if (s.size() + 1 > len) throw Error("buffer too small: need " + std::to_string(s.size() + 1));
+  std::memcpy(buf, s.c_str(), s.size() + 1);
+}
+
+extern "C" {
+
+int mh_engine_create(mh_engine **e, const char *config_json, int device) {
+  ENG_TRY({
+    if (!e || !config_json) throw Error("null argument");
+    auto eng = std::make_unique<mh_engine>();
+    eng->impl.cfg = mh::json::parse(config_json);
+    const std::string dts = eng->impl.cfg.get_str("dtype", "float32");
+    if (dts == "float32") eng->impl.dt = mh::F32;
+    else if (dts == "float16") eng->impl.dt = mh::F16;
+    else if (dts == "bfloat16") eng->impl.dt = mh::BF16;
+    else throw Error("unsupported dtype '" + dts + "'");
+    eng->impl.device = device;
+    eng->impl.plan_only = device < 0;
+    *e = eng.release();
+  })
+}
+
+int mh_engine_destroy(mh_engine *e) { ENG_TRY(delete e) }
+
+int mh_engine_set_param(mh_engine *e, const char *name, const void *data, size_t bytes, int dtype) {
+  ENG_TRY({
+    if (!e || !name || (!data && bytes)) throw Error("null argument");
+    if (e->impl.compiled) throw Error("parameters must be set before compile");
+    mh::Param p;
+    p.dt = dtype;
+    p.host.assign(static_cast<const uint8_t *>(data), static_cast<const uint8_t *>(data) + bytes);
+    e->impl.params[name] = std::move(p);
+  })
+}
+
+int mh_engine_compile(mh_engine *e, const int *shape, int ndim) {
+  ENG_TRY({
+    if (!e || !shape || ndim <= 0) throw Error("bad input shape");
+    e->impl.compile(mh::Shape(shape, shape + ndim));
+  })
+}
+
+int mh_engine_input_ptr(mh_engine *e, void **p) {
+  ENG_TRY({
+    e->impl.require_device();
+    *p = e->impl.dptr(e->impl.input);
+  })
+}
+
+int mh_engine_output_ptr(mh_engine *e, void **p) {
+  ENG_TRY({
+    e->impl.require_device();
+    *p = e->impl.dptr(e->impl.output);
+  })
+}
+
+int mh_engine_output_shape(mh_engine *e, int *shape, int *ndim) {
+  ENG_TRY({
+    if (!e->impl.compiled) throw Error("engine is not compiled");
+    const auto &s = e->impl.vals[e->impl.output].shape;
+    *ndim = int(s.size());
+    for (size_t i = 0; i < s.size(); ++i) shape[i] = s[i];
+  })
+}
+
+int mh_engine_run(mh_engine *e, const void *in, void *out) { ENG_TRY(e->impl.run(in, out)) }
+int mh_engine_run_device(mh_engine *e) { ENG_TRY(e->impl.run_device()) }
+int mh_engine_launch(mh_engine *e) { ENG_TRY(e->impl.launch()) }
+int mh_engine_stream(mh_engine *e, void **s) {
+  ENG_TRY({
+    e->impl.require_device();
+    *s = e->impl.stream;
+  })
+}
+int mh_engine_stats(mh_engine *e, char *buf, size_t len) { ENG_TRY(put_str(e->impl.stats_json(), buf, len)) }
+int mh_engine_plan(mh_engine *e, char *buf, size_t len) { ENG_TRY(put_str(e->impl.plan_json(), buf, len)) }
+
+}  // extern "C"

@@ -35,6 +35,7 @@ namespace {
 
 constexpr int kThreads = 256;
 
+
 template <int DT> struct Mfma;
 template <> struct Mfma<BF16> {
   static constexpr int kElems = 8;  // elements per 16-byte chunk
@@ -115,7 +116,7 @@ __device__ __forceinline__ void epi_store4(const EpiArgs &ep, int m, int n, int 
     const int which = n / ep.E, e = n - which * ep.E;
     const int h = e / ep.hd, dd = e - h * ep.hd;
     const int b = m / ep.T, t = m - b * ep.T;
-    out = static_cast<T *>(ep.outs[which]);
+    out = static_cast<T *>(which == 0 ? ep.outs[0] : which == 1 ? ep.outs[1] : ep.outs[2]);
     idx = ((long(b) * ep.H + h) * ep.T + t) * ep.hd + dd;
   } else if (ep.mode == EPI_CONVT) {
     // column n = (kh*k + kw)*oC + oc of input pixel m = (b, ih, iw) lands on
@@ -151,6 +152,20 @@ __device__ __forceinline__ void epi_store4(const EpiArgs &ep, int m, int n, int 
     for (int i = 0; i < 4; ++i)
       if (n + i < N) out[idx + i] = S::enc(v[i]);
   }
+}
+
+// Chunk at the K tail: values at or beyond K read as zero.
+template <int DT, bool VEC>
+__device__ __forceinline__ uint4 load_tail(const typename Store<DT>::T *__restrict__ src, int k, int K) {
+  typedef typename Store<DT>::T T;
+  constexpr int E = Mfma<DT>::kElems;
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (VEC && k + E <= K) return *reinterpret_cast<const uint4 *>(src);
+  T tmp[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) tmp[e] = (k + e < K) ? src[e] : T(0);
+  __builtin_memcpy(&v, tmp, 16);
+  return v;
 }
 
 // im2col chunk from an NHWC activation: GEMM row m = output pixel
@@ -226,46 +241,63 @@ gemm_nt_kernel(const typename Store<DT>::T *__restrict__ A, const typename Store
   const int wm = wave / WGN, wn = wave % WGN;
 
   uint4 ra[ACH], rb[BCH];
+  // Per-thread source rows are fixed for the whole K loop.  Rows past M / N
+  // are clamped to the last valid row: they only feed output rows/columns
+  // that are never stored, so no per-load branch is needed.
+  const typename Store<DT>::T *arow[CONV ? 1 : ACH];
+  const typename Store<DT>::T *brow[BCH];
   long pixbase[CONV ? ACH : 1];
   int ih0[CONV ? ACH : 1], iw0[CONV ? ACH : 1];
-  if (CONV) {
+  bool rowok[CONV ? ACH : 1];
+  const int cidx = (tid & 7) * E;  // column of this thread's chunk in a slab
 #pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const int m = m0 + ((tid + i * kThreads) >> 3);
+  for (int i = 0; i < ACH; ++i) {
+    const int m = m0 + ((tid + i * kThreads) >> 3);
+    if (CONV) {
       const int ow = m % cv.oW, t2 = m / cv.oW, oh = t2 % cv.oH, b = t2 / cv.oH;
       pixbase[i] = long(b) * cv.iH * cv.iW;
       ih0[i] = oh * cv.s - cv.p;
       iw0[i] = ow * cv.s - cv.p;
+      rowok[i] = m < M;
+    } else {
+      arow[i] = A + long(min(m, M - 1)) * lda + cidx;
     }
   }
-  auto gload = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const int id = tid + i * kThreads, r = id >> 3, c = id & 7;
-      if (CONV)
-        ra[i] = load_im2col<DT, VEC>(A, cv, m0 + r < M, pixbase[i], ih0[i], iw0[i], k0 + c * E, K);
-      else
-        ra[i] = load_chunk<DT, VEC>(A, lda, m0 + r, M, k0 + c * E, K);
-    }
-#pragma unroll
-    for (int i = 0; i < BCH; ++i) {
-      const int id = tid + i * kThreads, r = id >> 3, c = id & 7;
-      rb[i] = load_chunk<DT, VEC>(Bt, ldb, n0 + r, N, k0 + c * E, K);
-    }
-  };
-  auto sstore = [&](int buf) {
-    uint4 *as = As + buf * BM * 8, *bs = Bs + buf * BN * 8;
-#pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const int id = tid + i * kThreads, r = id >> 3, c = id & 7;
-      as[r * 8 + (c ^ (r & 7))] = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < BCH; ++i) {
-      const int id = tid + i * kThreads, r = id >> 3, c = id & 7;
-      bs[r * 8 + (c ^ (r & 7))] = rb[i];
-    }
-  };
+  for (int i = 0; i < BCH; ++i) {
+    const int n = n0 + ((tid + i * kThreads) >> 3);
+    brow[i] = Bt + long(min(n, N - 1)) * ldb + cidx;
+  }
+
+#define MH_GLOAD(k0)                                                                                   \
+  {                                                                                                    \
+    const bool kfull = VEC && ((k0) + BK <= K);                                                        \
+    if (kfull) {                                                                                       \
+      _Pragma("unroll") for (int i = 0; i < ACH; ++i) {                                                \
+        if (CONV) ra[i] = load_im2col<DT, true>(A, cv, rowok[i], pixbase[i], ih0[i], iw0[i], (k0) + cidx, K); \
+        else ra[i] = *reinterpret_cast<const uint4 *>(arow[i] + (k0));                                 \
+      }                                                                                                \
+      _Pragma("unroll") for (int i = 0; i < BCH; ++i) rb[i] = *reinterpret_cast<const uint4 *>(brow[i] + (k0)); \
+    } else {                                                                                           \
+      _Pragma("unroll") for (int i = 0; i < ACH; ++i) {                                                \
+        if (CONV) ra[i] = load_im2col<DT, VEC>(A, cv, rowok[i], pixbase[i], ih0[i], iw0[i], (k0) + cidx, K); \
+        else ra[i] = load_tail<DT, VEC>(arow[i] + (k0), (k0) + cidx, K);                               \
+      }                                                                                                \
+      _Pragma("unroll") for (int i = 0; i < BCH; ++i) rb[i] = load_tail<DT, VEC>(brow[i] + (k0), (k0) + cidx, K); \
+    }                                                                                                  \
+  }
+#define MH_SSTORE(buf)                                                                                 \
+  {                                                                                                    \
+    uint4 *as_ = As + (buf) * BM * 8, *bs_ = Bs + (buf) * BN * 8;                                      \
+    _Pragma("unroll") for (int i = 0; i < ACH; ++i) {                                                  \
+      const int id = tid + i * kThreads, r = id >> 3, c = id & 7;                                      \
+      as_[r * 8 + (c ^ (r & 7))] = ra[i];                                                              \
+    }                                                                                                  \
+    _Pragma("unroll") for (int i = 0; i < BCH; ++i) {                                                  \
+      const int id = tid + i * kThreads, r = id >> 3, c = id & 7;                                      \
+      bs_[r * 8 + (c ^ (r & 7))] = rb[i];                                                              \
+    }                                                                                                  \
+  }
 
   f32x4 acc[FM][FN];
 #pragma unroll
@@ -274,14 +306,14 @@ gemm_nt_kernel(const typename Store<DT>::T *__restrict__ A, const typename Store
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int KT = (K + BK - 1) / BK;
-  gload(0);
-  sstore(0);
+  MH_GLOAD(0);
+  MH_SSTORE(0);
   __syncthreads();
 
   const int lrow = lane & 15, lgrp = lane >> 4;
   for (int kt = 0; kt < KT; ++kt) {
     const int buf = kt & 1;
-    if (kt + 1 < KT) gload((kt + 1) * BK);
+    if (kt + 1 < KT) MH_GLOAD((kt + 1) * BK);
     const uint4 *as = As + buf * BM * 8, *bs = Bs + buf * BN * 8;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -302,24 +334,51 @@ gemm_nt_kernel(const typename Store<DT>::T *__restrict__ A, const typename Store
 #pragma unroll
         for (int j = 0; j < FN; ++j) Mfma<DT>::step(acc[i][j], bf[j], af[i]);
     }
-    if (kt + 1 < KT) sstore(buf ^ 1);
+    if (kt + 1 < KT) MH_SSTORE(buf ^ 1);
     __syncthreads();
   }
+#undef MH_GLOAD
+#undef MH_SSTORE
 
-  // ---- epilogue: lane holds C[m][n..n+3] ----
+  // ---- epilogue ----
+  // Each wave stages its accumulators through its own slice of the (now
+  // idle) LDS in PASSES row bands, then streams the band back row by row:
+  // 4 consecutive columns per lane, consecutive lanes on consecutive columns,
+  // so the global stores are full contiguous row segments.  The fragment
+  // writes use only compile-time accumulator indices (keeps the accumulators
+  // in registers) and the epilogue body exists once (rolled loop).
+  constexpr int LDS_BYTES = 2 * (BM + BN) * 8 * 16;
+  constexpr int RSTRIDE = WTN + 4;  // floats per staged row (+16 B pad)
+  constexpr int PASSES = (4 * WTM * RSTRIDE * 4 <= LDS_BYTES) ? 1 : (4 * (WTM / 2) * RSTRIDE * 4 <= LDS_BYTES) ? 2 : 4;
+  constexpr int FMP = FM / PASSES;
+  static_assert(FM % PASSES == 0, "epilogue passes");
+  float *stage = reinterpret_cast<float *>(smem) + wave * (FMP * 16) * RSTRIDE;
   EpiArgs e2 = ep;
   if (ep.mode == EPI_ROWMAJOR) e2.out = static_cast<T *>(ep.out) + z * sc;
+  constexpr int LPR = WTN / 4;        // lanes per staged row
+  constexpr int RPI = 64 / LPR;       // rows per wave iteration
+  const int rl = lane / LPR, cl = (lane % LPR) * 4;
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int m = m0 + wm * WTM + i * 16 + lrow;
-    if (m >= M) continue;
+  for (int p = 0; p < PASSES; ++p) {
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int n = n0 + wn * WTN + j * 16 + lgrp * 4;
-      if (n >= N) continue;
-      float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-      epi_store4<DT>(e2, m, n, N, v);
+    for (int i = 0; i < FMP; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        *reinterpret_cast<f32x4 *>(stage + (i * 16 + lrow) * RSTRIDE + j * 16 + lgrp * 4) = acc[p * FMP + i][j];
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): own writes visible to own reads
+    __builtin_amdgcn_wave_barrier();
+    const int mbase = m0 + wm * WTM + p * FMP * 16;
+    const int n = n0 + wn * WTN + cl;
+    for (int r = rl; r < FMP * 16; r += RPI) {
+      const int m = mbase + r;
+      if (m < M && n < N) {
+        const f32x4 a = *reinterpret_cast<const f32x4 *>(stage + r * RSTRIDE + cl);
+        float v[4] = {a[0], a[1], a[2], a[3]};
+        epi_store4<DT>(e2, m, n, N, v);
+      }
     }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -328,7 +387,13 @@ void launch_one(dim3 grid, size_t lds, hipStream_t st, const void *A, const void
                 long ldb, long sa, long sb, long sc, const EpiArgs &ep, const ConvArgs &cv) {
   typedef typename Store<DT>::T T;
   auto kfn = gemm_nt_kernel<DT, BM, BN, WGM, WGN, VEC, CONV>;
-  if (lds > 65536) (void)hipFuncSetAttribute((const void *)kfn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+  // Raise the dynamic-LDS limit once per instantiation (first launch happens
+  // outside stream capture: engines run one eager forward before capturing).
+  static bool lds_attr_set = false;
+  if (lds > 65536 && !lds_attr_set) {
+    (void)hipFuncSetAttribute((const void *)kfn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    lds_attr_set = true;
+  }
   hipLaunchKernelGGL(kfn, grid, dim3(kThreads), lds, st, (const T *)A, (const T *)Bt, M, N, K, lda, ldb, sa, sb, sc,
                      ep, cv);
 }
@@ -344,12 +409,22 @@ hipError_t launch_cfg(const void *A, const void *Bt, int M, int N, int K, long l
   else vec = vec && (lda % E == 0) && (sa % E == 0);
   dim3 grid(tiles, 1, batch);
   const ConvArgs none{};
+  // Instantiated variants: the aligned (VEC) path for every tile; the
+  // unaligned path only for the 64x64 tile (host falls back to it); the conv
+  // loader for tiles up to 256x128.
+  constexpr bool kSmall = (BM == 64 && BN == 64);
   if (cv) {
-    if (vec) launch_one<DT, BM, BN, WGM, WGN, true, true>(grid, lds, st, A, Bt, M, N, K, lda, ldb, sa, sb, sc, ep, *cv);
-    else launch_one<DT, BM, BN, WGM, WGN, false, true>(grid, lds, st, A, Bt, M, N, K, lda, ldb, sa, sb, sc, ep, *cv);
+    if constexpr (BM * BN <= 256 * 128) {
+      if (vec) launch_one<DT, BM, BN, WGM, WGN, true, true>(grid, lds, st, A, Bt, M, N, K, lda, ldb, sa, sb, sc, ep, *cv);
+      else if constexpr (kSmall) launch_one<DT, BM, BN, WGM, WGN, false, true>(grid, lds, st, A, Bt, M, N, K, lda, ldb, sa, sb, sc, ep, *cv);
+      else return hipErrorInvalidValue;
+    } else {
+      return hipErrorInvalidValue;
+    }
   } else {
     if (vec) launch_one<DT, BM, BN, WGM, WGN, true, false>(grid, lds, st, A, Bt, M, N, K, lda, ldb, sa, sb, sc, ep, none);
-    else launch_one<DT, BM, BN, WGM, WGN, false, false>(grid, lds, st, A, Bt, M, N, K, lda, ldb, sa, sb, sc, ep, none);
+    else if constexpr (kSmall) launch_one<DT, BM, BN, WGM, WGN, false, false>(grid, lds, st, A, Bt, M, N, K, lda, ldb, sa, sb, sc, ep, none);
+    else return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
@@ -375,6 +450,12 @@ hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long ld
       if (t < best_t * 0.999) { best_t = t; best = c; }
     }
   }
+  constexpr int E = Mfma<DT>::kElems;
+  bool vec = (ldb % E == 0) && (sb % E == 0) && ((uintptr_t)A % 16 == 0) && ((uintptr_t)Bt % 16 == 0);
+  if (cv) vec = vec && (cv->iC % E == 0) && (cv->ldx % E == 0);
+  else vec = vec && (lda % E == 0) && (sa % E == 0);
+  if (!vec) best = 4;
+  if ((cv || DT == F32) && best == 0) best = 1;  // 256x256 only for 16-bit plain GEMMs
   switch (best) {
   case 0: return launch_cfg<DT, 256, 256, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, cv, st);
   case 1: return launch_cfg<DT, 256, 128, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, cv, st);

@@ -15,9 +15,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-namespace mh {
+#include "mh_kernels.hpp"
 
-enum DType : int { F32 = 0, F16 = 1, BF16 = 2, I32 = 3 };
+namespace mh {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -119,6 +119,6 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-inline size_t dtype_size(int dt) { return (dt == F16 || dt == BF16) ? 2 : 4; }
+inline size_t dtype_size(int dt) { return dt_size(dt); }
 
 }  // namespace mh

@@ -9,6 +9,9 @@
 
 namespace mh {
 
+// Storage dtype codes (MuNet DataType order, reference src/types.hpp:16).
+enum DType : int { F32 = 0, F16 = 1, BF16 = 2, I32 = 3 };
+
 enum Act : int { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU = 2 };
 enum EpiMode : int { EPI_ROWMAJOR = 0, EPI_HEADSPLIT = 1, EPI_CONVT = 2 };
 enum BinOp : int { BIN_ADD = 0, BIN_SUB = 1, BIN_MUL = 2, BIN_DIV = 3 };

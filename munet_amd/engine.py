@@ -1,0 +1,123 @@
+"""Engine: the compiled HIP executor behind MuNet's inference::Engine contract.
+
+Mirrors ``inference::Engine`` (reference src/inference.hpp:292-801):
+
+* ``Engine.load(config, params)`` - module config in the reference's
+  serialized schema (src/inference_serialization.cpp:762-860) and parameters
+  by ``named_parameters`` name (src/core/module.hpp:95-107);
+* ``compile(example_input)`` - exact shape contract; traces, fuses, plans the
+  arena and captures the forward as a hipGraph (src/inference.hpp:446-537);
+* ``run(x)`` - host input in storage format -> host output
+  (src/inference.hpp:541-610); ``run_device()`` forwards on the resident
+  input buffer (used by the benchmark, inputs already in HBM);
+* ``stats()`` - EngineStats fields (src/inference.hpp:43-66) plus the
+  executor's own (arena bytes, fused epilogues, ops).
+
+All compute runs in libmunet_hip.so; there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+
+import numpy as np
+
+from . import _lib, synth
+
+_vp = ctypes.c_void_p
+
+
+class Engine:
+    def __init__(self, device: int = 0):
+        self.device = device
+        self._h = None
+        self.config = None
+        self.out_shape = None
+        self.in_shape = None
+
+    # -- load ---------------------------------------------------------------
+    def load(self, config: dict, params: dict):
+        lib = _lib.load()
+        h = _vp()
+        _lib.call("mh_engine_create", ctypes.byref(h), json.dumps(config).encode(), self.device)
+        self._h = h
+        self.config = config
+        dt = synth.DTYPE_CODES[config.get("dtype", "float32")]
+        for name, arr in params.items():
+            a = np.ascontiguousarray(arr)
+            _lib.call("mh_engine_set_param", h, name.encode(), a.ctypes.data_as(_vp), a.nbytes, dt)
+        del lib
+        return self
+
+    # -- compile ------------------------------------------------------------
+    def compile(self, example_input_shape):
+        shape = [int(s) for s in example_input_shape]
+        _lib.call("mh_engine_compile", self._h, _lib.ints(shape), len(shape))
+        self.in_shape = tuple(shape)
+        dims = (ctypes.c_int * 8)()
+        nd = ctypes.c_int()
+        _lib.call("mh_engine_output_shape", self._h, dims, ctypes.byref(nd))
+        self.out_shape = tuple(dims[i] for i in range(nd.value))
+        return self
+
+    # -- run ----------------------------------------------------------------
+    def _out_dtype(self):
+        return synth.storage_dtype(synth.DTYPE_CODES[self.config.get("dtype", "float32")])
+
+    def run(self, x: np.ndarray) -> np.ndarray:
+        if tuple(x.shape) != self.in_shape:
+            raise ValueError(f"input shape {tuple(x.shape)} does not match the compiled contract {self.in_shape}")
+        x = np.ascontiguousarray(x)
+        out = np.empty(self.out_shape, dtype=self._out_dtype())
+        _lib.call("mh_engine_run", self._h, x.ctypes.data_as(_vp), out.ctypes.data_as(_vp))
+        return out
+
+    def run_device(self):
+        _lib.call("mh_engine_run_device", self._h)
+
+    def launch(self):
+        _lib.call("mh_engine_launch", self._h)
+
+    def stream(self) -> int:
+        s = _vp()
+        _lib.call("mh_engine_stream", self._h, ctypes.byref(s))
+        return s.value or 0
+
+    def input_ptr(self) -> int:
+        p = _vp()
+        _lib.call("mh_engine_input_ptr", self._h, ctypes.byref(p))
+        return p.value
+
+    def output_ptr(self) -> int:
+        p = _vp()
+        _lib.call("mh_engine_output_ptr", self._h, ctypes.byref(p))
+        return p.value
+
+    # -- introspection --------------------------------------------------------
+    def _json(self, fn, size=1 << 16):
+        while True:
+            buf = ctypes.create_string_buffer(size)
+            try:
+                _lib.call(fn, self._h, buf, size)
+                return json.loads(buf.value.decode())
+            except _lib.HipError as e:
+                if "buffer too small" not in str(e):
+                    raise
+                size *= 4
+
+    def stats(self) -> dict:
+        return self._json("mh_engine_stats")
+
+    def plan(self) -> dict:
+        return self._json("mh_engine_plan", 1 << 20)
+
+    def close(self):
+        if self._h is not None:
+            _lib.call("mh_engine_destroy", self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

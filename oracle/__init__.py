@@ -70,6 +70,11 @@ class CpuOracle:
             msg = getattr(self.lib, self.pre + "last_error")()
             raise OracleError(f"{self.which}.{name}: {msg.decode() if msg else rc}")
 
+    def threads(self):
+        """Threads the restatement's parallel loops use (hardware_concurrency)."""
+        fn = getattr(self.lib, "orc_threads", None)
+        return int(fn()) if fn else 1
+
     @staticmethod
     def _c(a, dt):
         return np.ascontiguousarray(a, dtype=storage_np(dt))

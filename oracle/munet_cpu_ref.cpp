@@ -537,6 +537,9 @@ extern "C" {
 
 const char *orc_last_error() { return g_err.c_str(); }
 
+// Threads the restatement's parallel loops use (std::thread::hardware_concurrency).
+int orc_threads() { return int(std::max(1u, std::thread::hardware_concurrency())); }
+
 int orc_encode(int dt, const float *src, void *dst, size_t n) {
   ORC_GUARD(for (size_t i = 0; i < n; ++i) wr(dst, dt, i, double(src[i])))
 }

@@ -12,11 +12,26 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs through libmunet_hip.so)")
 
 
+def _gpu_count():
+    import ctypes
+    from munet_amd import _lib
+    n = ctypes.c_int(0)
+    try:
+        _lib.call("mh_device_count", ctypes.byref(n))
+    except Exception:
+        return 0
+    return n.value
+
+
 @pytest.fixture(scope="session")
 def hip():
+    n = _gpu_count()
+    if n == 0:
+        pytest.skip("no GPU visible to the HIP runtime")
     import torch
-    if not torch.cuda.is_available():
-        pytest.skip("no GPU")
+    assert torch.cuda.is_available(), (
+        f"HIP sees {n} device(s) but torch does not "
+        f"(torch device count {torch._C._cuda_getDeviceCount()})")
     from munet_amd.backend import HipBackend
     return HipBackend(0)
 

@@ -1,0 +1,100 @@
+"""Compile-time passes of the engine on a plan-only engine (no GPU):
+fusion decisions, liveness-planned arena, zero-copy concat."""
+import json
+
+import numpy as np
+import pytest
+
+from munet_amd import _lib, models, synth
+from munet_amd.engine import Engine
+
+
+def _zero_params(cfg):
+    dt = synth.DTYPE_CODES[cfg.get("dtype", "float32")]
+    return {n: np.zeros(s, dtype=synth.storage_dtype(dt)) for n, s, _r, _i in models.param_specs(cfg)}
+
+
+def _plan(cfg, in_shape):
+    e = Engine(device=-1).load(cfg, _zero_params(cfg)).compile(in_shape)
+    return e, e.plan()
+
+
+def _check_arena(plan):
+    vals = plan["values"]
+    roots = [v for v in vals if v["alias_of"] < 0 and v["offset"] >= 0]
+    for i, a in enumerate(roots):
+        for b in roots[i + 1:]:
+            live = not (a["last"] < b["def"] or b["last"] < a["def"])
+            if live:
+                sep = a["offset"] + a["bytes"] <= b["offset"] or b["offset"] + b["bytes"] <= a["offset"]
+                assert sep, f"live values overlap in the arena: {a} {b}"
+    assert plan["arena_bytes"] >= max(v["offset"] + v["bytes"] for v in roots)
+    return sum(v["bytes"] for v in roots)
+
+
+def test_mlp_plan_fuses_relu():
+    cfg = models.mlp_config()
+    e, p = _plan(cfg, (64, 784))
+    kinds = [o["kind"] for o in p["ops"]]
+    assert kinds == ["gemm", "gemm", "gemm"]
+    assert [o["act"] for o in p["ops"]] == [1, 1, 0]
+    _check_arena(p)
+    assert e.out_shape == (64, 10)
+
+
+def test_decoder_plan_structure_and_reuse():
+    cfg = models.decoder_config(vocab=1000, ctx=256, d_model=128, num_heads=2, num_layers=3, ffn=512)
+    e, p = _plan(cfg, (2, 256))
+    kinds = [o["kind"] for o in p["ops"]]
+    per_layer = ["layer_norm", "qkv_gemm", "attention", "gemm", "layer_norm", "gemm", "gemm"]
+    assert kinds == ["embedding_pos"] + per_layer * 3 + ["layer_norm", "gemm"]
+    st = e.stats()
+    assert st["fused_epilogues"] == 3 * 3  # out_proj+resid, ffn0+gelu, ffn2+resid per layer
+    total = _check_arena(p)
+    assert p["arena_bytes"] < total / 2  # liveness reuse
+    assert e.out_shape == (2, 256, 1000)
+
+
+def test_unet_zero_copy_concat():
+    cfg = models.unet_config(channels=(8, 16, 32), out_channels=2)
+    e, p = _plan(cfg, (2, 3, 32, 32))
+    assert e.stats()["zero_copy_concats"] == 2
+    assert not any(o["kind"] == "concat" for o in p["ops"])
+    assert [o["kind"] for o in p["ops"]].count("conv_transpose2d") == 2
+    _check_arena(p)
+    assert e.out_shape == (2, 2, 32, 32)
+
+
+def test_cnn_plan_layouts():
+    cfg = models.cnn_config()
+    e, p = _plan(cfg, (32, 3, 32, 32))
+    kinds = [o["kind"] for o in p["ops"]]
+    assert kinds[0] == "nchw_to_nhwc" and "nhwc_to_nchw" in kinds
+    assert kinds.count("conv2d") == 2 and kinds.count("max_pool2d") == 2
+    _check_arena(p)
+    assert e.out_shape == (32, 10)
+
+
+def test_full_gpt_plan_fits_and_reuses():
+    """BASELINE config 5 shape contract: the plan for the 12-layer decoder."""
+    cfg = models.decoder_config()
+    e, p = _plan(cfg, (4, 1024))
+    st = e.stats()
+    assert st["ops"] == 1 + 12 * 7 + 2
+    assert e.out_shape == (4, 1024, 32000)
+    _check_arena(p)
+    # logits (262 MB) + a few activations; far below one buffer per op
+    assert st["arena_bytes"] < 400 * 2 ** 20
+
+
+def test_engine_errors():
+    cfg = models.mlp_config()
+    params = _zero_params(cfg)
+    del params["0.weight"]
+    with pytest.raises(_lib.HipError, match="missing parameter '0.weight'"):
+        Engine(device=-1).load(cfg, params).compile((64, 784))
+    with pytest.raises(_lib.HipError, match="does not end in 784"):
+        Engine(device=-1).load(cfg, _zero_params(cfg)).compile((64, 783))
+    with pytest.raises(_lib.HipError, match="unsupported module type"):
+        bad = {"type": "Sequential", "dtype": "float32", "layers": [{"type": "LSTM"}]}
+        Engine(device=-1).load(bad, {}).compile((2, 3))
