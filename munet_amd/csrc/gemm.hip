@@ -28,38 +28,15 @@
 //     grouped along M so consecutive tiles share Bt panels in that XCD's L2.
 #include "mh_common.hpp"
 #include "mh_kernels.hpp"
+#include "gemm_common.hpp"
+
+#include <cstdlib>
 
 namespace mh {
 
 namespace {
 
-constexpr int kThreads = 256;
 
-
-template <int DT> struct Mfma;
-template <> struct Mfma<BF16> {
-  static constexpr int kElems = 8;  // elements per 16-byte chunk
-  static __device__ __forceinline__ void step(f32x4 &acc, uint4 a, uint4 b) {
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                  __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
-  }
-};
-template <> struct Mfma<F16> {
-  static constexpr int kElems = 8;
-  static __device__ __forceinline__ void step(f32x4 &acc, uint4 a, uint4 b) {
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                 __builtin_bit_cast(f16x8, b), acc, 0, 0, 0);
-  }
-};
-template <> struct Mfma<F32> {
-  static constexpr int kElems = 4;
-  static __device__ __forceinline__ void step(f32x4 &acc, uint4 a, uint4 b) {
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.x), __uint_as_float(b.x), acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.y), __uint_as_float(b.y), acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.z), __uint_as_float(b.z), acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.w), __uint_as_float(b.w), acc, 0, 0, 0);
-  }
-};
 
 // Load one 16-byte chunk (kElems values starting at column k of row `row`),
 // zero-filling whatever lies outside [0,rows) x [0,K).
@@ -76,82 +53,6 @@ __device__ __forceinline__ uint4 load_chunk(const typename Store<DT>::T *__restr
   for (int e = 0; e < E; ++e) tmp[e] = (k + e < K) ? src[e] : typename Store<DT>::T(0);
   __builtin_memcpy(&v, tmp, 16);
   return v;
-}
-
-template <int DT>
-__device__ __forceinline__ void epi_store4(const EpiArgs &ep, int m, int n, int N, float v[4]) {
-  typedef Store<DT> S;
-  typedef typename S::T T;
-  // reference rounding chain, one op at a time
-  if (ep.bias && ep.bias_first) {
-    // conv: the reference initialises the float accumulator with the bias and
-    // rounds once (src/core/ops/conv2d.cpp:51-72 fallback converts to fp32)
-    const T *b = static_cast<const T *>(ep.bias);
-    const int nb = ep.mode == EPI_CONVT ? ep.convt_oc : 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = S::round(v[i] + (n + i < N ? S::dec(b[(n + i) % nb]) : 0.0f));
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = S::round(v[i]);
-    if (ep.bias) {
-      const T *b = static_cast<const T *>(ep.bias);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = S::round(v[i] + (n + i < N ? S::dec(b[n + i]) : 0.0f));
-    }
-  }
-  if (ep.act == ACT_RELU) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = v[i] > 0.0f ? v[i] : 0.0f;
-  } else if (ep.act == ACT_GELU) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float t1 = S::round(v[i] * ep.gelu_c);
-      const float t2 = S::round(sigmoidf_ref(t1));
-      v[i] = S::round(v[i] * t2);
-    }
-  }
-  T *out;
-  long idx;
-  if (ep.mode == EPI_HEADSPLIT) {
-    const int which = n / ep.E, e = n - which * ep.E;
-    const int h = e / ep.hd, dd = e - h * ep.hd;
-    const int b = m / ep.T, t = m - b * ep.T;
-    out = static_cast<T *>(which == 0 ? ep.outs[0] : which == 1 ? ep.outs[1] : ep.outs[2]);
-    idx = ((long(b) * ep.H + h) * ep.T + t) * ep.hd + dd;
-  } else if (ep.mode == EPI_CONVT) {
-    // column n = (kh*k + kw)*oC + oc of input pixel m = (b, ih, iw) lands on
-    // output pixel (b, ih*k + kh, iw*k + kw) of an NHWC tensor (row stride ldc)
-    const int oc = n % ep.convt_oc, ph = n / ep.convt_oc;
-    const int kh = ph / ep.convt_k, kw = ph - kh * ep.convt_k;
-    const int iw = m % ep.convt_iw, rest = m / ep.convt_iw;
-    const int ih = rest % ep.convt_ih, b = rest / ep.convt_ih;
-    const long opix = (long(b) * ep.convt_ih * ep.convt_k + ih * ep.convt_k + kh) * (long(ep.convt_iw) * ep.convt_k) +
-                      iw * ep.convt_k + kw;
-    out = static_cast<T *>(ep.out);
-    idx = opix * ep.ldc + oc;
-  } else {
-    out = static_cast<T *>(ep.out);
-    idx = long(m) * ep.ldc + n;
-  }
-  if (ep.resid) {
-    const T *r = static_cast<const T *>(ep.resid) + long(m) * ep.ldr + n;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = S::round((n + i < N ? S::dec(r[i]) : 0.0f) + v[i]);
-  }
-  const bool full = (n + 4 <= N) && (((uintptr_t)(out + idx) & (sizeof(T) * 4 - 1)) == 0);
-  if (full) {
-    if (DT == F32) {
-      *reinterpret_cast<float4 *>(out + idx) = make_float4(v[0], v[1], v[2], v[3]);
-    } else {
-      u16x4 w;
-      w.x = S::enc(v[0]); w.y = S::enc(v[1]); w.z = S::enc(v[2]); w.w = S::enc(v[3]);
-      *reinterpret_cast<u16x4 *>(out + idx) = w;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (n + i < N) out[idx + i] = S::enc(v[i]);
-  }
 }
 
 // Chunk at the K tail: values at or beyond K read as zero.
@@ -203,7 +104,7 @@ __device__ __forceinline__ uint4 load_im2col(const typename Store<DT>::T *__rest
 }
 
 template <int DT, int BM, int BN, int WGM, int WGN, bool VEC, bool CONV>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(WGM * WGN * 64)
 gemm_nt_kernel(const typename Store<DT>::T *__restrict__ A, const typename Store<DT>::T *__restrict__ Bt,
                int M, int N, int K, long lda, long ldb, long sa, long sb, long sc, EpiArgs ep, ConvArgs cv) {
   typedef typename Store<DT>::T T;
@@ -211,8 +112,8 @@ gemm_nt_kernel(const typename Store<DT>::T *__restrict__ A, const typename Store
   constexpr int BK = 8 * E;  // 8 chunks of 16 bytes per row
   constexpr int WTM = BM / WGM, WTN = BN / WGN;
   constexpr int FM = WTM / 16, FN = WTN / 16;
+  constexpr int kThreads = WGM * WGN * 64;
   constexpr int ACH = BM * 8 / kThreads, BCH = BN * 8 / kThreads;
-  static_assert(WGM * WGN == 4, "4 waves");
   static_assert(ACH >= 1 && BCH >= 1, "tile too small");
 
   extern __shared__ uint4 smem[];
@@ -341,45 +242,10 @@ gemm_nt_kernel(const typename Store<DT>::T *__restrict__ A, const typename Store
 #undef MH_SSTORE
 
   // ---- epilogue ----
-  // Each wave stages its accumulators through its own slice of the (now
-  // idle) LDS in PASSES row bands, then streams the band back row by row:
-  // 4 consecutive columns per lane, consecutive lanes on consecutive columns,
-  // so the global stores are full contiguous row segments.  The fragment
-  // writes use only compile-time accumulator indices (keeps the accumulators
-  // in registers) and the epilogue body exists once (rolled loop).
-  constexpr int LDS_BYTES = 2 * (BM + BN) * 8 * 16;
-  constexpr int RSTRIDE = WTN + 4;  // floats per staged row (+16 B pad)
-  constexpr int PASSES = (4 * WTM * RSTRIDE * 4 <= LDS_BYTES) ? 1 : (4 * (WTM / 2) * RSTRIDE * 4 <= LDS_BYTES) ? 2 : 4;
-  constexpr int FMP = FM / PASSES;
-  static_assert(FM % PASSES == 0, "epilogue passes");
-  float *stage = reinterpret_cast<float *>(smem) + wave * (FMP * 16) * RSTRIDE;
   EpiArgs e2 = ep;
   if (ep.mode == EPI_ROWMAJOR) e2.out = static_cast<T *>(ep.out) + z * sc;
-  constexpr int LPR = WTN / 4;        // lanes per staged row
-  constexpr int RPI = 64 / LPR;       // rows per wave iteration
-  const int rl = lane / LPR, cl = (lane % LPR) * 4;
-#pragma unroll
-  for (int p = 0; p < PASSES; ++p) {
-#pragma unroll
-    for (int i = 0; i < FMP; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        *reinterpret_cast<f32x4 *>(stage + (i * 16 + lrow) * RSTRIDE + j * 16 + lgrp * 4) = acc[p * FMP + i][j];
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): own writes visible to own reads
-    __builtin_amdgcn_wave_barrier();
-    const int mbase = m0 + wm * WTM + p * FMP * 16;
-    const int n = n0 + wn * WTN + cl;
-    for (int r = rl; r < FMP * 16; r += RPI) {
-      const int m = mbase + r;
-      if (m < M && n < N) {
-        const f32x4 a = *reinterpret_cast<const f32x4 *>(stage + r * RSTRIDE + cl);
-        float v[4] = {a[0], a[1], a[2], a[3]};
-        epi_store4<DT>(e2, m, n, N, v);
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-  }
+  store_tile<DT, BM, BN, WTM, WTN, FM, FN, WGM * WGN>(acc, reinterpret_cast<float *>(smem), e2, m0 + wm * WTM,
+                                                     n0 + wn * WTN, M, N, wave, lane);
 }
 
 template <int DT, int BM, int BN, int WGM, int WGN, bool VEC, bool CONV>
@@ -394,7 +260,7 @@ void launch_one(dim3 grid, size_t lds, hipStream_t st, const void *A, const void
     (void)hipFuncSetAttribute((const void *)kfn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
     lds_attr_set = true;
   }
-  hipLaunchKernelGGL(kfn, grid, dim3(kThreads), lds, st, (const T *)A, (const T *)Bt, M, N, K, lda, ldb, sa, sb, sc,
+  hipLaunchKernelGGL(kfn, grid, dim3(WGM * WGN * 64), lds, st, (const T *)A, (const T *)Bt, M, N, K, lda, ldb, sa, sb, sc,
                      ep, cv);
 }
 
@@ -414,7 +280,7 @@ hipError_t launch_cfg(const void *A, const void *Bt, int M, int N, int K, long l
   // loader for tiles up to 256x128.
   constexpr bool kSmall = (BM == 64 && BN == 64);
   if (cv) {
-    if constexpr (BM * BN <= 256 * 128) {
+    if constexpr (BM * BN <= 256 * 128 && WGM * WGN == 4) {
       if (vec) launch_one<DT, BM, BN, WGM, WGN, true, true>(grid, lds, st, A, Bt, M, N, K, lda, ldb, sa, sb, sc, ep, *cv);
       else if constexpr (kSmall) launch_one<DT, BM, BN, WGM, WGN, false, true>(grid, lds, st, A, Bt, M, N, K, lda, ldb, sa, sb, sc, ep, *cv);
       else return hipErrorInvalidValue;
@@ -438,8 +304,12 @@ hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long ld
   const int kCU = 256;
   Cand cands[5] = {{256, 256, 4.0}, {256, 128, 2.0}, {128, 128, 1.0}, {128, 64, 0.55}, {64, 64, 0.3}};
   int best = 2;
-  if (tile_hint >= 0 && tile_hint < 5) {
+  if (tile_hint >= 0 && tile_hint < 8) {
     best = tile_hint;
+  } else if (DT != F32 && !cv && long((M + 255) / 256) * ((N + 255) / 256) * batch >= 1024) {
+    best = 7;  // 256x256, 8 waves: measured best for large GEMMs (LM head)
+  } else if (DT != F32 && !cv && long((M + 127) / 128) * ((N + 127) / 128) * batch >= 128) {
+    best = 2;  // 128x128, two blocks per CU: measured best for the layer GEMMs
   } else {
     double best_t = 1e30;
     for (int c = 0; c < 5; ++c) {
@@ -456,11 +326,21 @@ hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long ld
   else vec = vec && (lda % E == 0) && (sa % E == 0);
   if (!vec) best = 4;
   if ((cv || DT == F32) && best == 0) best = 1;  // 256x256 only for 16-bit plain GEMMs
+  if ((cv || DT == F32) && best >= 5) best = 2;  // 8-wave tiles only for 16-bit plain GEMMs
   switch (best) {
   case 0: return launch_cfg<DT, 256, 256, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, cv, st);
   case 1: return launch_cfg<DT, 256, 128, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, cv, st);
   case 2: return launch_cfg<DT, 128, 128, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, cv, st);
   case 3: return launch_cfg<DT, 128, 64, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, cv, st);
+  case 5:
+    if constexpr (DT != F32) return launch_cfg<DT, 256, 128, 4, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, cv, st);
+    return hipErrorInvalidValue;
+  case 6:
+    if constexpr (DT != F32) return launch_cfg<DT, 128, 256, 2, 4>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, cv, st);
+    return hipErrorInvalidValue;
+  case 7:
+    if constexpr (DT != F32) return launch_cfg<DT, 256, 256, 4, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, cv, st);
+    return hipErrorInvalidValue;
   default: return launch_cfg<DT, 64, 64, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, cv, st);
   }
 }
@@ -470,6 +350,18 @@ hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long ld
 hipError_t gemm_nt(int dt, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch,
                    long sa, long sb, long sc, const EpiArgs &ep, int tile_hint, hipStream_t st) {
   if (M <= 0 || N <= 0 || batch <= 0) return hipSuccess;
+  if (tile_hint < 0) {
+    // MUNET_HIP_GEMM_TILE forces a block tile (0-4 direct-to-LDS kernel,
+    // 100-104 register-staged kernel) for tests and tuning.
+    static const char *force = std::getenv("MUNET_HIP_GEMM_TILE");
+    if (force && *force) tile_hint = std::atoi(force);
+  }
+  // 0-6: the direct-to-LDS kernel (selected explicitly; measured no faster
+  // than the register-staged kernel on the decoder shapes), 100+: a
+  // register-staged tile, <0: automatic register-staged choice.
+  if (tile_hint >= 0 && tile_hint < 100 && gemm_dma_ok(dt, A, Bt, K, lda, ldb, sa, sb))
+    return gemm_dma(dt, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile_hint, st);
+  if (tile_hint >= 100) tile_hint -= 100;
   switch (dt) {
   case F32: return launch_dt<F32>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, nullptr, tile_hint, st);
   case F16: return launch_dt<F16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, nullptr, tile_hint, st);

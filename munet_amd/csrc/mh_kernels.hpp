@@ -73,6 +73,11 @@ struct StridedArgs {
 // picks the block tile automatically.
 hipError_t gemm_nt(int dt, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch,
                    long sa, long sb, long sc, const EpiArgs &ep, int tile_hint, hipStream_t st);
+// Direct-to-LDS pipeline for aligned 16-bit operands (K % 64 == 0);
+// tile: 0 256x256, 1 256x128, 2 128x256, 3 128x128, 4 128x64.
+bool gemm_dma_ok(int dt, const void *A, const void *Bt, int K, long lda, long ldb, long sa, long sb);
+hipError_t gemm_dma(int dt, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch, long sa,
+                    long sb, long sc, const EpiArgs &ep, int tile, hipStream_t st);
 hipError_t conv_nhwc(int dt, const void *x, const void *w_ohwi, const ConvArgs &cv, int oC, const EpiArgs &ep,
                      int tile_hint, hipStream_t st);
 
