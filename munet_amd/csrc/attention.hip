@@ -17,17 +17,25 @@
 //             when causal).
 //   ctx     = probs.matmul(v), merged back to [B, T, H*hd].
 //
-// Fast path (bf16/fp16, hd = 64): one workgroup of 4 wave64s owns QB query
-// rows of one (b,h) block; KV tiles of 64 columns are staged through LDS in
-// the MFMA operand layouts (K transposed to [j][d], V transposed to [d][j]);
-// S^T = K*Q^T and O^T = V^T*P^T on v_mfma_f32_16x16x32 so that every lane owns
-// one query row: the online-softmax max/sum need only two cross-lane shuffles
-// and P goes from the S accumulators into the PV operand without touching LDS.
-// Scores are rounded like the reference (round(matmul) then round(*scale)).
+// Three kernels, chosen per call:
+//  * flash_attn_tr_kernel (bf16/fp16, hd = 64, T % 8 == 0, power-of-two
+//    scale -- the scale is round(1/sqrt(64)) = 0.125 for every hd = 64 call):
+//    K and V tiles are copied to LDS in their natural layouts and the MFMA
+//    operands are read back transposed with ds_read_b64_tr_b16;
+//  * flash_attn_kernel (bf16/fp16, hd = 64, any T): transposes K and V while
+//    writing them to LDS, and applies both score roundings;
+//  * attn_generic_kernel (below).
+// Both flash kernels compute S^T = K*Q^T and O^T = V^T*P^T on
+// v_mfma_f32_16x16x32 so that every lane owns one query row: P goes from the
+// S accumulators into the PV operand without touching LDS.  Scores are
+// rounded like the reference (round(matmul), then round(*scale)).
 //
 // Generic path (any dtype / head size): one wave per query row, scores kept in
 // LDS, float max / double sum / per-j float accumulation as the reference's
 // fp32 CPU kernels do (src/backend/cpu_backend.hpp:334-374, 587-611).
+#include <cmath>
+#include <cstdlib>
+
 #include "mh_common.hpp"
 #include "mh_kernels.hpp"
 
@@ -45,6 +53,12 @@ template <> struct AttnMfma<BF16> {
                                                 0, 0);
   }
   static __device__ __forceinline__ uint16_t cvt(float v) { return f32_to_bf16(v); }
+  // two floats -> packed bf16 (hardware round-to-nearest-even)
+  static __device__ __forceinline__ uint32_t cvt2(float a, float b) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, b2));
+  }
 };
 template <> struct AttnMfma<F16> {
   static __device__ __forceinline__ void mma(f32x4 &c, uint4 a, uint4 b) {
@@ -55,7 +69,26 @@ template <> struct AttnMfma<F16> {
   static __device__ __forceinline__ uint16_t cvt(float v) {
     return __builtin_bit_cast(uint16_t, _Float16(v));
   }
+  static __device__ __forceinline__ uint32_t cvt2(float a, float b) {
+    return uint32_t(cvt(a)) | (uint32_t(cvt(b)) << 16);
+  }
 };
+
+// Round 4 floats through the storage dtype (MuNet's codecs; bf16 via the
+// packed hardware RNE conversion, identical for non-NaN values).
+template <int DT> __device__ __forceinline__ void round4(float v[4]);
+template <> __device__ __forceinline__ void round4<BF16>(float v[4]) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  const uint32_t p0 = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{v[0], v[1]}, b2));
+  const uint32_t p1 = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{v[2], v[3]}, b2));
+  v[0] = __uint_as_float(p0 << 16); v[1] = __uint_as_float(p0 & 0xffff0000u);
+  v[2] = __uint_as_float(p1 << 16); v[3] = __uint_as_float(p1 & 0xffff0000u);
+}
+template <> __device__ __forceinline__ void round4<F16>(float v[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = Store<F16>::round(v[i]);
+}
 
 // LDS tiles: 64 rows x 8 chunks of 16 bytes, chunk c of row r stored at
 // c ^ (r & 7).
@@ -253,6 +286,258 @@ flash_attn_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K
   }
 }
 
+// ---------------------------------------------------------------------------
+// Main path (bf16/fp16, hd = 64, T % 8 == 0, power-of-two scale).
+//
+// K and V tiles are staged in their natural layouts with 16-byte copies:
+//   K tile [d][j] : 64 rows of the [64, B*H*T] slab view, 64 columns each
+//   V tile [j][d] : 64 consecutive rows of the (b,h) block
+// and the MFMA operands, which need 8 consecutive d (for K) or j (for V) per
+// lane, are read with ds_read_b64_tr_b16.  Within each group of 16 lanes that
+// instruction returns to lane i, element e, the value (i & 3) of the 8 bytes
+// addressed by lane (i >> 2) + 4e, so a lane whose address names row
+// R + 4h + (s >> 2), columns 4(s & 3).. of a row-major tile hands every lane i
+// four consecutive rows of column i.
+// Rows are 128 bytes; chunk c of row r is stored at chunk c ^ 2((r & 3) ^
+// ((r >> SH) & 1)) (SH = 3 for K, 2 for V): the four rows one 16-lane group
+// reads and the rows of the neighbouring group land on disjoint banks.
+//
+// Scores: the reference rounds q.k to the dtype and multiplies by the [1]
+// scale tensor (rounded again); with a power-of-two scale that product is
+// exact, so s = round(q.k) and the softmax runs in the log2 domain
+// u = s * scale * log2(e).  The running max is only raised when it grows by
+// more than 2^8 (p stays <= 256, exact enough for bf16 P and fp32 sums); row
+// sums stay lane-partial until the end.
+typedef short v4s __attribute__((ext_vector_type(4)));
+
+template <int SH> __device__ __forceinline__ int tswz(int r, int c) {
+  return r * 8 + (c ^ (2 * ((r & 3) ^ ((r >> SH) & 1))));
+}
+
+__device__ __forceinline__ uint2 lds_tr(const uint8_t *p) {
+  const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s *)(p));
+  return __builtin_bit_cast(uint2, r);
+}
+
+template <int DT> __device__ __forceinline__ void round_scores(float v[4]) {
+  if (DT == BF16) {
+    round4<BF16>(v);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = Store<F16>::round(v[e]);
+  }
+}
+
+template <int DT, int RW>
+__global__ void __launch_bounds__(256)
+flash_attn_tr_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
+                     uint16_t *__restrict__ O, int B, int H, int T, int causal, float c2) {
+  constexpr int QB = 4 * 16 * RW;
+  constexpr float kRaise = 8.0f;  // log2 of the largest unnormalised p
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][KB * HD * 2];  // [buf][K|V][tile]
+
+  const int BH = B * H, nq = (T + QB - 1) / QB;
+  const int lvl = blockIdx.x / BH, bh = blockIdx.x - lvl * BH;
+  const int q0 = (causal ? nq - 1 - lvl : lvl) * QB;  // causal: longest rows first
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const long N = long(BH) * T;
+  const uint16_t *Kb = K + long(bh) * T;  // column offset into the [64, N] slab
+  const uint16_t *Vb = V + long(bh) * T * HD;
+  const int wrow0 = q0 + wave * 16 * RW;
+
+  // rows past T (ragged last block) read row T-1; their results are not stored
+  uint4 qf[RW][2];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int i = min(wrow0 + r * 16 + li, T - 1);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      qf[r][ks] = *reinterpret_cast<const uint4 *>(Q + (long(bh) * T + i) * HD + ks * 32 + lg * 8);
+  }
+  // o: lane holds O[i = li][d = dt*16 + 4*lg + e]; osum: the row sum of the
+  // (rounded) P fed to the MFMA, from a ones operand; mrow: running max (log2 units)
+  f32x4 o[RW][4], osum[RW];
+  float mrow[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    mrow[r] = -1e30f;
+    osum[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) o[r][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const uint32_t one2 = DT == BF16 ? 0x3F803F80u : 0x3C003C00u;
+  const uint4 ones = make_uint4(one2, one2, one2, one2);
+
+  // staging: rows r0 and r0 + 32 of each tile, chunk c0
+  const int r0 = tid >> 3, c0 = tid & 7;
+  const int st_k0 = tswz<3>(r0, c0) * 16, st_k1 = tswz<3>(r0 + 32, c0) * 16;
+  const int st_v0 = tswz<2>(r0, c0) * 16, st_v1 = tswz<2>(r0 + 32, c0) * 16;
+  // transposed reads: this lane addresses row base + (s >> 2), 8 bytes at
+  // column 4(s & 3) of a 16-column block; the row swizzle term is lane-fixed
+  const int s16 = lane & 15, sr = s16 >> 2, sx = ((s16 & 3) >> 1) ^ (2 * (sr ^ (lg & 1))), sh = (s16 & 1) * 8;
+  const int rd_k = (8 * lg + sr) * 128 + sh;  // + (32ks + 4h) rows, chunk (2jt ^ sx)
+  const int rd_v = (4 * lg + sr) * 128 + sh;  // + (32kk + 16h) rows, chunk (2dt ^ sx)
+
+  const int kv_end = causal ? min(T, q0 + QB) : T;
+  const int ntiles = (kv_end + KB - 1) / KB;
+  // loop-carried load pointers (advanced one tile per gload) keep the address
+  // registers live, so they are never recycled while a prefetch is in flight
+  const uint16_t *kp0 = Kb + long(r0) * N + c0 * 8, *kp1 = Kb + long(r0 + 32) * N + c0 * 8;
+  const uint16_t *vp0 = Vb + long(r0) * HD + c0 * 8, *vp1 = Vb + long(r0 + 32) * HD + c0 * 8;
+  uint4 kr[2], vr[2];
+  auto gload = [&](int j0) {
+    if (j0 + KB <= T) {  // whole tile in range (wave-uniform)
+      kr[0] = *reinterpret_cast<const uint4 *>(kp0);
+      kr[1] = *reinterpret_cast<const uint4 *>(kp1);
+      vr[0] = *reinterpret_cast<const uint4 *>(vp0);
+      vr[1] = *reinterpret_cast<const uint4 *>(vp1);
+    } else {  // ragged last tile: zero what lies past T
+      const bool kin = j0 + c0 * 8 < T;
+      kr[0] = kin ? *reinterpret_cast<const uint4 *>(kp0) : make_uint4(0, 0, 0, 0);
+      kr[1] = kin ? *reinterpret_cast<const uint4 *>(kp1) : make_uint4(0, 0, 0, 0);
+      vr[0] = (j0 + r0 < T) ? *reinterpret_cast<const uint4 *>(vp0) : make_uint4(0, 0, 0, 0);
+      vr[1] = (j0 + r0 + 32 < T) ? *reinterpret_cast<const uint4 *>(vp1) : make_uint4(0, 0, 0, 0);
+    }
+    kp0 += KB;
+    kp1 += KB;
+    vp0 += KB * HD;
+    vp1 += KB * HD;
+  };
+  auto sstore = [&](int buf) {
+    *reinterpret_cast<uint4 *>(&lds[buf][0][st_k0]) = kr[0];
+    *reinterpret_cast<uint4 *>(&lds[buf][0][st_k1]) = kr[1];
+    *reinterpret_cast<uint4 *>(&lds[buf][1][st_v0]) = vr[0];
+    *reinterpret_cast<uint4 *>(&lds[buf][1][st_v1]) = vr[1];
+  };
+  if (ntiles > 0) {
+    gload(0);
+    sstore(0);
+  }
+  __syncthreads();
+  // The Q fragments arrived with the first tile (in-order completion).  Re-
+  // defining them through an empty asm tells the wait-count insertion they
+  // are settled, so the MFMAs of every tile do not wait for the prefetch.
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      asm volatile("" : "+v"(qf[r][ks].x), "+v"(qf[r][ks].y), "+v"(qf[r][ks].z), "+v"(qf[r][ks].w)::"memory");
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int j0 = t * KB, buf = t & 1;
+    if (t + 1 < ntiles) gload(j0 + KB);
+
+    if (!(causal && j0 > wrow0 + 16 * RW - 1)) {  // skip tiles wholly above the diagonal
+      const uint8_t *kt = lds[buf][0], *vt = lds[buf][1];
+      // ---- S^T = K * Q^T : lane holds S[i = li][j = jt*16 + 4*lg + e] ----
+      uint4 kf[2][4];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+          const uint8_t *p = kt + rd_k + ((2 * jt) ^ sx) * 16 + ks * 32 * 128;
+          const uint2 lo = lds_tr(p), hi = lds_tr(p + 4 * 128);
+          kf[ks][jt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        }
+      f32x4 s[RW][4];
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+          s[r][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          AttnMfma<DT>::mma(s[r][jt], kf[0][jt], qf[r][0]);
+          AttnMfma<DT>::mma(s[r][jt], kf[1][jt], qf[r][1]);
+        }
+
+      uint4 pf[RW][2];
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        float v[16];
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+          float w[4] = {s[r][jt][0], s[r][jt][1], s[r][jt][2], s[r][jt][3]};
+          round_scores<DT>(w);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[jt * 4 + e] = w[e];
+        }
+        if (j0 + KB > T || (causal && j0 + KB - 1 > wrow0 + r * 16)) {  // boundary tile (wave-uniform)
+          // element (jt, e) is column j0 + 4lg + jt*16 + e: masked past T or above the diagonal
+          int lim = T - 1 - j0 - 4 * lg;
+          if (causal) lim = min(lim, wrow0 + r * 16 + li - j0 - 4 * lg);
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (jt * 16 + e > lim) v[jt * 4 + e] = -INFINITY;
+        }
+        float mx = v[0];
+#pragma unroll
+        for (int e = 1; e < 16; ++e) mx = fmaxf(mx, v[e]);
+        // raise the row max only when some lane's own max exceeds it by 2^kRaise
+        if (__any(mx * c2 > mrow[r] + kRaise)) {
+          mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+          const float mnew = fmaxf(mrow[r], mx * c2);
+          const float alpha = __builtin_amdgcn_exp2f(mrow[r] - mnew);
+          mrow[r] = mnew;
+          osum[r] *= alpha;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) o[r][d] *= alpha;
+        }
+        const float nm = -mrow[r];
+        uint32_t pk[8];
+#pragma unroll
+        for (int e = 0; e < 16; e += 2)
+          pk[e >> 1] = AttnMfma<DT>::cvt2(__builtin_amdgcn_exp2f(__builtin_fmaf(v[e], c2, nm)),
+                                          __builtin_amdgcn_exp2f(__builtin_fmaf(v[e + 1], c2, nm)));
+        // P^T operand for k-step kk: slots 0..3 <- j = 32kk + 4lg + e, slots 4..7 <- j = 32kk + 16 + 4lg + e
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) pf[r][kk] = make_uint4(pk[4 * kk], pk[4 * kk + 1], pk[4 * kk + 2], pk[4 * kk + 3]);
+      }
+
+      // ---- O^T += V^T * P^T : lane holds O[i = li][d = dt*16 + 4*lg + e] ----
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        uint4 vf[4];
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const uint8_t *p = vt + rd_v + ((2 * dt) ^ sx) * 16 + kk * 32 * 128;
+          const uint2 lo = lds_tr(p), hi = lds_tr(p + 16 * 128);
+          vf[dt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        }
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+          AttnMfma<DT>::mma(osum[r], ones, pf[r][kk]);
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) AttnMfma<DT>::mma(o[r][dt], vf[dt], pf[r][kk]);
+        }
+      }
+    }
+    if (t + 1 < ntiles) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  const int b = bh / H, h = bh - b * H;
+  const long E = long(H) * HD;
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int i = wrow0 + r * 16 + li;
+    if (i >= T) continue;
+    const float inv = 1.0f / osum[r][0];
+    uint16_t *dst = O + (long(b) * T + i) * E + long(h) * HD;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      u16x4 w;
+      w.x = Store<DT>::enc(o[r][dt][0] * inv);
+      w.y = Store<DT>::enc(o[r][dt][1] * inv);
+      w.z = Store<DT>::enc(o[r][dt][2] * inv);
+      w.w = Store<DT>::enc(o[r][dt][3] * inv);
+      *reinterpret_cast<u16x4 *>(dst + dt * 16 + lg * 4) = w;
+    }
+  }
+}
+
 // Generic attention: one wave per (query row, bh); scores in LDS.
 template <int DT>
 __global__ void __launch_bounds__(64)
@@ -295,11 +580,44 @@ attn_generic_kernel(const void *__restrict__ Qv, const void *__restrict__ Kv, co
 
 }  // namespace
 
+namespace {
+bool pow2(float x) {
+  int e;
+  return x > 0.f && std::frexp(x, &e) == 0.5f;
+}
+int tr_rows_env() {
+  // tuning override: 1 or 2 (16 or 32 query rows per wave)
+  const char *e = std::getenv("MUNET_HIP_ATTN_RW");
+  const int v = e ? std::atoi(e) : 0;
+  return (v == 1 || v == 2) ? v : 0;
+}
+}  // namespace
+
 hipError_t attention(int dt, const void *q, const void *k, const void *v, void *ctx, int B, int H, int T, int hd,
                      int causal, float scale, int force_generic, hipStream_t st) {
   if (B <= 0 || H <= 0 || T <= 0) return hipSuccess;
   const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)k % 16 == 0) && ((uintptr_t)v % 16 == 0) &&
                        ((uintptr_t)ctx % 8 == 0);
+  if (!force_generic && hd == HD && (dt == BF16 || dt == F16) && aligned && T % 8 == 0 && pow2(scale)) {
+    const int bh = B * H;
+    static const int forced = tr_rows_env();
+    // 16 query rows per wave: more resident waves hide the softmax latency
+    // better than the operand reuse of 32 rows per wave (measured on MI355X)
+    const int rw = forced ? forced : 1;
+    const int qb = 64 * rw;
+    const dim3 grid(unsigned(long((T + qb - 1) / qb) * bh));
+    const float c2 = scale * 1.4426950408889634f;
+    const uint16_t *Q = (const uint16_t *)q, *K = (const uint16_t *)k, *V = (const uint16_t *)v;
+    uint16_t *O = (uint16_t *)ctx;
+    if (dt == BF16) {
+      if (rw == 2) hipLaunchKernelGGL((flash_attn_tr_kernel<BF16, 2>), grid, dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2);
+      else hipLaunchKernelGGL((flash_attn_tr_kernel<BF16, 1>), grid, dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2);
+    } else {
+      if (rw == 2) hipLaunchKernelGGL((flash_attn_tr_kernel<F16, 2>), grid, dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2);
+      else hipLaunchKernelGGL((flash_attn_tr_kernel<F16, 1>), grid, dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2);
+    }
+    return hipGetLastError();
+  }
   if (!force_generic && hd == HD && (dt == BF16 || dt == F16) && aligned) {
     const int bh = B * H;
     // 128-row blocks when that still fills the chip, else 64-row blocks

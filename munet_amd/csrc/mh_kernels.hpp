@@ -81,6 +81,7 @@ hipError_t gemm_dma(int dt, const void *A, const void *Bt, int M, int N, int K, 
 hipError_t conv_nhwc(int dt, const void *x, const void *w_ohwi, const ConvArgs &cv, int oC, const EpiArgs &ep,
                      int tile_hint, hipStream_t st);
 
+// Fused attention core (q, k, v in the head-split [B*H, T, hd] layout).
 hipError_t attention(int dt, const void *q, const void *k, const void *v, void *ctx, int B, int H, int T, int hd,
                      int causal, float scale, int force_generic, hipStream_t st);
 

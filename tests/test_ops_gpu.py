@@ -93,11 +93,15 @@ def _mha_params(E, dt, seed):
 
 
 @pytest.mark.parametrize("dt", [F16, BF16, F32])
-@pytest.mark.parametrize("B,T,H,hd", [(2, 64, 2, 64), (1, 200, 3, 64), (2, 40, 2, 32), (1, 3, 2, 4)])
+@pytest.mark.parametrize("B,T,H,hd", [(2, 64, 2, 64), (1, 200, 3, 64), (64, 72, 4, 64), (1, 77, 2, 64),
+                                      (2, 40, 2, 32), (1, 3, 2, 4)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_attention_core(hip, orc, dt, B, T, H, hd, causal):
     """q/k/v projection (fused head split) + fused attention vs the reference
-    MHA core, including MuNet's K-reinterpretation."""
+    MHA core, including MuNet's K-reinterpretation.  hd = 64 with T % 8 == 0
+    runs the pre-transposed-operand kernel (T = 72 with 256 (b,h) blocks takes
+    its 32-rows-per-wave variant and a ragged last tile); T = 77 runs the
+    in-LDS-transpose kernel; the rest the generic kernel."""
     E = H * hd
     x = rand((B * T, E), dt, 20)
     p = _mha_params(E, dt, 30)
