@@ -24,7 +24,7 @@ LIB = os.path.join(HERE, "libmunet_hip.so")
 PLUGIN = os.path.join(HERE, "libmunet_backend_hip.so")
 ARCH = "gfx950"
 
-KERNEL_SOURCES = ["gemm.hip", "gemm_dma.hip", "attention.hip", "eltwise.hip", "norm.hip", "layout.hip"]
+KERNEL_SOURCES = ["gemm.hip", "gemm_pipe.hip", "gemm_dma.hip", "attention.hip", "eltwise.hip", "norm.hip", "layout.hip"]
 HOST_SOURCES = ["capi.cpp", "engine.cpp", "backend.cpp"]
 PLUGIN_SOURCES = ["plugin.cpp"]
 
@@ -47,10 +47,12 @@ def _flags():
     ]
 
 
-# Per-source code-generation options.  attention.hip: MFMA results in
-# ordinary VGPRs (the softmax reads every score accumulator with VALU ops;
-# accumulation registers would cost a copy per value).
-SOURCE_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Per-source code-generation options: MFMA results in ordinary VGPRs for the
+# attention kernels (the softmax reads every score accumulator with VALU ops;
+# accumulation registers would cost a copy per value) and the pipelined GEMM
+# (measured faster on MI355X).
+_VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+SOURCE_FLAGS = {"attention.hip": _VGPR_FORM, "gemm_pipe.hip": _VGPR_FORM}
 
 
 def _compile(src: str) -> str:

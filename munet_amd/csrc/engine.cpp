@@ -328,6 +328,8 @@ struct EngineImpl {
     if (s.size() != 3 || s[2] != E) throw Error(pfx + ": MultiHeadAttention expects [B,T,E]");
     const int B = s[0], T = s[1], hd = E / H;
     if (E % H) throw Error(pfx + ": embed_dim must be divisible by num_heads");
+    // the head-split epilogue stores 4 consecutive columns of one head
+    if (hd % 4) throw Error(pfx + ": head_dim must be a multiple of 4 on the HIP engine");
     // fused q/k/v projection: weights [E,3E] -> [3E,E], biases [3E]
     std::vector<uint8_t> wcat, bcat;
     for (const char *p : {"q_proj.", "k_proj.", "v_proj."}) {
@@ -467,6 +469,8 @@ struct EngineImpl {
     }
     for (int l = L - 2; l >= 0; --l) {
       const int c = ch[l];
+      // the transposed-conv epilogue stores 4 consecutive output channels
+      if (c % 4) throw Error(pfx + "up" + std::to_string(l) + ": channels must be a multiple of 4 on the HIP engine");
       const Shape xs = vals[x].shape;
       const int up = alias(cat[l], {xs[0], c, xs[2] * 2, xs[3] * 2}, 0, NHWC, 2 * c);
       Op &o = emit(OP_CONVT, pfx + "up" + std::to_string(l), {x}, {up});

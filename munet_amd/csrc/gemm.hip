@@ -242,10 +242,11 @@ gemm_nt_kernel(const typename Store<DT>::T *__restrict__ A, const typename Store
 #undef MH_SSTORE
 
   // ---- epilogue ----
-  EpiArgs e2 = ep;
-  if (ep.mode == EPI_ROWMAJOR) e2.out = static_cast<T *>(ep.out) + z * sc;
-  store_tile<DT, BM, BN, WTM, WTN, FM, FN, WGM * WGN>(acc, reinterpret_cast<float *>(smem), e2, m0 + wm * WTM,
-                                                     n0 + wn * WTN, M, N, wave, lane);
+  // the batch slice offset is passed separately: a modified copy of the
+  // epilogue arguments would live in private memory
+  store_tile<DT, BM, BN, WTM, WTN, FM, FN, WGM * WGN>(acc, reinterpret_cast<float *>(smem), ep, m0 + wm * WTM,
+                                                     n0 + wn * WTN, M, N, wave, lane,
+                                                     ep.mode == EPI_ROWMAJOR ? z * sc : 0);
 }
 
 template <int DT, int BM, int BN, int WGM, int WGN, bool VEC, bool CONV>
@@ -351,14 +352,17 @@ hipError_t gemm_nt(int dt, const void *A, const void *Bt, int M, int N, int K, l
                    long sa, long sb, long sc, const EpiArgs &ep, int tile_hint, hipStream_t st) {
   if (M <= 0 || N <= 0 || batch <= 0) return hipSuccess;
   if (tile_hint < 0) {
-    // MUNET_HIP_GEMM_TILE forces a block tile (0-4 direct-to-LDS kernel,
-    // 100-104 register-staged kernel) for tests and tuning.
+    // MUNET_HIP_GEMM_TILE forces a kernel and block tile for tests and tuning:
+    // 0-6 direct-to-LDS kernel, 100-107 general kernel, 200-202 pipelined kernel.
     static const char *force = std::getenv("MUNET_HIP_GEMM_TILE");
     if (force && *force) tile_hint = std::atoi(force);
   }
-  // 0-6: the direct-to-LDS kernel (selected explicitly; measured no faster
-  // than the register-staged kernel on the decoder shapes), 100+: a
-  // register-staged tile, <0: automatic register-staged choice.
+  // <0: the pipelined 16-bit kernel when the operands allow it, else the
+  // general kernel with an automatic tile.
+  const bool pipe = gemm_pipe_ok(dt, A, Bt, K, lda, ldb, sa, sb);
+  if (pipe && (tile_hint < 0 || tile_hint >= 200))
+    return gemm_pipe(dt, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile_hint < 0 ? -1 : tile_hint - 200, st);
+  if (tile_hint >= 200) tile_hint = -1;
   if (tile_hint >= 0 && tile_hint < 100 && gemm_dma_ok(dt, A, Bt, K, lda, ldb, sa, sb))
     return gemm_dma(dt, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile_hint, st);
   if (tile_hint >= 100) tile_hint -= 100;

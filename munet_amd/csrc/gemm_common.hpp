@@ -52,8 +52,9 @@ __device__ __forceinline__ uint2 round4_bf16(float v[4]) {
 }
 
 // Destination of output element (m, n) for the epilogue modes.
+// `off` is an element offset added to row-major outputs (the batch slice).
 template <typename T>
-__device__ __forceinline__ T *epi_dst(const EpiArgs &ep, int m, int n) {
+__device__ __forceinline__ T *epi_dst(const EpiArgs &ep, int m, int n, long off) {
   if (ep.mode == EPI_HEADSPLIT) {
     const int which = n / ep.E, e = n - which * ep.E;
     const int h = e / ep.hd, dd = e - h * ep.hd;
@@ -72,7 +73,7 @@ __device__ __forceinline__ T *epi_dst(const EpiArgs &ep, int m, int n) {
                       iw * ep.convt_k + kw;
     return static_cast<T *>(ep.out) + opix * ep.ldc + oc;
   }
-  return static_cast<T *>(ep.out) + long(m) * ep.ldc + n;
+  return static_cast<T *>(ep.out) + off + long(m) * ep.ldc + n;
 }
 
 // Epilogue for C[m][n..n+3]: the reference's per-op rounding chain in
@@ -88,7 +89,8 @@ template <int DT> __device__ __forceinline__ bool epi_fast(const EpiArgs &ep, in
 
 // The bf16 fast path with the bias and the residual already loaded (the
 // caller batches those loads; bias columns are fixed per lane).
-__device__ __forceinline__ void epi_fast_bf16(const EpiArgs &ep, int m, int n, float v[4], uint2 bias, uint2 resid) {
+__device__ __forceinline__ void epi_fast_bf16(const EpiArgs &ep, int m, int n, float v[4], uint2 bias, uint2 resid,
+                                              long off) {
   uint2 pk;
   if (ep.bias && ep.bias_first) {
     v[0] += lo_bf16(bias.x); v[1] += hi_bf16(bias.x); v[2] += lo_bf16(bias.y); v[3] += hi_bf16(bias.y);
@@ -116,7 +118,7 @@ __device__ __forceinline__ void epi_fast_bf16(const EpiArgs &ep, int m, int n, f
     for (int i = 0; i < 4; ++i) v[i] *= t[i];
     pk = round4_bf16(v);
   }
-  uint16_t *dst = epi_dst<uint16_t>(ep, m, n);
+  uint16_t *dst = epi_dst<uint16_t>(ep, m, n, off);
   if (ep.resid) {
     v[0] = lo_bf16(resid.x) + v[0]; v[1] = hi_bf16(resid.x) + v[1];
     v[2] = lo_bf16(resid.y) + v[2]; v[3] = hi_bf16(resid.y) + v[3];
@@ -130,7 +132,7 @@ __device__ __forceinline__ void epi_fast_bf16(const EpiArgs &ep, int m, int n, f
 }
 
 template <int DT>
-__device__ __forceinline__ void epi_store4(const EpiArgs &ep, int m, int n, int N, float v[4]) {
+__device__ __forceinline__ void epi_store4(const EpiArgs &ep, int m, int n, int N, float v[4], long off) {
   typedef Store<DT> S;
   typedef typename S::T T;
   const bool full = n + 4 <= N;
@@ -138,7 +140,7 @@ __device__ __forceinline__ void epi_store4(const EpiArgs &ep, int m, int n, int 
     const uint2 b = ep.bias ? *reinterpret_cast<const uint2 *>(static_cast<const T *>(ep.bias) + n) : make_uint2(0, 0);
     const uint2 r = ep.resid ? *reinterpret_cast<const uint2 *>(static_cast<const T *>(ep.resid) + long(m) * ep.ldr + n)
                              : make_uint2(0, 0);
-    epi_fast_bf16(ep, m, n, v, b, r);
+    epi_fast_bf16(ep, m, n, v, b, r, off);
     return;
   }
   // generic path (fp32, fp16, tails, transposed-conv scatter)
@@ -167,7 +169,7 @@ __device__ __forceinline__ void epi_store4(const EpiArgs &ep, int m, int n, int 
       v[i] = S::round(v[i] * t2);
     }
   }
-  T *out = epi_dst<T>(ep, m, n);
+  T *out = epi_dst<T>(ep, m, n, off);
   if (ep.resid) {
     const T *r = static_cast<const T *>(ep.resid) + long(m) * ep.ldr + n;
 #pragma unroll
@@ -197,7 +199,7 @@ __device__ __forceinline__ void epi_store4(const EpiArgs &ep, int m, int n, int 
 // (keeps the accumulators in registers) and the epilogue body exists once.
 template <int DT, int BM, int BN, int WTM, int WTN, int FM, int FN, int NW = 4>
 __device__ __forceinline__ void store_tile(f32x4 (&acc)[FM][FN], float *lds, const EpiArgs &ep, int row0, int col0,
-                                           int M, int N, int wave, int lane) {
+                                           int M, int N, int wave, int lane, long off) {
   constexpr int LDS_BYTES = 2 * (BM + BN) * 8 * 16;
   constexpr int RSTRIDE = WTN + 4;  // floats per staged row (+16 B pad)
   constexpr int PASSES = (NW * WTM * RSTRIDE * 4 <= LDS_BYTES) ? 1 : (NW * (WTM / 2) * RSTRIDE * 4 <= LDS_BYTES) ? 2 : 4;
@@ -225,7 +227,7 @@ __device__ __forceinline__ void store_tile(f32x4 (&acc)[FM][FN], float *lds, con
         if (m < M && n < N) {
           const f32x4 a = *reinterpret_cast<const f32x4 *>(stage + r * RSTRIDE + cl);
           float v[4] = {a[0], a[1], a[2], a[3]};
-          epi_store4<DT>(ep, m, n, N, v);
+          epi_store4<DT>(ep, m, n, N, v, off);
         }
       }
     }

@@ -201,10 +201,9 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
   }
   barrier_nofence();  // every wave done reading the stages before they are reused
 
-  EpiArgs e2 = ep;
-  if (ep.mode == EPI_ROWMAJOR) e2.out = static_cast<T *>(ep.out) + z * sc;
   store_tile<DT, BM, BN, Tile::WTM, Tile::WTN, Tile::FM, Tile::FN, Tile::NW>(
-      t.acc, reinterpret_cast<float *>(&sm), e2, m0 + t.wm * Tile::WTM, n0 + t.wn * Tile::WTN, M, N, t.wave, lane);
+      t.acc, reinterpret_cast<float *>(&sm), ep, m0 + t.wm * Tile::WTM, n0 + t.wn * Tile::WTN, M, N, t.wave, lane,
+      ep.mode == EPI_ROWMAJOR ? z * sc : 0);
 #endif
 }
 

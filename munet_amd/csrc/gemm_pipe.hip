@@ -1,0 +1,251 @@
+// Pipelined 16-bit MFMA GEMM for gfx950: C[M,N] = A[M,K] * Bt[N,K]^T with the
+// fused epilogue of gemm_common.hpp (the reference semantics are those of
+// BackendBlasCapability::matmul and nn::Linear, src/core/backend.hpp:250-260,
+// src/nn/linear.hpp:28-34).
+//
+// The hot path of the decoder's Linear layers (bf16/fp16, 16-byte aligned
+// K-contiguous operands).  Differences from the general kernel in gemm.hip:
+//   * prefetch distance 2: slab k+2 is requested from memory while slab k is
+//     multiplied and slab k+1 waits in registers, so every global load has two
+//     K steps of MFMA work to hide behind; LDS is double buffered, one barrier
+//     per K step;
+//   * the K loop has no conditional loads: a K % 64 remainder is taken as a
+//     short (zero-padded) first slab, every later slab is whole, and the loop
+//     runs two steps per trip with a peeled tail, so the staging registers
+//     never merge values from different control paths;
+//   * staging registers and LDS use native clang vector types (no struct
+//     copies through private memory);
+//   * the epilogue runs on each accumulator fragment in registers (no LDS
+//     staging): lane (r, g) of a 16x16 fragment owns row r, columns 4g..4g+3.
+// Built with MFMA results in ordinary VGPRs (see build.py).
+#include "mh_common.hpp"
+#include "mh_kernels.hpp"
+#include "gemm_common.hpp"
+
+namespace mh {
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int DT> struct PipeMfma;
+template <> struct PipeMfma<BF16> {
+  static __device__ __forceinline__ void mma(f32x4 &c, u32x4 a, u32x4 b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                0, 0);
+  }
+};
+template <> struct PipeMfma<F16> {
+  static __device__ __forceinline__ void mma(f32x4 &c, u32x4 a, u32x4 b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                               0);
+  }
+};
+
+template <int DT, int BM, int BN, int WGM, int WGN>
+__global__ void __launch_bounds__(WGM * WGN * 64)
+gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt, int M, int N, int K, long lda,
+                 long ldb, long sa, long sb, long sc, EpiArgs ep) {
+  constexpr int NT = WGM * WGN * 64, BK = 64;
+  constexpr int WTM = BM / WGM, WTN = BN / WGN, FM = WTM / 16, FN = WTN / 16;
+  constexpr int ACH = BM * 8 / NT, BCH = BN * 8 / NT;
+  static_assert(ACH >= 1 && BCH >= 1 && NT % 8 == 0, "tile too small for the thread count");
+  __shared__ u32x4 lds[2][(BM + BN) * 8];  // [buf][A rows | Bt rows][8 chunks], chunk-swizzled
+
+  // ---- tile scheduling: XCD band, then group-M (same order as gemm.hip) ----
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, ntiles = tiles_m * tiles_n;
+  int pid = blockIdx.x;
+  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+  constexpr int GROUP = 8;
+  const int span = GROUP * tiles_n, gid = pid / span, fm = gid * GROUP, gs = min(tiles_m - fm, GROUP);
+  const int tm = fm + (pid % span) % gs, tn = (pid % span) / gs;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int z = blockIdx.z;
+  A += z * sa;
+  Bt += z * sb;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave / WGN, wn = wave % WGN;
+  const int li = lane & 15, lg = lane >> 4;
+  // each thread stages chunk c0 (8 values) of ACH rows of A and BCH rows of Bt;
+  // rows past M / N read the last valid row (their results are not stored)
+  const int c0 = tid & 7;
+  const uint16_t *ap[ACH], *bp[BCH];
+  int ast[ACH], bst[BCH];
+#pragma unroll
+  for (int i = 0; i < ACH; ++i) {
+    const int r = (tid + i * NT) >> 3;
+    ap[i] = A + long(min(m0 + r, M - 1)) * lda + c0 * 8;
+    ast[i] = r * 8 + (c0 ^ (r & 7));
+  }
+#pragma unroll
+  for (int i = 0; i < BCH; ++i) {
+    const int r = (tid + i * NT) >> 3;
+    bp[i] = Bt + long(min(n0 + r, N - 1)) * ldb + c0 * 8;
+    bst[i] = BM * 8 + r * 8 + (c0 ^ (r & 7));
+  }
+
+  u32x4 ra0[ACH], rb0[BCH], ra1[ACH], rb1[BCH];
+#define MH_PGLOAD(RA, RB)                                                                         \
+  {                                                                                               \
+    _Pragma("unroll") for (int i = 0; i < ACH; ++i) {                                             \
+      RA[i] = *reinterpret_cast<const u32x4 *>(ap[i]);                                            \
+      ap[i] += BK;                                                                                \
+    }                                                                                             \
+    _Pragma("unroll") for (int i = 0; i < BCH; ++i) {                                             \
+      RB[i] = *reinterpret_cast<const u32x4 *>(bp[i]);                                            \
+      bp[i] += BK;                                                                                \
+    }                                                                                             \
+  }
+#define MH_PSTORE(RA, RB, BUF)                                                                    \
+  {                                                                                               \
+    _Pragma("unroll") for (int i = 0; i < ACH; ++i) lds[BUF][ast[i]] = RA[i];                     \
+    _Pragma("unroll") for (int i = 0; i < BCH; ++i) lds[BUF][bst[i]] = RB[i];                     \
+  }
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#define MH_PCOMPUTE(BUF)                                                                          \
+  {                                                                                               \
+    const u32x4 *as = lds[BUF], *bs = lds[BUF] + BM * 8;                                          \
+    _Pragma("unroll") for (int ks = 0; ks < 2; ++ks) {                                            \
+      const int c = ks * 4 + lg;                                                                  \
+      u32x4 af[FM], bf[FN];                                                                       \
+      _Pragma("unroll") for (int i = 0; i < FM; ++i) {                                            \
+        const int r = wm * WTM + i * 16 + li;                                                     \
+        af[i] = as[r * 8 + (c ^ (r & 7))];                                                        \
+      }                                                                                           \
+      _Pragma("unroll") for (int j = 0; j < FN; ++j) {                                            \
+        const int r = wn * WTN + j * 16 + li;                                                     \
+        bf[j] = bs[r * 8 + (c ^ (r & 7))];                                                        \
+      }                                                                                           \
+      _Pragma("unroll") for (int i = 0; i < FM; ++i)                                              \
+        _Pragma("unroll") for (int j = 0; j < FN; ++j) PipeMfma<DT>::mma(acc[i][j], bf[j], af[i]); \
+    }                                                                                             \
+  }
+
+  // slab 0 covers columns [0, K0), K0 = K % 64 (or 64): chunks at or past K0
+  // are zero; every later slab is whole
+  const int KT = (K + BK - 1) / BK, K0 = K - (KT - 1) * BK;
+  {
+    const bool cin = c0 * 8 < K0;
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      ra0[i] = cin ? *reinterpret_cast<const u32x4 *>(ap[i]) : u32x4{0, 0, 0, 0};
+      ap[i] += K0;
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      rb0[i] = cin ? *reinterpret_cast<const u32x4 *>(bp[i]) : u32x4{0, 0, 0, 0};
+      bp[i] += K0;
+    }
+  }
+  if (KT > 1) MH_PGLOAD(ra1, rb1);
+  MH_PSTORE(ra0, rb0, 0);
+  __syncthreads();
+  int k = 0;
+  for (; k + 3 < KT; k += 2) {  // slab k in LDS 0, slab k+1 in regs 1; slabs k+2, k+3 exist
+    MH_PGLOAD(ra0, rb0);
+    MH_PCOMPUTE(0);
+    MH_PSTORE(ra1, rb1, 1);
+    __syncthreads();
+    MH_PGLOAD(ra1, rb1);
+    MH_PCOMPUTE(1);
+    MH_PSTORE(ra0, rb0, 0);
+    __syncthreads();
+  }
+  const int rem = KT - k;  // 1, 2 or 3 slabs left
+  if (rem == 3) {
+    MH_PGLOAD(ra0, rb0);
+    MH_PCOMPUTE(0);
+    MH_PSTORE(ra1, rb1, 1);
+    __syncthreads();
+    MH_PCOMPUTE(1);
+    MH_PSTORE(ra0, rb0, 0);
+    __syncthreads();
+    MH_PCOMPUTE(0);
+  } else if (rem == 2) {
+    MH_PCOMPUTE(0);
+    MH_PSTORE(ra1, rb1, 1);
+    __syncthreads();
+    MH_PCOMPUTE(1);
+  } else {
+    MH_PCOMPUTE(0);
+  }
+#undef MH_PGLOAD
+#undef MH_PSTORE
+#undef MH_PCOMPUTE
+
+  // ---- epilogue ----
+  const long off = ep.mode == EPI_ROWMAJOR ? z * sc : 0;
+  if (DT == BF16 && ep.mode != EPI_CONVT && N % 4 == 0 && (!ep.resid || (ep.ldr & 3) == 0)) {
+    // straight from the accumulators: every fragment takes the bf16 fast path
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int m = m0 + wm * WTM + i * 16 + li;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = n0 + wn * WTN + j * 16 + lg * 4;
+        if (m < M && n < N) {
+          float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+          const uint2 b = ep.bias ? *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(ep.bias) + n)
+                                  : make_uint2(0, 0);
+          const uint2 r = ep.resid
+                              ? *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(ep.resid) + long(m) * ep.ldr + n)
+                              : make_uint2(0, 0);
+          epi_fast_bf16(ep, m, n, v, b, r, off);
+        }
+      }
+    }
+  } else {
+    // general epilogue (fp16 rounding, transposed-conv scatter, ragged N)
+    // through the idle LDS
+    __syncthreads();
+    store_tile<DT, BM, BN, WTM, WTN, FM, FN, WGM * WGN>(acc, reinterpret_cast<float *>(&lds[0][0]), ep,
+                                                       m0 + wm * WTM, n0 + wn * WTN, M, N, wave, lane, off);
+  }
+}
+
+template <int DT, int BM, int BN, int WGM, int WGN>
+void launch(const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch, long sa, long sb,
+            long sc, const EpiArgs &ep, hipStream_t st) {
+  const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm_pipe_kernel<DT, BM, BN, WGM, WGN>), dim3(tiles, 1, batch), dim3(WGM * WGN * 64), 0, st,
+                     (const uint16_t *)A, (const uint16_t *)Bt, M, N, K, lda, ldb, sa, sb, sc, ep);
+}
+
+template <int DT>
+hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch, long sa,
+                     long sb, long sc, const EpiArgs &ep, int tile, hipStream_t st) {
+  if (tile < 0) {
+    // measured on MI355X (decoder shapes, K = 768 / 3072): 128x128 when it
+    // gives >= 2.5 tiles per CU, else 128x64; 64x64 for small problems
+    const long t128 = long((M + 127) / 128) * ((N + 127) / 128) * batch;
+    const long t64 = long((M + 127) / 128) * ((N + 63) / 64) * batch;
+    tile = t128 >= 640 ? 0 : (t64 >= 256 ? 1 : 2);
+  }
+  switch (tile) {
+  case 0: launch<DT, 128, 128, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;
+  case 1: launch<DT, 128, 64, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;
+  default: launch<DT, 64, 64, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemm_pipe_ok(int dt, const void *A, const void *Bt, int K, long lda, long ldb, long sa, long sb) {
+  return (dt == BF16 || dt == F16) && K > 0 && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && sa % 8 == 0 &&
+         sb % 8 == 0 && (uintptr_t)A % 16 == 0 && (uintptr_t)Bt % 16 == 0;
+}
+
+hipError_t gemm_pipe(int dt, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch,
+                     long sa, long sb, long sc, const EpiArgs &ep, int tile, hipStream_t st) {
+  if (M <= 0 || N <= 0 || batch <= 0) return hipSuccess;
+  if (!gemm_pipe_ok(dt, A, Bt, K, lda, ldb, sa, sb)) return hipErrorInvalidValue;
+  if (dt == BF16) return launch_dt<BF16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile, st);
+  return launch_dt<F16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile, st);
+}
+
+}  // namespace mh

@@ -1,6 +1,7 @@
-"""Every GEMM block-tile variant (direct-to-LDS and register-staged) against
-the oracle, forced through MUNET_HIP_GEMM_TILE in a child process, on shapes
-with ragged M / N tails and K multiples of 64 (and one ragged K)."""
+"""Every GEMM block-tile variant (direct-to-LDS, general register-staged and
+pipelined) against the oracle, forced through MUNET_HIP_GEMM_TILE in a child
+process, on shapes with ragged M / N tails, N % 4 != 0 (general epilogue),
+K from one to seven 64-wide slabs and ragged K (short first slab)."""
 import os
 import subprocess
 import sys
@@ -21,7 +22,8 @@ from oracle import CpuOracle
 from util import assert_close, rand
 hip, orc = HipBackend(0), CpuOracle("restatement")
 for dt in (synth.BF16, synth.F16):
-    for (M, K, N) in [(300, 192, 200), (257, 128, 129), (64, 64, 64), (520, 256, 264), (96, 200, 72)]:
+    for (M, K, N) in [(300, 192, 200), (257, 128, 129), (64, 64, 64), (520, 256, 264), (96, 200, 72),
+                      (130, 320, 96), (70, 448, 136), (33, 40, 48)]:
         x, w, b = rand((M, K), dt, 1), rand((K, N), dt, 2, 0.2), rand((N,), dt, 3)
         r = rand((M, N), dt, 4)
         ref = orc.add(r, orc.gelu(orc.linear(x, w, b, dt), dt), dt)
@@ -34,7 +36,7 @@ print("ok")
 '''
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 100, 101, 102, 103, 104, 105, 106, 107])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 100, 101, 102, 103, 104, 105, 106, 107, 200, 201, 202])
 def test_forced_tile(tile):
     root = os.path.dirname(HERE)
     code = SCRIPT.format(root=root, tests=HERE, tile=tile)
