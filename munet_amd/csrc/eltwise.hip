@@ -157,6 +157,45 @@ embedding_kernel(const int32_t *__restrict__ ids, const typename Store<DT>::T *_
   }
 }
 
+// Rows of D <= 256*NV values with D % 4 == 0: 4 values per lane per step,
+// every load of the row issued before the first store.
+template <int DT, int NV>
+__global__ void __launch_bounds__(256)
+embedding_vec_kernel(const int32_t *__restrict__ ids, const typename Store<DT>::T *__restrict__ w,
+                     const typename Store<DT>::T *__restrict__ pos, typename Store<DT>::T *__restrict__ out, int n,
+                     int V, int D, int T, int *__restrict__ err) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= n) return;
+  const int tok = ids[row];
+  const bool ok = tok >= 0 && tok < V;
+  if (!ok && lane == 0) atomicOr(err, 1);
+  const typename Store<DT>::T *src = w + long(ok ? tok : 0) * D;
+  const typename Store<DT>::T *prow = pos ? pos + long(row % T) * D : nullptr;
+  typename Store<DT>::T *dst = out + long(row) * D;
+  float v[NV][4], p[NV][4];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c = (k * 64 + lane) * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[k][e] = p[k][e] = 0.f;
+    if (c < D) {
+      if (ok) ld4<DT>(src + c, v[k]);
+      if (prow) ld4<DT>(prow + c, p[k]);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c = (k * 64 + lane) * 4;
+    if (c < D) {
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = prow ? p[k][e] + v[k][e] : v[k][e];
+      st4<DT>(dst + c, o);
+    }
+  }
+}
+
 // One wave per row: first index of the maximum (NaN never wins).
 template <int DT>
 __global__ void __launch_bounds__(256)
@@ -248,6 +287,26 @@ hipError_t embedding(int dt, const int32_t *ids, const void *w, const void *pos,
                      int T, int *err, hipStream_t st) {
   if (n <= 0) return hipSuccess;
   dim3 grid((n + 3) / 4);
+  const size_t es = dt == F32 ? 4 : 2;
+  const bool vec = D % 4 == 0 && D <= 1024 && (uintptr_t)w % (4 * es) == 0 && (uintptr_t)out % (4 * es) == 0 &&
+                   (uintptr_t)pos % (4 * es) == 0;
+  if (vec) {
+#define MH_EMB(DTV, T, NV)                                                                                      \
+  hipLaunchKernelGGL((embedding_vec_kernel<DTV, NV>), grid, dim3(256), 0, st, ids, (const T *)w, (const T *)pos, \
+                     (T *)out, n, V, D, T_, err)
+#define MH_EMB_NV(DTV, T) \
+  { if (D <= 256) MH_EMB(DTV, T, 1); else if (D <= 512) MH_EMB(DTV, T, 2); else if (D <= 768) MH_EMB(DTV, T, 3); else MH_EMB(DTV, T, 4); }
+    const int T_ = T;
+    switch (dt) {
+    case F32: MH_EMB_NV(F32, float); break;
+    case F16: MH_EMB_NV(F16, uint16_t); break;
+    case BF16: MH_EMB_NV(BF16, uint16_t); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef MH_EMB_NV
+#undef MH_EMB
+    return hipGetLastError();
+  }
   switch (dt) {
   case F32: hipLaunchKernelGGL(embedding_kernel<F32>, grid, dim3(256), 0, st, ids, (const float *)w, (const float *)pos, (float *)out, n, V, D, T, err); break;
   case F16: hipLaunchKernelGGL(embedding_kernel<F16>, grid, dim3(256), 0, st, ids, (const uint16_t *)w, (const uint16_t *)pos, (uint16_t *)out, n, V, D, T, err); break;

@@ -28,6 +28,14 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// 16-byte load through a global-address-space pointer.  The loop-carried
+// staging pointers would otherwise compile to FLAT loads, which also count on
+// the LDS wait counter: every wait for an LDS fragment would then wait for the
+// in-flight prefetch as well.
+__device__ __forceinline__ u32x4 ldg16(const uint16_t *p) {
+  return *(const __attribute__((address_space(1))) u32x4 *)(p);
+}
+
 template <int DT> struct PipeMfma;
 template <> struct PipeMfma<BF16> {
   static __device__ __forceinline__ void mma(f32x4 &c, u32x4 a, u32x4 b) {
@@ -88,11 +96,11 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
 #define MH_PGLOAD(RA, RB)                                                                         \
   {                                                                                               \
     _Pragma("unroll") for (int i = 0; i < ACH; ++i) {                                             \
-      RA[i] = *reinterpret_cast<const u32x4 *>(ap[i]);                                            \
+      RA[i] = ldg16(ap[i]);                                                                       \
       ap[i] += BK;                                                                                \
     }                                                                                             \
     _Pragma("unroll") for (int i = 0; i < BCH; ++i) {                                             \
-      RB[i] = *reinterpret_cast<const u32x4 *>(bp[i]);                                            \
+      RB[i] = ldg16(bp[i]);                                                                       \
       bp[i] += BK;                                                                                \
     }                                                                                             \
   }
@@ -132,12 +140,12 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
     const bool cin = c0 * 8 < K0;
 #pragma unroll
     for (int i = 0; i < ACH; ++i) {
-      ra0[i] = cin ? *reinterpret_cast<const u32x4 *>(ap[i]) : u32x4{0, 0, 0, 0};
+      ra0[i] = cin ? ldg16(ap[i]) : u32x4{0, 0, 0, 0};
       ap[i] += K0;
     }
 #pragma unroll
     for (int i = 0; i < BCH; ++i) {
-      rb0[i] = cin ? *reinterpret_cast<const u32x4 *>(bp[i]) : u32x4{0, 0, 0, 0};
+      rb0[i] = cin ? ldg16(bp[i]) : u32x4{0, 0, 0, 0};
       bp[i] += K0;
     }
   }
@@ -180,7 +188,26 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
   // ---- epilogue ----
   const long off = ep.mode == EPI_ROWMAJOR ? z * sc : 0;
   if (DT == BF16 && ep.mode != EPI_CONVT && N % 4 == 0 && (!ep.resid || (ep.ldr & 3) == 0)) {
-    // straight from the accumulators: every fragment takes the bf16 fast path
+    // straight from the accumulators: every fragment takes the bf16 fast
+    // path; all bias / residual quads of the tile are requested before the
+    // first is used, so their latencies overlap
+    const uint16_t *bias = static_cast<const uint16_t *>(ep.bias), *resid = static_cast<const uint16_t *>(ep.resid);
+    uint2 bq[FN], rq[FM][FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = n0 + wn * WTN + j * 16 + lg * 4;
+      bq[j] = (bias && n < N) ? *reinterpret_cast<const uint2 *>(bias + n) : make_uint2(0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int m = m0 + wm * WTM + i * 16 + li;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = n0 + wn * WTN + j * 16 + lg * 4;
+        rq[i][j] = (resid && m < M && n < N) ? *reinterpret_cast<const uint2 *>(resid + long(m) * ep.ldr + n)
+                                             : make_uint2(0, 0);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int m = m0 + wm * WTM + i * 16 + li;
@@ -189,12 +216,7 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
         const int n = n0 + wn * WTN + j * 16 + lg * 4;
         if (m < M && n < N) {
           float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-          const uint2 b = ep.bias ? *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(ep.bias) + n)
-                                  : make_uint2(0, 0);
-          const uint2 r = ep.resid
-                              ? *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(ep.resid) + long(m) * ep.ldr + n)
-                              : make_uint2(0, 0);
-          epi_fast_bf16(ep, m, n, v, b, r, off);
+          epi_fast_bf16(ep, m, n, v, bq[j], rq[i][j], off);
         }
       }
     }
@@ -220,10 +242,11 @@ hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long ld
                      long sb, long sc, const EpiArgs &ep, int tile, hipStream_t st) {
   if (tile < 0) {
     // measured on MI355X (decoder shapes, K = 768 / 3072): 128x128 when it
-    // gives >= 2.5 tiles per CU, else 128x64; 64x64 for small problems
+    // gives >= 2.5 tiles per CU or K is deep enough to amortise a partly
+    // filled chip, else 128x64; 64x64 for small problems
     const long t128 = long((M + 127) / 128) * ((N + 127) / 128) * batch;
     const long t64 = long((M + 127) / 128) * ((N + 63) / 64) * batch;
-    tile = t128 >= 640 ? 0 : (t64 >= 256 ? 1 : 2);
+    tile = (t128 >= 640 || (K >= 2048 && t128 >= 128)) ? 0 : (t64 >= 256 ? 1 : 2);
   }
   switch (tile) {
   case 0: launch<DT, 128, 128, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;

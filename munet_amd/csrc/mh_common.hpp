@@ -88,6 +88,29 @@ template <> struct Store<BF16> {
   static __device__ __forceinline__ float dec(uint16_t v) { return bf16_to_f32(v); }
 };
 
+// Four consecutive values (8-byte aligned for 16-bit types, 16-byte for fp32)
+// decoded to / encoded from floats with the dtype's codec.
+template <int DT>
+__device__ __forceinline__ void ld4(const typename Store<DT>::T *p, float v[4]) {
+  if constexpr (DT == F32) {
+    const f32x4 x = *reinterpret_cast<const f32x4 *>(p);
+    v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
+  } else {
+    const u16x4 x = *reinterpret_cast<const u16x4 *>(p);
+    v[0] = Store<DT>::dec(x[0]); v[1] = Store<DT>::dec(x[1]); v[2] = Store<DT>::dec(x[2]); v[3] = Store<DT>::dec(x[3]);
+  }
+}
+template <int DT>
+__device__ __forceinline__ void st4(typename Store<DT>::T *p, const float v[4]) {
+  if constexpr (DT == F32) {
+    *reinterpret_cast<f32x4 *>(p) = f32x4{v[0], v[1], v[2], v[3]};
+  } else {
+    u16x4 x;
+    x[0] = Store<DT>::enc(v[0]); x[1] = Store<DT>::enc(v[1]); x[2] = Store<DT>::enc(v[2]); x[3] = Store<DT>::enc(v[3]);
+    *reinterpret_cast<u16x4 *>(p) = x;
+  }
+}
+
 // Generic (runtime dtype) scalar access for the cold paths.
 __device__ __forceinline__ float ld_any(const void *p, int dt, size_t i) {
   if (dt == F32) return static_cast<const float *>(p)[i];
@@ -105,7 +128,11 @@ __device__ __forceinline__ void st_any(void *p, int dt, size_t i, float v) {
 
 // Sigmoid in float: 1 / (1 + e^-x), as the reference's fp32 kernel writes it
 // (src/backend/cpu_backend.hpp:509-531).
-__device__ __forceinline__ float sigmoidf_ref(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// 1 / (1 + exp(-x)) as the reference writes it (src/nn/activations.hpp:31-38),
+// with the hardware exp2 and reciprocal (within 2 ulp of the correctly rounded
+// float expression; every caller rounds the result to the storage dtype or
+// compares at fp32 tolerance).
+__device__ __forceinline__ float sigmoidf_ref(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 // Wavefront (64-lane) reductions via cross-lane shuffles.
 __device__ __forceinline__ float wave_sum(float v) {

@@ -55,6 +55,59 @@ layernorm_kernel(const typename Store<DT>::T *__restrict__ x, const typename Sto
   }
 }
 
+// Rows of <= 256*NV values with cols % 4 == 0: each lane holds NV groups of 4
+// consecutive values, every load of the row (x, w, b) is issued before the
+// first reduction.
+template <int DT, int NV>
+__global__ void __launch_bounds__(256)
+layernorm_vec_kernel(const typename Store<DT>::T *__restrict__ x, const typename Store<DT>::T *__restrict__ w,
+                     const typename Store<DT>::T *__restrict__ b, typename Store<DT>::T *__restrict__ y, int rows,
+                     int cols, float eps) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const typename Store<DT>::T *xr = x + long(row) * cols;
+  float v[NV][4], wv[NV][4], bv[NV][4];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c = (k * 64 + lane) * 4;
+    if (c < cols) {
+      ld4<DT>(xr + c, v[k]);
+      ld4<DT>(w + c, wv[k]);
+      ld4<DT>(b + c, bv[k]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[k][e] = wv[k][e] = bv[k][e] = 0.f;
+    }
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) sum += (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]);
+  const float mean = wave_sum(sum) / float(cols);
+  float var = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+    if ((k * 64 + lane) * 4 < cols)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d = v[k][e] - mean;
+        var += d * d;
+      }
+  var = wave_sum(var) / float(cols);
+  const float inv = 1.0f / sqrtf(var + eps);
+  typename Store<DT>::T *yr = y + long(row) * cols;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c = (k * 64 + lane) * 4;
+    if (c < cols) {
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (v[k][e] - mean) * inv * wv[k][e] + bv[k][e];
+      st4<DT>(yr + c, o);
+    }
+  }
+}
+
 // Long rows: three streaming passes (mean, variance, normalise).
 template <int DT>
 __global__ void __launch_bounds__(256)
@@ -105,7 +158,14 @@ hipError_t ln_dt(const void *x, const void *w, const void *b, void *y, int rows,
   dim3 grid((rows + 3) / 4), block(256);
   const T *X = (const T *)x, *W = (const T *)w, *B = (const T *)b;
   T *Y = (T *)y;
-  if (cols <= 64 * 4) hipLaunchKernelGGL((layernorm_kernel<DT, 4>), grid, block, 0, st, X, W, B, Y, rows, cols, eps);
+  const bool vec = cols % 4 == 0 && (uintptr_t)x % (4 * sizeof(T)) == 0 && (uintptr_t)y % (4 * sizeof(T)) == 0 &&
+                   (uintptr_t)w % (4 * sizeof(T)) == 0 && (uintptr_t)b % (4 * sizeof(T)) == 0;
+  if (vec && cols <= 256) hipLaunchKernelGGL((layernorm_vec_kernel<DT, 1>), grid, block, 0, st, X, W, B, Y, rows, cols, eps);
+  else if (vec && cols <= 512) hipLaunchKernelGGL((layernorm_vec_kernel<DT, 2>), grid, block, 0, st, X, W, B, Y, rows, cols, eps);
+  else if (vec && cols <= 768) hipLaunchKernelGGL((layernorm_vec_kernel<DT, 3>), grid, block, 0, st, X, W, B, Y, rows, cols, eps);
+  else if (vec && cols <= 1024) hipLaunchKernelGGL((layernorm_vec_kernel<DT, 4>), grid, block, 0, st, X, W, B, Y, rows, cols, eps);
+  else if (vec && cols <= 2048) hipLaunchKernelGGL((layernorm_vec_kernel<DT, 8>), grid, block, 0, st, X, W, B, Y, rows, cols, eps);
+  else if (cols <= 64 * 4) hipLaunchKernelGGL((layernorm_kernel<DT, 4>), grid, block, 0, st, X, W, B, Y, rows, cols, eps);
   else if (cols <= 64 * 8) hipLaunchKernelGGL((layernorm_kernel<DT, 8>), grid, block, 0, st, X, W, B, Y, rows, cols, eps);
   else if (cols <= 64 * 16) hipLaunchKernelGGL((layernorm_kernel<DT, 16>), grid, block, 0, st, X, W, B, Y, rows, cols, eps);
   else hipLaunchKernelGGL((layernorm_long_kernel<DT>), grid, block, 0, st, X, W, B, Y, rows, cols, eps);

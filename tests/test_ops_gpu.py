@@ -188,8 +188,10 @@ def test_masked_fill(hip, orc, dt):
 
 
 @pytest.mark.parametrize("dt", DTS)
-def test_embedding(hip, orc, dt):
-    V, D, B, T = 50, 24, 3, 7
+@pytest.mark.parametrize("D", [24, 30, 768, 1100])
+def test_embedding(hip, orc, dt, D):
+    """D % 4 == 0 and D <= 1024 take the vectorised kernel, the rest the scalar one."""
+    V, B, T = 50, 3, 7
     w = rand((V, D), dt, 90)
     ids = np.random.default_rng(1).integers(0, V, (B, T)).astype(np.int32)
     out = empty((B * T, D), dt)
