@@ -10,8 +10,9 @@ One step = one compiled forward (one hipGraph launch) over the resident
 steps bracketed by torch.cuda.synchronize() on both sides.
 
 Roofline: every kernel of the forward is also timed on its own with HIP
-events (eager launches on torch's current stream, the stream they are
-enqueued on); the kernel with the largest time per forward is reported
+events on the stream it runs on (20 launches captured in one graph and
+replayed, so host launch cost is excluded); the kernel with the largest time
+per forward is reported
 against the bf16 MFMA peak (GEMM / attention: algorithmic 2*M*N*K FLOPs) or
 the HBM peak (LayerNorm: unique bytes).  CPU baseline: the C++ restatement
 of MuNet's CPU backend (oracle/, "port") on a bounded sample of the same
@@ -42,7 +43,8 @@ def log(msg):
 
 
 def kernel_table(hip, torch):
-    """Per-kernel event timing of every distinct kernel of the forward."""
+    """Per-kernel timing (graph-replayed, HIP events) of every distinct kernel
+    of the forward."""
     from munet_amd.backend import empty
     d, H, F, V = CFG["d_model"], CFG["num_heads"], CFG["ffn"], CFG["vocab"]
     M, hd, L = B * T, d // H, CFG["num_layers"]
@@ -56,13 +58,23 @@ def kernel_table(hip, torch):
     rows = []
 
     def timeit(name, fn, count, flops=0.0, bytes_=0.0, reps=20):
-        fn()
-        torch.cuda.synchronize()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        for _ in range(reps):
+        # `reps` launches captured in one HIP graph on a side stream and
+        # replayed between HIP events on that stream: GPU time per launch,
+        # free of host launch overhead (the engine replays a graph too)
+        st = torch.cuda.Stream()
+        with torch.cuda.stream(st):
             fn()
-        e.record()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=st):
+            for _ in range(reps):
+                fn()
+        with torch.cuda.stream(st):
+            graph.replay()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            graph.replay()
+            e.record()
         torch.cuda.synchronize()
         t = s.elapsed_time(e) / reps * 1e-3
         rows.append(dict(name=name, t=t, count=count, flops=flops, bytes=bytes_))

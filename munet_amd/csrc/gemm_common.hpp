@@ -87,10 +87,9 @@ template <int DT> __device__ __forceinline__ bool epi_fast(const EpiArgs &ep, in
   return DT == BF16 && n + 4 <= N && ep.mode != EPI_CONVT && (!ep.resid || (ep.ldr & 3) == 0);
 }
 
-// The bf16 fast path with the bias and the residual already loaded (the
-// caller batches those loads; bias columns are fixed per lane).
-__device__ __forceinline__ void epi_fast_bf16(const EpiArgs &ep, int m, int n, float v[4], uint2 bias, uint2 resid,
-                                              long off) {
+// The bf16 fast path's arithmetic: the rounded, packed 4 output values, with
+// the bias and the residual already loaded (callers batch those loads).
+__device__ __forceinline__ uint2 epi_fast_bf16_value(const EpiArgs &ep, float v[4], uint2 bias, uint2 resid) {
   uint2 pk;
   if (ep.bias && ep.bias_first) {
     v[0] += lo_bf16(bias.x); v[1] += hi_bf16(bias.x); v[2] += lo_bf16(bias.y); v[3] += hi_bf16(bias.y);
@@ -118,12 +117,19 @@ __device__ __forceinline__ void epi_fast_bf16(const EpiArgs &ep, int m, int n, f
     for (int i = 0; i < 4; ++i) v[i] *= t[i];
     pk = round4_bf16(v);
   }
-  uint16_t *dst = epi_dst<uint16_t>(ep, m, n, off);
   if (ep.resid) {
     v[0] = lo_bf16(resid.x) + v[0]; v[1] = hi_bf16(resid.x) + v[1];
     v[2] = lo_bf16(resid.y) + v[2]; v[3] = hi_bf16(resid.y) + v[3];
     pk = round4_bf16(v);
   }
+  return pk;
+}
+
+// The bf16 fast path for output columns n..n+3 of row m.
+__device__ __forceinline__ void epi_fast_bf16(const EpiArgs &ep, int m, int n, float v[4], uint2 bias, uint2 resid,
+                                              long off) {
+  const uint2 pk = epi_fast_bf16_value(ep, v, bias, resid);
+  uint16_t *dst = epi_dst<uint16_t>(ep, m, n, off);
   if (((uintptr_t)dst & 7) == 0) {
     *reinterpret_cast<uint2 *>(dst) = pk;
   } else {

@@ -208,6 +208,36 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
                                              : make_uint2(0, 0);
       }
     }
+    // destination = column part (per fragment column) + row part (per
+    // fragment row): the head-split index divisions run FM + FN times, not
+    // FM * FN times
+    uint16_t *cbase[FN];
+    long roff[FM];
+    bool al8;
+    if (ep.mode == EPI_HEADSPLIT) {
+      // [B, T, 3E] -> q/k/v [B, H, T, hd]: row (b, t), column (which, h, dd)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = min(n0 + wn * WTN + j * 16 + lg * 4, N - 4);
+        const int which = n / ep.E, e = n - which * ep.E, h = e / ep.hd, dd = e - h * ep.hd;
+        uint16_t *o = static_cast<uint16_t *>(which == 0 ? ep.outs[0] : which == 1 ? ep.outs[1] : ep.outs[2]);
+        cbase[j] = o + long(h) * ep.T * ep.hd + dd;
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int m = min(m0 + wm * WTM + i * 16 + li, M - 1);
+        const int b = m / ep.T, t = m - b * ep.T;
+        roff[i] = (long(b) * ep.H * ep.T + t) * ep.hd;
+      }
+      al8 = (ep.hd & 3) == 0 && ((uintptr_t)ep.outs[0] & 7) == 0 && ((uintptr_t)ep.outs[1] & 7) == 0 &&
+            ((uintptr_t)ep.outs[2] & 7) == 0;
+    } else {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) cbase[j] = static_cast<uint16_t *>(ep.out) + off + n0 + wn * WTN + j * 16 + lg * 4;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) roff[i] = long(m0 + wm * WTM + i * 16 + li) * ep.ldc;
+      al8 = ((uintptr_t)ep.out & 7) == 0 && (ep.ldc & 3) == 0 && (off & 3) == 0;
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int m = m0 + wm * WTM + i * 16 + li;
@@ -216,7 +246,13 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
         const int n = n0 + wn * WTN + j * 16 + lg * 4;
         if (m < M && n < N) {
           float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-          epi_fast_bf16(ep, m, n, v, bq[j], rq[i][j], off);
+          const uint2 pk = epi_fast_bf16_value(ep, v, bq[j], rq[i][j]);
+          uint16_t *dst = cbase[j] + roff[i];
+          if (al8) {
+            *reinterpret_cast<uint2 *>(dst) = pk;
+          } else {
+            dst[0] = uint16_t(pk.x); dst[1] = uint16_t(pk.x >> 16); dst[2] = uint16_t(pk.y); dst[3] = uint16_t(pk.y >> 16);
+          }
         }
       }
     }
