@@ -42,9 +42,9 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def kernel_table(hip, torch):
-    """Per-kernel timing (graph-replayed, HIP events) of every distinct kernel
-    of the forward."""
+def kernel_specs(hip, torch):
+    """(name, launch, launches per forward, FLOPs, bytes) for every distinct
+    kernel of the forward, on inputs of the forward's shapes."""
     from munet_amd.backend import empty
     d, H, F, V = CFG["d_model"], CFG["num_heads"], CFG["ffn"], CFG["vocab"]
     M, hd, L = B * T, d // H, CFG["num_layers"]
@@ -55,12 +55,44 @@ def kernel_table(hip, torch):
         return (torch.randn(*s, device="cuda", generator=g) * scale).to(bf)
 
     x, w = rnd(M, d), rnd(M, F)
-    rows = []
+    specs = []
 
-    def timeit(name, fn, count, flops=0.0, bytes_=0.0, reps=20):
+    def linear(name, K_, N_, act, resid):
+        a = x if K_ == d else w
+        wt = rnd(N_, K_, scale=0.02)
+        bias = torch.zeros(N_, device="cuda", dtype=bf)
+        out = empty((M, N_), 2)
+        r = rnd(M, N_) if resid else None
+        specs.append((name, lambda: hip.linear(a, wt, bias, out, M, K_, N_, act, r), 1 if name == "lm_head" else L,
+                      2.0 * M * N_ * K_, 0.0))
+
+    linear("ffn_up_gelu", d, F, 2, False)
+    linear("ffn_down_resid", F, d, 0, True)
+    linear("attn_out_resid", d, d, 0, True)
+    linear("lm_head", d, V, 0, False)
+    wqkv = rnd(3 * d, d, scale=0.02)
+    bq = torch.zeros(3 * d, device="cuda", dtype=bf)
+    q, k, v = (empty((M * d,), 2) for _ in range(3))
+    specs.append(("qkv_headsplit", lambda: hip.qkv_projection(x, wqkv, bq, q, k, v, B, T, d, H), L,
+                  2.0 * M * 3 * d * d, 0.0))
+    ctx = empty((M, d), 2)
+    specs.append(("attention_causal", lambda: hip.attention(q, k, v, ctx, B, H, T, hd, True), L,
+                  4.0 * B * H * T * T * hd / 2, 0.0))
+    lw, lb, ly = rnd(d), rnd(d), empty((M, d), 2)
+    specs.append(("layer_norm", lambda: hip.layer_norm(x, lw, lb, ly, M, d), 2 * L + 1, 0.0,
+                  2.0 * M * d * 2 + 2 * d * 2))
+    return specs
+
+
+def kernel_table(hip, torch):
+    """Per-kernel timing (graph-replayed, HIP events) of every distinct kernel
+    of the forward."""
+    rows = []
+    for name, fn, count, flops, bytes_ in kernel_specs(hip, torch):
         # `reps` launches captured in one HIP graph on a side stream and
         # replayed between HIP events on that stream: GPU time per launch,
         # free of host launch overhead (the engine replays a graph too)
+        reps = 20
         st = torch.cuda.Stream()
         with torch.cuda.stream(st):
             fn()
@@ -78,26 +110,39 @@ def kernel_table(hip, torch):
         torch.cuda.synchronize()
         t = s.elapsed_time(e) / reps * 1e-3
         rows.append(dict(name=name, t=t, count=count, flops=flops, bytes=bytes_))
-
-    for (name, K_, N_, act, resid) in [("ffn_up_gelu", d, F, 2, False), ("ffn_down_resid", F, d, 0, True),
-                                        ("attn_out_resid", d, d, 0, True), ("lm_head", d, V, 0, False)]:
-        a = x if K_ == d else w
-        wt = rnd(N_, K_, scale=0.02)
-        bias = torch.zeros(N_, device="cuda", dtype=bf)
-        out = empty((M, N_), 2)
-        r = rnd(M, N_) if resid else None
-        timeit(name, lambda: hip.linear(a, wt, bias, out, M, K_, N_, act, r), 1 if name == "lm_head" else L,
-               flops=2.0 * M * N_ * K_)
-    wqkv = rnd(3 * d, d, scale=0.02)
-    bq = torch.zeros(3 * d, device="cuda", dtype=bf)
-    q, k, v = (empty((M * d,), 2) for _ in range(3))
-    timeit("qkv_headsplit", lambda: hip.qkv_projection(x, wqkv, bq, q, k, v, B, T, d, H), L, flops=2.0 * M * 3 * d * d)
-    ctx = empty((M, d), 2)
-    timeit("attention_causal", lambda: hip.attention(q, k, v, ctx, B, H, T, hd, True), L,
-           flops=4.0 * B * H * T * T * hd / 2)
-    lw, lb, ly = rnd(d), rnd(d), empty((M, d), 2)
-    timeit("layer_norm", lambda: hip.layer_norm(x, lw, lb, ly, M, d), 2 * L + 1, bytes_=2.0 * M * d * 2 + 2 * d * 2)
     return rows
+
+
+COPY_BYTES = 256 << 20  # the calibration copy of --probe
+
+
+def probe(hip, torch, name):
+    """For rocprofv3 --pmc passes: 5 eager launches of one kernel of the
+    forward, then one device-to-device copy of COPY_BYTES (the counter
+    calibration: it reads and writes exactly that many bytes)."""
+    spec = {s[0]: s for s in kernel_specs(hip, torch)}[name]
+    torch.cuda.synchronize()
+    for _ in range(5):
+        spec[1]()
+    torch.cuda.synchronize()
+    a = torch.ones(COPY_BYTES // 2, device="cuda", dtype=torch.bfloat16)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    log(f"probe: {name} x5, copy {COPY_BYTES} bytes")
+
+
+def measured_traffic(name):
+    """HBM bytes per launch of `name` from its committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (profiles/<name>_traffic.md), or None."""
+    path = os.path.join(ROOT, "profiles", f"{name}_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
 
 
 def cpu_baseline():
@@ -133,6 +178,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--probe", default=None, help="run one kernel of the forward for rocprofv3 --pmc and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -145,6 +191,9 @@ def main():
     from munet_amd.engine import Engine
 
     hip = HipBackend(0)
+    if args.probe:
+        probe(hip, torch, args.probe)
+        return
     cfg = models.decoder_config(**CFG)
     log("bench: initialising weights")
     params = models.init_params(cfg, "gpt", scope="bench")
@@ -177,7 +226,7 @@ def main():
     else:
         ach = dom["bytes"] / dom["t"]
         roof = dict(bound="hbm", achieved=ach / 1e9, peak=PEAK_HBM / 1e9, unit="GB/s", frac=ach / PEAK_HBM)
-    roof.update(kernel=dom["name"], avg_us=dom["t"] * 1e6, traffic=None)
+    roof.update(kernel=dom["name"], avg_us=dom["t"] * 1e6, traffic=measured_traffic(dom["name"]))
     gemm = [r for r in rows if r["flops"] and r["name"] != "attention_causal"]
     gemm_frac = sum(r["flops"] * r["count"] for r in gemm) / sum(r["per_fwd"] for r in gemm) / PEAK_BF16
     ln = next(r for r in rows if r["name"] == "layer_norm")
