@@ -37,6 +37,13 @@ typedef struct mh_engine mh_engine;
 
 int mh_engine_create(mh_engine **engine, const char *config_json, int device);
 int mh_engine_destroy(mh_engine *engine);
+/* Create an engine from a MuNet deploy artifact (`munet_model` rev-1 .npz:
+ * `__config__` JSON + one .npy per named parameter), validating its metadata
+ * as the reference loader does (reference inference::load_serialized,
+ * src/inference_serialization.cpp:902-1080, plus Engine::load).  Tensors may
+ * be <f4, <f2, <i4, or <u2 holding bf16 bit patterns; floating tensors are
+ * converted to the config's dtype with MuNet's codecs. */
+int mh_engine_create_from_artifact(mh_engine **engine, const char *path, int device);
 /* Copy one parameter (host storage bits of `dtype`, MuNet layout) into the
  * engine; weights are packed for the kernels at compile time. */
 int mh_engine_set_param(mh_engine *engine, const char *name, const void *host_data, size_t bytes, int dtype);

@@ -75,6 +75,7 @@ _SIGS = {
     # engine (include/munet_hip_engine.h)
     "mh_engine_create": [ctypes.POINTER(_vp), ctypes.c_char_p, _i],
     "mh_engine_destroy": [_vp],
+    "mh_engine_create_from_artifact": [ctypes.POINTER(_vp), ctypes.c_char_p, _i],
     "mh_engine_set_param": [_vp, ctypes.c_char_p, _vp, _sz, _i],
     "mh_engine_compile": [_vp, _ip, _i],
     "mh_engine_input_ptr": [_vp, ctypes.POINTER(_vp)],

@@ -812,8 +812,35 @@ int mh_engine_set_param(mh_engine *e, const char *name, const void *data, size_t
     if (!e || !name || (!data && bytes)) throw Error("null argument");
     if (e->impl.compiled) throw Error("parameters must be set before compile");
     mh::Param p;
-    p.dt = dtype;
-    p.host.assign(static_cast<const uint8_t *>(data), static_cast<const uint8_t *>(data) + bytes);
+    const int edt = e->impl.dt;
+    const bool fl = dtype == mh::F32 || dtype == mh::F16 || dtype == mh::BF16;
+    if (fl && dtype != edt) {
+      // another floating dtype: convert to the engine's with MuNet's codecs,
+      // as the reference's loader does with Tensor::to (src/tensor.cpp:249-284)
+      const size_t ies = mh::dt_size(dtype), n = bytes / ies;
+      if (n * ies != bytes) throw Error(std::string("parameter '") + name + "' has a ragged byte size");
+      const uint8_t *src = static_cast<const uint8_t *>(data);
+      p.host.resize(n * mh::dt_size(edt));
+      for (size_t i = 0; i < n; ++i) {
+        float v;
+        if (dtype == mh::F32) std::memcpy(&v, src + 4 * i, 4);
+        else {
+          uint16_t h;
+          std::memcpy(&h, src + 2 * i, 2);
+          v = dtype == mh::F16 ? mh::host_f16_to_f32(h) : mh::host_bf16_to_f32(h);
+        }
+        if (edt == mh::F32) {
+          std::memcpy(&p.host[4 * i], &v, 4);
+        } else {
+          const uint16_t h = edt == mh::F16 ? mh::host_f32_to_f16(v) : mh::host_f32_to_bf16(v);
+          std::memcpy(&p.host[2 * i], &h, 2);
+        }
+      }
+      p.dt = edt;
+    } else {
+      p.dt = dtype;
+      p.host.assign(static_cast<const uint8_t *>(data), static_cast<const uint8_t *>(data) + bytes);
+    }
     e->impl.params[name] = std::move(p);
   })
 }

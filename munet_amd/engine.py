@@ -5,6 +5,10 @@ Mirrors ``inference::Engine`` (reference src/inference.hpp:292-801):
 * ``Engine.load(config, params)`` - module config in the reference's
   serialized schema (src/inference_serialization.cpp:762-860) and parameters
   by ``named_parameters`` name (src/core/module.hpp:95-107);
+* ``Engine.load_artifact(path)`` - the same from a MuNet deploy artifact
+  (``munet_model`` rev-1 .npz, reference inference::load_serialized,
+  src/inference_serialization.cpp:902-1080), parsed and validated in
+  libmunet_hip.so;
 * ``compile(example_input)`` - exact shape contract; traces, fuses, plans the
   arena and captures the forward as a hipGraph (src/inference.hpp:446-537);
 * ``run(x)`` - host input in storage format -> host output
@@ -47,6 +51,15 @@ class Engine:
             a = np.ascontiguousarray(arr)
             _lib.call("mh_engine_set_param", h, name.encode(), a.ctypes.data_as(_vp), a.nbytes, dt)
         del lib
+        return self
+
+    def load_artifact(self, path: str):
+        h = _vp()
+        _lib.call("mh_engine_create_from_artifact", ctypes.byref(h), str(path).encode(), self.device)
+        self._h = h
+        # the config is read again here only for the output dtype on the host
+        with np.load(path, allow_pickle=False) as z:
+            self.config = json.loads(str(z["__config__"]))
         return self
 
     # -- compile ------------------------------------------------------------

@@ -1,0 +1,138 @@
+"""Deploy-artifact loader (mh_engine_create_from_artifact) on plan-only
+engines (no GPU): the reference's `munet_model` rev-1 .npz format and its
+validations (src/inference_serialization.cpp:902-1080), bf16 tensors as <u2
+bit patterns, and dtype conversion into the config's dtype."""
+import json
+import zipfile
+
+import numpy as np
+import pytest
+
+from munet_amd import _lib, models, synth
+from munet_amd.artifact import save_deploy_artifact
+from munet_amd.engine import Engine
+
+
+def _params(cfg, scheme):
+    return models.init_params(cfg, scheme, scope="artifact")
+
+
+def _decoder():
+    return models.decoder_config(vocab=500, ctx=64, d_model=64, num_heads=2, num_layers=2, ffn=128,
+                                 dtype="bfloat16")
+
+
+def _plan_json(e):
+    p = e.plan()
+    return json.dumps(p["ops"], sort_keys=True), p["arena_bytes"]
+
+
+@pytest.mark.parametrize("which", ["mlp", "decoder"])
+def test_artifact_round_trip_plan(tmp_path, which):
+    cfg, scheme, shape = ((models.mlp_config(), "mlp", (8, 784)) if which == "mlp"
+                          else (_decoder(), "gpt", (2, 64)))
+    params = _params(cfg, scheme)
+    path = tmp_path / "model.npz"
+    save_deploy_artifact(str(path), cfg, params)
+    a = Engine(device=-1).load_artifact(str(path)).compile(shape)
+    b = Engine(device=-1).load(cfg, params).compile(shape)
+    assert _plan_json(a) == _plan_json(b)
+    assert a.out_shape == b.out_shape
+    assert a.config == cfg
+
+
+def test_bf16_members_are_u2_bit_patterns(tmp_path):
+    cfg = _decoder()
+    params = _params(cfg, "gpt")
+    path = tmp_path / "m.npz"
+    save_deploy_artifact(str(path), cfg, params)
+    with np.load(str(path), allow_pickle=False) as z:
+        w = z["blocks.0.ff.0.weight"]
+        assert w.dtype == np.dtype("<u2")
+        assert np.array_equal(w, params["blocks.0.ff.0.weight"])
+        assert json.loads(str(z["__tensor_names__"])) == sorted(params)
+
+
+def _write(path, state):
+    with open(path, "wb") as f:
+        np.savez(f, **state)
+
+
+def _good_state(cfg, params):
+    """A minimal valid artifact's members (metadata the reference requires)."""
+    state = dict(params)
+    state.update({
+        "__config__": np.array(json.dumps(cfg)),
+        "__format_name__": np.array("munet_model"),
+        "__format_revision__": np.array(1, dtype=np.int64),
+        "__artifact_kind__": np.array("deploy_model"),
+        "__artifact_scope__": np.array("runtime_only"),
+        "__default_load_mode__": np.array("eval"),
+        "__contains_training_state__": np.array(False),
+        "__recommended_loader__": np.array("load_for_inference"),
+        "__compile_contract_policy__": np.array("external"),
+    })
+    return state
+
+
+@pytest.mark.parametrize("change,msg", [
+    (lambda s: s.update(__format_name__=np.array("other")), "format name"),
+    (lambda s: s.update(__format_revision__=np.array(2, dtype=np.int64)), "revision"),
+    (lambda s: s.update(__artifact_kind__=np.array("training_checkpoint")), "artifact kind"),
+    (lambda s: s.update(__artifact_scope__=np.array("training+inference")), "artifact scope"),
+    (lambda s: s.update(__default_load_mode__=np.array("train")), "load mode"),
+    (lambda s: s.update(__contains_training_state__=np.array(True)), "training state"),
+    (lambda s: s.update(__recommended_loader__=np.array("load_checkpoint")), "recommended loader"),
+    (lambda s: s.update(__compile_contract_policy__=np.array("dynamic")), "compile contract"),
+    (lambda s: s.pop("__config__"), "__config__"),
+    (lambda s: s.update({"optimizer.state": np.zeros(3, np.float32)}), "training state"),
+    (lambda s: s.update(__tensor_names__=np.array(json.dumps(["a"]))), "manifest"),
+    (lambda s: s.update(__producer__=np.array("someone_else")), "producer"),
+    (lambda s: s.update({"0.weight": np.zeros((784, 256), np.float64)}), "unsupported dtype"),
+])
+def test_artifact_validation(tmp_path, change, msg):
+    cfg = models.mlp_config()
+    state = _good_state(cfg, _params(cfg, "mlp"))
+    change(state)
+    path = tmp_path / "bad.npz"
+    _write(path, state)
+    with pytest.raises(_lib.HipError, match=msg):
+        Engine(device=-1).load_artifact(str(path))
+
+
+def test_compressed_members_are_rejected(tmp_path):
+    cfg = models.mlp_config()
+    path = tmp_path / "c.npz"
+    with open(path, "wb") as f:
+        np.savez_compressed(f, **_good_state(cfg, _params(cfg, "mlp")))
+    with pytest.raises(_lib.HipError, match="compressed"):
+        Engine(device=-1).load_artifact(str(path))
+
+
+def test_not_a_zip(tmp_path):
+    path = tmp_path / "x.npz"
+    path.write_bytes(b"\x00" * 100)
+    with pytest.raises(_lib.HipError, match="central directory"):
+        Engine(device=-1).load_artifact(str(path))
+
+
+def test_accepts_writer_producers(tmp_path):
+    """The reference's Python writers tag 'munet_nn' / 'munet_pytorch_interop'."""
+    cfg = models.mlp_config()
+    for prod in ("munet", "munet_nn", "munet_pytorch_interop"):
+        state = _good_state(cfg, _params(cfg, "mlp"))
+        state["__producer__"] = np.array(prod)
+        path = tmp_path / f"{prod}.npz"
+        _write(path, state)
+        Engine(device=-1).load_artifact(str(path)).compile((4, 784))
+
+
+def test_zip64_members_parse(tmp_path):
+    """numpy writes every member with ZIP64 local headers; check that is the
+    layout under test and that it loads."""
+    cfg = models.mlp_config()
+    path = tmp_path / "z.npz"
+    save_deploy_artifact(str(path), cfg, _params(cfg, "mlp"))
+    with zipfile.ZipFile(path) as z:
+        assert all(i.compress_type == zipfile.ZIP_STORED for i in z.infolist())
+    Engine(device=-1).load_artifact(str(path)).compile((4, 784))

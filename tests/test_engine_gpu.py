@@ -140,3 +140,27 @@ def test_engine_bad_token_raises():
         eng.run(ids)
     ids[0, 3] = 5
     eng.run(ids)  # the error flag was cleared
+
+
+def test_decoder_from_deploy_artifact(tmp_path):
+    """An engine built from a deploy artifact (bf16 members as <u2 bits)
+    computes exactly what the same engine loaded from the parameter dict
+    does; an fp32 artifact loaded into a bf16 config is encoded with the
+    reference's bf16 codec (round-to-nearest-even) on the host."""
+    from munet_amd.artifact import save_deploy_artifact
+    cfg = models.decoder_config(vocab=1000, ctx=128, d_model=256, num_heads=4, num_layers=2, ffn=1024,
+                                dtype="bfloat16")
+    params = models.init_params(cfg, "gpt", scope="art")
+    ids = models.make_input(cfg, (2, 128), "gpt", scope="art_in")
+    ref = Engine(0).load(cfg, params).compile((2, 128)).run(ids)
+    path = tmp_path / "gpt_bf16.npz"
+    save_deploy_artifact(str(path), cfg, params)
+    y = Engine(0).load_artifact(str(path)).compile((2, 128)).run(ids)
+    assert np.array_equal(y, ref)
+    # fp32 tensors into the bf16 model: decode the bf16 weights to fp32 (exact),
+    # write them as <f4, load: the loader's RNE encode restores the same bits
+    p32 = {k: synth.decode(v, synth.BF16) for k, v in params.items()}
+    path32 = tmp_path / "gpt_f32.npz"
+    save_deploy_artifact(str(path32), cfg, p32, dtype="float32")
+    y32 = Engine(0).load_artifact(str(path32)).compile((2, 128)).run(ids)
+    assert np.array_equal(y32, ref)
