@@ -64,6 +64,38 @@ int mh_engine_launch(mh_engine *engine);
 int mh_engine_stream(mh_engine *engine, void **stream);
 /* EngineStats as a JSON object. */
 int mh_engine_stats(mh_engine *engine, char *buf, size_t len);
+/* ---- caller features of the reference Engine ----------------------------
+ * Compile with an expected input shape whose -1 entries are wildcards
+ * (reference Engine::compile(example, expected_input_shape) and ShapeContract,
+ * src/inference.hpp:128-184, 446-537).  Runs on other shapes that satisfy the
+ * contract compile one more graph instance per concrete shape on first use;
+ * all instances share the weight arena. */
+int mh_engine_compile_expected(mh_engine *engine, const int *example_shape, int ndim, const int *expected_shape);
+/* Output shape for an input shape (compiles its instance if needed). */
+int mh_engine_output_shape_for(mh_engine *engine, const int *input_shape, int ndim, int *out_shape, int *out_ndim);
+/* Host-to-host forward for an input of the given shape (contract-checked). */
+int mh_engine_run_shaped(mh_engine *engine, const void *host_input, const int *shape, int ndim, void *host_output);
+/* Forward through the prepared-input cache (reference PreparedInputCache and
+ * prepare_input, src/inference.hpp:186-289, 665-686): `key` identifies the
+ * caller's input tensor and `version` its mutation count; a hit reuses the
+ * device copy made on a miss. */
+int mh_engine_run_cached(mh_engine *engine, const void *host_input, uint64_t key, uint64_t version,
+                         void *host_output);
+/* Cache capacity (EngineConfig prepared_input_cache_entries / _max_bytes,
+ * defaults 8 and 64 MiB); clears the cache. */
+int mh_engine_set_input_cache(mh_engine *engine, size_t max_entries, size_t max_bytes);
+int mh_engine_clear_input_cache(mh_engine *engine);
+/* run_batch_into (src/inference.hpp:618-627): n host inputs -> n host outputs. */
+int mh_engine_run_batch(mh_engine *engine, int n, const void *const *host_inputs, void *const *host_outputs);
+/* Observer (EngineObserver / EngineEvent, src/inference.hpp:68-94): called
+ * with one JSON object per CompileStarted / CompileCompleted / RunStarted /
+ * RunCompleted / Error event; NULL removes it. */
+typedef void (*mh_engine_observer)(const char *event_json, void *user);
+int mh_engine_set_observer(mh_engine *engine, mh_engine_observer fn, void *user);
+/* Pinned host staging for the PCIe path: the engine's page-locked input and
+ * output buffers (allocated on first call) and a forward between them. */
+int mh_engine_pinned_io(mh_engine *engine, void **host_input, void **host_output);
+int mh_engine_run_pinned(mh_engine *engine);
 /* The compiled plan (ops, fused epilogues, arena offsets) as JSON. */
 int mh_engine_plan(mh_engine *engine, char *buf, size_t len);
 

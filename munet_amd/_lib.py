@@ -87,6 +87,16 @@ _SIGS = {
     "mh_engine_stats": [_vp, ctypes.c_char_p, _sz],
     "mh_engine_plan": [_vp, ctypes.c_char_p, _sz],
     "mh_engine_stream": [_vp, ctypes.POINTER(_vp)],
+    "mh_engine_compile_expected": [_vp, _ip, _i, _ip],
+    "mh_engine_output_shape_for": [_vp, _ip, _i, _ip, _ip],
+    "mh_engine_run_shaped": [_vp, _vp, _ip, _i, _vp],
+    "mh_engine_run_cached": [_vp, _vp, ctypes.c_uint64, ctypes.c_uint64, _vp],
+    "mh_engine_set_input_cache": [_vp, _sz, _sz],
+    "mh_engine_clear_input_cache": [_vp],
+    "mh_engine_run_batch": [_vp, _i, ctypes.POINTER(_vp), ctypes.POINTER(_vp)],
+    "mh_engine_set_observer": [_vp, _vp, _vp],
+    "mh_engine_pinned_io": [_vp, ctypes.POINTER(_vp), ctypes.POINTER(_vp)],
+    "mh_engine_run_pinned": [_vp],
 }
 _RESTYPES = {
     "mh_last_error": ctypes.c_char_p,

@@ -104,6 +104,14 @@ struct EngineImpl {
   bool plan_only = false;
   int dt = F32;
   std::map<std::string, Param> params;
+  // Instances compiled for further input shapes read the primary instance's
+  // parameters and weight arena (the packed weights do not depend on the
+  // input shape): pp points at the owning map, shared_wbuf at its arena.
+  const std::map<std::string, Param> *pp = &params;
+  char *shared_wbuf = nullptr;
+  size_t shared_wbytes = 0;
+  // pinned host staging for the PCIe path (allocated on first use)
+  void *pin_in = nullptr, *pin_out = nullptr;
 
   std::vector<Val> vals;
   std::vector<Op> ops;
@@ -131,7 +139,9 @@ struct EngineImpl {
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
     if (arena) (void)hipFree(arena);
-    if (wbuf) (void)hipFree(wbuf);
+    if (wbuf && wbuf != shared_wbuf) (void)hipFree(wbuf);
+    if (pin_in) (void)hipHostFree(pin_in);
+    if (pin_out) (void)hipHostFree(pin_out);
     if (ev0) (void)hipEventDestroy(ev0);
     if (ev1) (void)hipEventDestroy(ev1);
     if (stream) (void)hipStreamDestroy(stream);
@@ -177,8 +187,8 @@ struct EngineImpl {
 
   // ---------------------------------------------------------------- params
   const Param &param(const std::string &n) const {
-    auto it = params.find(n);
-    if (it == params.end()) throw Error("missing parameter '" + n + "'");
+    auto it = pp->find(n);
+    if (it == pp->end()) throw Error("missing parameter '" + n + "'");
     if (it->second.dt != dt) throw Error("parameter '" + n + "' has the wrong dtype");
     return it->second;
   }
@@ -222,8 +232,8 @@ struct EngineImpl {
     return t;
   }
   const void *bias_or_zero(const std::string &n, int len) {
-    auto it = params.find(n);
-    if (it != params.end()) return upload(it->second.host);
+    auto it = pp->find(n);
+    if (it != pp->end()) return upload(it->second.host);
     return upload(std::vector<uint8_t>(size_t(len) * dt_size(dt), 0));
   }
 
@@ -662,9 +672,15 @@ struct EngineImpl {
       hip_check(hipEventCreate(&ev0), "hipEventCreate");
       hip_check(hipEventCreate(&ev1), "hipEventCreate");
       hip_check(hipMalloc(&arena, std::max<size_t>(arena_bytes, 256)), "hipMalloc(arena)");
-      hip_check(hipMalloc(&wbuf, std::max<size_t>(wbytes, 256)), "hipMalloc(weights)");
-      for (auto &p : wpending)
-        hip_check(hipMemcpy(wbuf + p.second, p.first.data(), p.first.size(), hipMemcpyHostToDevice), "upload weights");
+      if (shared_wbuf) {
+        if (wbytes != shared_wbytes) throw Error("engine: weight layout differs between input shapes");
+        wbuf = shared_wbuf;
+      } else {
+        hip_check(hipMalloc(&wbuf, std::max<size_t>(wbytes, 256)), "hipMalloc(weights)");
+        for (auto &p : wpending)
+          hip_check(hipMemcpy(wbuf + p.second, p.first.data(), p.first.size(), hipMemcpyHostToDevice),
+                    "upload weights");
+      }
       wpending.clear();
       wpending.shrink_to_fit();
       (void)device_error_flag();
@@ -712,20 +728,48 @@ struct EngineImpl {
     ++runs;
   }
 
-  void run(const void *hin, void *hout) {
-    require_device();
-    const auto t0 = std::chrono::steady_clock::now();
-    hip_check(hipMemcpyAsync(dptr(input), hin, vals[input].bytes(), hipMemcpyHostToDevice, stream), "input H2D");
-    run_device();
-    hip_check(hipMemcpyAsync(hout, dptr(output), vals[output].bytes(), hipMemcpyDeviceToHost, stream), "output D2H");
-    hip_check(hipStreamSynchronize(stream), "output D2H");
+  void check_error_flag() {
     int flag = 0;
     hip_check(hipMemcpy(&flag, device_error_flag(), sizeof(int), hipMemcpyDeviceToHost), "error flag");
     if (flag) {
       hip_check(hipMemset(device_error_flag(), 0, sizeof(int)), "clear error flag");
       throw Error("Embedding index out of range");
     }
+  }
+
+  // Host input -> device (hin == nullptr: the input buffer already holds it).
+  double last_prepare_ms = 0;
+  void stage_input(const void *hin) {
+    const auto t0 = std::chrono::steady_clock::now();
+    if (hin) hip_check(hipMemcpyAsync(dptr(input), hin, vals[input].bytes(), hipMemcpyHostToDevice, stream), "input H2D");
+    last_prepare_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  }
+
+  void run(const void *hin, void *hout) {
+    require_device();
+    const auto t0 = std::chrono::steady_clock::now();
+    stage_input(hin);
+    run_device();
+    hip_check(hipMemcpyAsync(hout, dptr(output), vals[output].bytes(), hipMemcpyDeviceToHost, stream), "output D2H");
+    hip_check(hipStreamSynchronize(stream), "output D2H");
+    check_error_flag();
     last_run_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  }
+
+  // Pinned host staging buffers sized to the input and the output.
+  void pinned(void **in, void **out) {
+    require_device();
+    if (!pin_in) hip_check(hipHostMalloc(&pin_in, std::max<size_t>(vals[input].bytes(), 64), hipHostMallocDefault), "hipHostMalloc(input)");
+    if (!pin_out) hip_check(hipHostMalloc(&pin_out, std::max<size_t>(vals[output].bytes(), 64), hipHostMallocDefault), "hipHostMalloc(output)");
+    *in = pin_in;
+    *out = pin_out;
+  }
+
+  // Forward from the pinned input staging buffer into the pinned output one.
+  void run_pinned() {
+    void *pi, *po;
+    pinned(&pi, &po);
+    run(pi, po);
   }
 
   std::string stats_json() const {
@@ -766,8 +810,191 @@ struct EngineImpl {
 
 }  // namespace mh
 
+// The engine handle: the primary compiled instance plus the caller-side
+// features of the reference Engine (src/inference.hpp:31-41, 128-289,
+// 446-627): an input shape contract with -1 wildcards served by one compiled
+// instance per concrete shape, the prepared-input cache, batch runs, an
+// observer and EngineStats.
 struct mh_engine {
-  mh::EngineImpl impl;
+  mh::EngineImpl impl;  // primary instance: owns the config, parameters and weights
+
+  // input shape contract (reference ShapeContract): empty = exact, else -1 wildcards
+  std::vector<int> expected;
+  std::map<std::vector<int>, std::unique_ptr<mh::EngineImpl>> shapes;  // further instances
+
+  // prepared-input cache (reference PreparedInputCache): device copies of host
+  // inputs keyed by the caller's tensor identity and version, FIFO eviction
+  struct Prepared {
+    uint64_t key = 0, version = 0;
+    size_t bytes = 0;
+    void *dev = nullptr;
+  };
+  std::vector<Prepared> cache;
+  size_t cache_max_entries = 8, cache_max_bytes = size_t(64) << 20, cache_bytes = 0;
+  size_t cache_hits = 0, cache_misses = 0, cache_evictions = 0;
+
+  mh_engine_observer observer = nullptr;
+  void *observer_user = nullptr;
+  size_t runs = 0;
+  double last_run_ms = 0, last_prepare_ms = 0, last_forward_ms = 0, last_validate_ms = 0;
+
+  ~mh_engine() { clear_cache(); }
+
+  void clear_cache() {
+    for (auto &c : cache)
+      if (c.dev) (void)hipFree(c.dev);
+    cache.clear();
+    cache_bytes = 0;
+  }
+
+  std::string mismatch(const std::vector<int> &actual) const {
+    const std::vector<int> want = expected.empty() ? std::vector<int>(impl.in_shape.begin(), impl.in_shape.end()) : expected;
+    if (actual.size() != want.size()) return "rank mismatch";
+    for (size_t i = 0; i < want.size(); ++i)
+      if (want[i] != -1 && want[i] != actual[i]) return "dim mismatch at index " + std::to_string(i);
+    return {};
+  }
+
+  // The instance compiled for `shape` (compiled on first use).
+  mh::EngineImpl &instance(const std::vector<int> &shape) {
+    if (!impl.compiled) throw mh::Error("engine is not compiled");
+    if (std::vector<int>(impl.in_shape.begin(), impl.in_shape.end()) == shape) return impl;
+    const std::string why = mismatch(shape);
+    if (!why.empty()) throw mh::Error("Engine: input shape mismatch with compiled shape: " + why);
+    auto it = shapes.find(shape);
+    if (it != shapes.end()) return *it->second;
+    auto inst = std::make_unique<mh::EngineImpl>();
+    inst->cfg = impl.cfg;
+    inst->dt = impl.dt;
+    inst->device = impl.device;
+    inst->plan_only = impl.plan_only;
+    inst->pp = &impl.params;
+    inst->shared_wbuf = impl.wbuf;
+    inst->shared_wbytes = impl.wbytes;
+    emit("CompileStarted", 0.0, shape, {}, "compiling an instance for a new input shape");
+    inst->compile(mh::Shape(shape.begin(), shape.end()));
+    const auto &os = inst->vals[inst->output].shape;
+    emit("CompileCompleted", inst->compile_ms, shape, std::vector<int>(os.begin(), os.end()), "instance compiled");
+    return *(shapes[shape] = std::move(inst));
+  }
+
+  static std::string json_str(const std::string &v) {
+    std::string o = "\"";
+    for (char c : v) {
+      if (c == '"' || c == '\\') o += '\\';
+      o += (c == '\n') ? ' ' : c;
+    }
+    return o + "\"";
+  }
+  static std::string json_shape(const std::vector<int> &s) {
+    std::string o = "[";
+    for (size_t i = 0; i < s.size(); ++i) o += (i ? "," : "") + std::to_string(s[i]);
+    return o + "]";
+  }
+  size_t memory_bytes() const {
+    size_t b = impl.arena_bytes + impl.wbytes + cache_bytes;
+    for (const auto &kv : shapes) b += kv.second->arena_bytes;
+    return b;
+  }
+
+  // Observer callback (reference EngineEvent, src/inference.hpp:68-94) as JSON.
+  void emit(const char *type, double ms, const std::vector<int> &in, const std::vector<int> &out,
+            const std::string &msg) const {
+    if (!observer) return;
+    std::ostringstream s;
+    s << "{\"type\":\"" << type << "\",\"device\":" << impl.device << ",\"run_index\":" << runs
+      << ",\"duration_ms\":" << ms << ",\"input_shape\":" << json_shape(in) << ",\"output_shape\":" << json_shape(out)
+      << ",\"current_memory_bytes\":" << memory_bytes() << ",\"peak_memory_bytes\":" << memory_bytes()
+      << ",\"message\":" << json_str(msg) << "}";
+    observer(s.str().c_str(), observer_user);
+  }
+
+  // One forward on the instance for `shape`; `hin` host input (or nullptr when
+  // `dev_in` holds a prepared device copy), `hout` host output.
+  void run_one(const std::vector<int> &shape, const void *hin, const void *dev_in, void *hout) {
+    const auto t0 = std::chrono::steady_clock::now();
+    mh::EngineImpl &e = instance(shape);
+    e.require_device();
+    const std::vector<int> os(e.vals[e.output].shape.begin(), e.vals[e.output].shape.end());
+    emit("RunStarted", 0.0, shape, {}, "Starting inference run");
+    try {
+      const auto tp = std::chrono::steady_clock::now();
+      if (dev_in)
+        mh::hip_check(hipMemcpyAsync(e.dptr(e.input), dev_in, e.vals[e.input].bytes(), hipMemcpyDeviceToDevice, e.stream),
+                      "prepared input D2D");
+      else
+        e.stage_input(hin);
+      last_prepare_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - tp).count();
+      e.run_device();
+      last_forward_ms = e.last_gpu_ms;
+      const auto tv = std::chrono::steady_clock::now();
+      mh::hip_check(hipMemcpyAsync(hout, e.dptr(e.output), e.vals[e.output].bytes(), hipMemcpyDeviceToHost, e.stream),
+                    "output D2H");
+      mh::hip_check(hipStreamSynchronize(e.stream), "output D2H");
+      e.check_error_flag();
+      last_validate_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - tv).count();
+    } catch (const std::exception &ex) {
+      emit("Error", 0.0, shape, {}, std::string("run failed: ") + ex.what());
+      throw;
+    }
+    ++runs;
+    last_run_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    emit("RunCompleted", last_run_ms, shape, os, "Inference run completed");
+  }
+
+  // Reference Engine::prepare_input with the prepared-input cache
+  // (src/inference.hpp:665-686, cache src/inference.hpp:186-289).
+  const void *prepared(const void *hin, size_t bytes, uint64_t key, uint64_t version) {
+    for (const auto &c : cache)
+      if (c.key == key && c.version == version && c.bytes == bytes) {
+        ++cache_hits;
+        return c.dev;
+      }
+    ++cache_misses;
+    if (cache_max_entries == 0 || cache_max_bytes == 0 || bytes > cache_max_bytes) return nullptr;
+    for (auto it = cache.begin(); it != cache.end(); ++it)
+      if (it->key == key) {  // same tensor, stale version: replace
+        cache_bytes -= it->bytes;
+        (void)hipFree(it->dev);
+        cache.erase(it);
+        break;
+      }
+    while (!cache.empty() && (cache.size() >= cache_max_entries || cache_bytes + bytes > cache_max_bytes)) {
+      cache_bytes -= cache.front().bytes;
+      (void)hipFree(cache.front().dev);
+      cache.erase(cache.begin());
+      ++cache_evictions;
+    }
+    Prepared c;
+    c.key = key;
+    c.version = version;
+    c.bytes = bytes;
+    mh::hip_check(hipMalloc(&c.dev, std::max<size_t>(bytes, 16)), "hipMalloc(prepared input)");
+    mh::hip_check(hipMemcpy(c.dev, hin, bytes, hipMemcpyHostToDevice), "prepared input H2D");
+    cache.push_back(c);
+    cache_bytes += bytes;
+    return cache.back().dev;
+  }
+
+  std::string stats_json() const {
+    std::string s = impl.stats_json();
+    // runs over every compiled instance (device-resident launches included)
+    size_t total = impl.runs;
+    for (const auto &kv : shapes) total += kv.second->runs;
+    const std::string first = "{\"runs\":" + std::to_string(impl.runs);
+    s = "{\"runs\":" + std::to_string(total) + s.substr(first.size());
+    std::ostringstream x;
+    x << ",\"host_runs\":" << runs << ",\"engine_last_run_ms\":" << last_run_ms
+      << ",\"last_prepare_input_ms\":" << last_prepare_ms << ",\"last_forward_ms\":" << last_forward_ms
+      << ",\"last_output_validation_ms\":" << last_validate_ms << ",\"compiled_instances\":" << (1 + shapes.size())
+      << ",\"expected_input_shape\":" << json_shape(expected) << ",\"prepared_input_cache_entries\":" << cache.size()
+      << ",\"prepared_input_cache_bytes\":" << cache_bytes << ",\"prepared_input_cache_hits\":" << cache_hits
+      << ",\"prepared_input_cache_misses\":" << cache_misses
+      << ",\"prepared_input_cache_evictions\":" << cache_evictions << ",\"engine_memory_bytes\":" << memory_bytes()
+      << "}";
+    // the primary instance's object minus its closing brace, then the engine's fields
+    return s.substr(0, s.size() - 1) + x.str();
+  }
 };
 
 using mh::Error;
@@ -875,7 +1102,94 @@ int mh_engine_output_shape(mh_engine *e, int *shape, int *ndim) {
   })
 }
 
-int mh_engine_run(mh_engine *e, const void *in, void *out) { ENG_TRY(e->impl.run(in, out)) }
+int mh_engine_run(mh_engine *e, const void *in, void *out) {
+  ENG_TRY({
+    if (!e->impl.compiled) throw Error("engine is not compiled");
+    e->run_one(std::vector<int>(e->impl.in_shape.begin(), e->impl.in_shape.end()), in, nullptr, out);
+  })
+}
+
+int mh_engine_compile_expected(mh_engine *e, const int *shape, int ndim, const int *expected) {
+  ENG_TRY({
+    if (!e || !shape || !expected || ndim <= 0) throw Error("bad input shape");
+    for (int i = 0; i < ndim; ++i)
+      if (expected[i] != -1 && expected[i] != shape[i])
+        throw Error("Engine: compile expected_input_shape mismatch: dim mismatch at index " + std::to_string(i));
+    const auto t0 = std::chrono::steady_clock::now();
+    e->emit("CompileStarted", 0.0, std::vector<int>(shape, shape + ndim), {}, "Starting compile");
+    try {
+      e->impl.compile(mh::Shape(shape, shape + ndim));
+    } catch (const std::exception &ex) {
+      e->emit("Error", 0.0, std::vector<int>(shape, shape + ndim), {}, std::string("compile failed: ") + ex.what());
+      throw;
+    }
+    e->expected.assign(expected, expected + ndim);
+    const auto &os = e->impl.vals[e->impl.output].shape;
+    e->emit("CompileCompleted", std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count(),
+            std::vector<int>(shape, shape + ndim), std::vector<int>(os.begin(), os.end()), "Inference compile completed");
+  })
+}
+
+int mh_engine_output_shape_for(mh_engine *e, const int *shape, int ndim, int *out_shape, int *out_ndim) {
+  ENG_TRY({
+    if (!e || !shape || ndim <= 0 || !out_shape || !out_ndim) throw Error("bad argument");
+    const mh::EngineImpl &inst = e->instance(std::vector<int>(shape, shape + ndim));
+    const auto &s = inst.vals[inst.output].shape;
+    *out_ndim = int(s.size());
+    for (size_t i = 0; i < s.size(); ++i) out_shape[i] = s[i];
+  })
+}
+
+int mh_engine_run_shaped(mh_engine *e, const void *in, const int *shape, int ndim, void *out) {
+  ENG_TRY({
+    if (!e || !shape || ndim <= 0) throw Error("bad input shape");
+    e->run_one(std::vector<int>(shape, shape + ndim), in, nullptr, out);
+  })
+}
+
+int mh_engine_run_cached(mh_engine *e, const void *in, uint64_t key, uint64_t version, void *out) {
+  ENG_TRY({
+    if (!e->impl.compiled) throw Error("engine is not compiled");
+    e->impl.require_device();
+    const void *dev = e->prepared(in, e->impl.vals[e->impl.input].bytes(), key, version);
+    e->run_one(std::vector<int>(e->impl.in_shape.begin(), e->impl.in_shape.end()), in, dev, out);
+  })
+}
+
+int mh_engine_run_batch(mh_engine *e, int n, const void *const *inputs, void *const *outputs) {
+  ENG_TRY({
+    if (n < 0 || (n > 0 && (!inputs || !outputs))) throw Error("bad batch");
+    if (!e->impl.compiled) throw Error("engine is not compiled");
+    const std::vector<int> shape(e->impl.in_shape.begin(), e->impl.in_shape.end());
+    for (int i = 0; i < n; ++i) e->run_one(shape, inputs[i], nullptr, outputs[i]);
+  })
+}
+
+int mh_engine_set_input_cache(mh_engine *e, size_t max_entries, size_t max_bytes) {
+  ENG_TRY({
+    e->cache_max_entries = max_entries;
+    e->cache_max_bytes = max_bytes;
+    e->clear_cache();
+  })
+}
+
+int mh_engine_clear_input_cache(mh_engine *e) { ENG_TRY(e->clear_cache()) }
+
+int mh_engine_set_observer(mh_engine *e, mh_engine_observer fn, void *user) {
+  ENG_TRY({
+    e->observer = fn;
+    e->observer_user = user;
+  })
+}
+
+int mh_engine_pinned_io(mh_engine *e, void **in, void **out) { ENG_TRY(e->impl.pinned(in, out)) }
+int mh_engine_run_pinned(mh_engine *e) {
+  ENG_TRY({
+    void *pi, *po;
+    e->impl.pinned(&pi, &po);
+    e->run_one(std::vector<int>(e->impl.in_shape.begin(), e->impl.in_shape.end()), pi, nullptr, po);
+  })
+}
 int mh_engine_run_device(mh_engine *e) { ENG_TRY(e->impl.run_device()) }
 int mh_engine_launch(mh_engine *e) { ENG_TRY(e->impl.launch()) }
 int mh_engine_stream(mh_engine *e, void **s) {
@@ -884,7 +1198,7 @@ int mh_engine_stream(mh_engine *e, void **s) {
     *s = e->impl.stream;
   })
 }
-int mh_engine_stats(mh_engine *e, char *buf, size_t len) { ENG_TRY(put_str(e->impl.stats_json(), buf, len)) }
+int mh_engine_stats(mh_engine *e, char *buf, size_t len) { ENG_TRY(put_str(e->stats_json(), buf, len)) }
 int mh_engine_plan(mh_engine *e, char *buf, size_t len) { ENG_TRY(put_str(e->impl.plan_json(), buf, len)) }
 
 }  // extern "C"

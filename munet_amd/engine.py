@@ -63,9 +63,18 @@ class Engine:
         return self
 
     # -- compile ------------------------------------------------------------
-    def compile(self, example_input_shape):
+    def compile(self, example_input_shape, expected_input_shape=None):
+        """Exact shape contract, or `expected_input_shape` with -1 wildcards:
+        other shapes meeting it get their own compiled instance on first run."""
         shape = [int(s) for s in example_input_shape]
-        _lib.call("mh_engine_compile", self._h, _lib.ints(shape), len(shape))
+        if expected_input_shape is None:
+            _lib.call("mh_engine_compile", self._h, _lib.ints(shape), len(shape))
+        else:
+            exp = [int(s) for s in expected_input_shape]
+            if len(exp) != len(shape):
+                raise ValueError("expected_input_shape rank differs from the example's")
+            _lib.call("mh_engine_compile_expected", self._h, _lib.ints(shape), len(shape), _lib.ints(exp))
+        self.expected = None if expected_input_shape is None else tuple(int(s) for s in expected_input_shape)
         self.in_shape = tuple(shape)
         dims = (ctypes.c_int * 8)()
         nd = ctypes.c_int()
@@ -77,13 +86,80 @@ class Engine:
     def _out_dtype(self):
         return synth.storage_dtype(synth.DTYPE_CODES[self.config.get("dtype", "float32")])
 
+    def output_shape_for(self, input_shape) -> tuple:
+        shape = [int(s) for s in input_shape]
+        dims = (ctypes.c_int * 8)()
+        nd = ctypes.c_int()
+        _lib.call("mh_engine_output_shape_for", self._h, _lib.ints(shape), len(shape), dims, ctypes.byref(nd))
+        return tuple(dims[i] for i in range(nd.value))
+
     def run(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x)
+        if tuple(x.shape) == self.in_shape:
+            out = np.empty(self.out_shape, dtype=self._out_dtype())
+            _lib.call("mh_engine_run", self._h, x.ctypes.data_as(_vp), out.ctypes.data_as(_vp))
+            return out
+        if getattr(self, "expected", None) is None:
+            raise ValueError(f"input shape {tuple(x.shape)} does not match the compiled contract {self.in_shape}")
+        out = np.empty(self.output_shape_for(x.shape), dtype=self._out_dtype())
+        _lib.call("mh_engine_run_shaped", self._h, x.ctypes.data_as(_vp), _lib.ints(x.shape), x.ndim,
+                  out.ctypes.data_as(_vp))
+        return out
+
+    def run_prepared(self, x: np.ndarray, key: int, version: int = 0) -> np.ndarray:
+        """Run through the prepared-input cache: `key` names the caller's input
+        tensor, `version` its mutation count (reference prepare_input)."""
+        x = np.ascontiguousarray(x)
         if tuple(x.shape) != self.in_shape:
             raise ValueError(f"input shape {tuple(x.shape)} does not match the compiled contract {self.in_shape}")
-        x = np.ascontiguousarray(x)
         out = np.empty(self.out_shape, dtype=self._out_dtype())
-        _lib.call("mh_engine_run", self._h, x.ctypes.data_as(_vp), out.ctypes.data_as(_vp))
+        _lib.call("mh_engine_run_cached", self._h, x.ctypes.data_as(_vp), int(key), int(version),
+                  out.ctypes.data_as(_vp))
         return out
+
+    def set_input_cache(self, max_entries: int, max_bytes: int):
+        _lib.call("mh_engine_set_input_cache", self._h, int(max_entries), int(max_bytes))
+
+    def clear_input_cache(self):
+        _lib.call("mh_engine_clear_input_cache", self._h)
+
+    def run_batch(self, xs) -> list:
+        """run_batch_into: one forward per input, in order."""
+        xs = [np.ascontiguousarray(x) for x in xs]
+        for x in xs:
+            if tuple(x.shape) != self.in_shape:
+                raise ValueError(f"input shape {tuple(x.shape)} does not match the compiled contract {self.in_shape}")
+        outs = [np.empty(self.out_shape, dtype=self._out_dtype()) for _ in xs]
+        ins = (_vp * max(1, len(xs)))(*[x.ctypes.data for x in xs])
+        os_ = (_vp * max(1, len(outs)))(*[o.ctypes.data for o in outs])
+        _lib.call("mh_engine_run_batch", self._h, len(xs), ins, os_)
+        return outs
+
+    _OBSERVER = ctypes.CFUNCTYPE(None, ctypes.c_char_p, ctypes.c_void_p)
+
+    def set_observer(self, fn):
+        """fn(event: dict) for each engine event (None removes it)."""
+        if fn is None:
+            self._observer = None
+            _lib.call("mh_engine_set_observer", self._h, None, None)
+            return
+        self._observer = self._OBSERVER(lambda ev, _user: fn(json.loads(ev.decode())))
+        _lib.call("mh_engine_set_observer", self._h, ctypes.cast(self._observer, _vp), None)
+
+    def pinned_io(self):
+        """(input, output) numpy views of the engine's page-locked staging
+        buffers; fill the input, call run_pinned(), read the output."""
+        pi, po = _vp(), _vp()
+        _lib.call("mh_engine_pinned_io", self._h, ctypes.byref(pi), ctypes.byref(po))
+        in_dt = np.int32 if self.config.get("type") in ("DecoderLM", "Embedding") else self._out_dtype()
+        n_in = int(np.prod(self.in_shape)) * np.dtype(in_dt).itemsize
+        n_out = int(np.prod(self.out_shape)) * np.dtype(self._out_dtype()).itemsize
+        a = np.ctypeslib.as_array((ctypes.c_uint8 * n_in).from_address(pi.value)).view(in_dt).reshape(self.in_shape)
+        b = np.ctypeslib.as_array((ctypes.c_uint8 * n_out).from_address(po.value)).view(self._out_dtype())
+        return a, b.reshape(self.out_shape)
+
+    def run_pinned(self):
+        _lib.call("mh_engine_run_pinned", self._h)
 
     def run_device(self):
         _lib.call("mh_engine_run_device", self._h)

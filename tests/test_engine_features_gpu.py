@@ -1,0 +1,92 @@
+"""Engine caller features on the GPU: per-shape instances under a wildcard
+contract, the prepared-input cache, run_batch, the observer's run events and
+the pinned-host staging path, each checked bit-exactly against plain runs of
+an engine compiled for that exact shape (reference src/inference.hpp:31-289,
+538-627)."""
+import numpy as np
+import pytest
+
+from munet_amd import models
+from munet_amd.engine import Engine
+
+pytestmark = pytest.mark.gpu
+
+
+def _mlp():
+    cfg = models.mlp_config()
+    return cfg, models.init_params(cfg, "mlp", scope="feat")
+
+
+def _x(cfg, b, scope):
+    return models.make_input(cfg, (b, 784), "mlp", scope=scope)
+
+
+def test_wildcard_batch_matches_exact_engines():
+    cfg, p = _mlp()
+    e = Engine(0).load(cfg, p).compile((8, 784), expected_input_shape=(-1, 784))
+    for b in (8, 16, 3, 16):
+        x = _x(cfg, b, f"w{b}")
+        ref = Engine(0).load(cfg, p).compile((b, 784)).run(x)
+        assert np.array_equal(e.run(x), ref)
+    assert e.stats()["compiled_instances"] == 3
+
+
+def test_decoder_wildcard_batch():
+    cfg = models.decoder_config(vocab=500, ctx=64, d_model=64, num_heads=2, num_layers=2, ffn=128, dtype="bfloat16")
+    p = models.init_params(cfg, "gpt", scope="featd")
+    e = Engine(0).load(cfg, p).compile((2, 64), expected_input_shape=(-1, 64))
+    for b in (1, 3):
+        ids = models.make_input(cfg, (b, 64), "gpt", scope=f"featd{b}")
+        assert np.array_equal(e.run(ids), Engine(0).load(cfg, p).compile((b, 64)).run(ids))
+
+
+def test_prepared_input_cache():
+    cfg, p = _mlp()
+    e = Engine(0).load(cfg, p).compile((8, 784))
+    x, x2 = _x(cfg, 8, "c1"), _x(cfg, 8, "c2")
+    ref, ref2 = e.run(x), e.run(x2)
+    assert np.array_equal(e.run_prepared(x, key=1, version=0), ref)
+    assert np.array_equal(e.run_prepared(x, key=1, version=0), ref)  # hit: no transfer
+    st = e.stats()
+    assert (st["prepared_input_cache_hits"], st["prepared_input_cache_misses"]) == (1, 1)
+    # a new version of the same tensor is a miss and replaces the entry
+    assert np.array_equal(e.run_prepared(x2, key=1, version=1), ref2)
+    st = e.stats()
+    assert st["prepared_input_cache_misses"] == 2 and st["prepared_input_cache_entries"] == 1
+    # capacity 2: a third tensor evicts the oldest
+    e.set_input_cache(2, 1 << 30)
+    for k in (10, 11, 12):
+        e.run_prepared(x, key=k)
+    st = e.stats()
+    assert st["prepared_input_cache_entries"] == 2 and st["prepared_input_cache_evictions"] == 1
+    # entries larger than the byte budget are not cached
+    e.set_input_cache(8, 16)
+    e.run_prepared(x, key=20)
+    assert e.stats()["prepared_input_cache_entries"] == 0
+
+
+def test_run_batch_and_observer():
+    cfg, p = _mlp()
+    e = Engine(0).load(cfg, p).compile((8, 784))
+    xs = [_x(cfg, 8, f"b{i}") for i in range(3)]
+    events = []
+    e.set_observer(events.append)
+    outs = e.run_batch(xs)
+    for x, o in zip(xs, outs):
+        assert np.array_equal(o, e.run(x))
+    kinds = [ev["type"] for ev in events[:6]]
+    assert kinds == ["RunStarted", "RunCompleted"] * 3
+    assert events[1]["output_shape"] == [8, 10] and events[1]["duration_ms"] > 0
+    assert e.stats()["host_runs"] == 6
+
+
+def test_pinned_io():
+    cfg = models.decoder_config(vocab=500, ctx=64, d_model=64, num_heads=2, num_layers=1, ffn=128, dtype="bfloat16")
+    p = models.init_params(cfg, "gpt", scope="pin")
+    ids = models.make_input(cfg, (2, 64), "gpt", scope="pin_in")
+    e = Engine(0).load(cfg, p).compile((2, 64))
+    ref = e.run(ids)
+    pin_in, pin_out = e.pinned_io()
+    pin_in[...] = ids
+    e.run_pinned()
+    assert np.array_equal(pin_out, ref)
