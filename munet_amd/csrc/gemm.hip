@@ -353,13 +353,13 @@ hipError_t gemm_nt(int dt, const void *A, const void *Bt, int M, int N, int K, l
   if (M <= 0 || N <= 0 || batch <= 0) return hipSuccess;
   if (tile_hint < 0) {
     // MUNET_HIP_GEMM_TILE forces a kernel and block tile for tests and tuning:
-    // 0-6 direct-to-LDS kernel, 100-107 general kernel, 200-202 pipelined kernel.
+    // 0-6 direct-to-LDS kernel, 100-107 general kernel, 200-203 pipelined kernel.
     static const char *force = std::getenv("MUNET_HIP_GEMM_TILE");
     if (force && *force) tile_hint = std::atoi(force);
   }
   // <0: the pipelined 16-bit kernel when the operands allow it, else the
   // general kernel with an automatic tile.
-  const bool pipe = gemm_pipe_ok(dt, A, Bt, K, lda, ldb, sa, sb);
+  const bool pipe = gemm_pipe_ok(dt, A, Bt, M, N, K, lda, ldb, sa, sb);
   if (pipe && (tile_hint < 0 || tile_hint >= 200))
     return gemm_pipe(dt, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile_hint < 0 ? -1 : tile_hint - 200, st);
   if (tile_hint >= 200) tile_hint = -1;

@@ -215,7 +215,9 @@ __device__ __forceinline__ void store_tile(f32x4 (&acc)[FM][FN], float *lds, con
   const int lrow = lane & 15, lgrp = lane >> 4;
   constexpr int LPR = WTN / 4;   // lanes per staged row
   constexpr int RPI = 64 / LPR;  // rows per wave iteration
-  const int rl = lane / LPR, cl = (lane % LPR) * 4;
+  // when LPR does not divide 64 the last lanes have no row of their own (they
+  // would repeat rows of other lanes, which is wrong for in-place residuals)
+  const int rl = lane < RPI * LPR ? lane / LPR : FMP * 16, cl = (lane % LPR) * 4;
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
 #pragma unroll

@@ -5,18 +5,26 @@
 //
 // The hot path of the decoder's Linear layers (bf16/fp16, 16-byte aligned
 // K-contiguous operands).  Differences from the general kernel in gemm.hip:
-//   * prefetch distance 2: slab k+2 is requested from memory while slab k is
-//     multiplied and slab k+1 waits in registers, so every global load has two
-//     K steps of MFMA work to hide behind; LDS is double buffered, one barrier
-//     per K step;
+//   * each 64-wide K step runs in two phases split by the one barrier of the
+//     step.  Phase A multiplies the first 32-wide K half (fragments already in
+//     registers) while it reads the second half's fragments, stores the next
+//     slab (staged in registers) to the other LDS buffer and requests the
+//     slab after it from memory; phase B multiplies the second half while it
+//     reads the next slab's first-half fragments.  __builtin_amdgcn_
+//     sched_group_barrier pins that interleaving, one memory operation after
+//     each MFMA, so every LDS and global access is covered by MFMA work of the
+//     same wave;
 //   * the K loop has no conditional loads: a K % 64 remainder is taken as a
-//     short (zero-padded) first slab, every later slab is whole, and the loop
-//     runs two steps per trip with a peeled tail, so the staging registers
-//     never merge values from different control paths;
+//     short (zero-padded) first slab, every later slab is whole, and the loads
+//     of the last step re-read the last slab, so the staging registers never
+//     merge values from different control paths;
+//   * global loads use 32-bit per-thread offsets from slab base pointers that
+//     advance one slab per step;
 //   * staging registers and LDS use native clang vector types (no struct
 //     copies through private memory);
 //   * the epilogue runs on each accumulator fragment in registers (no LDS
-//     staging): lane (r, g) of a 16x16 fragment owns row r, columns 4g..4g+3.
+//     staging): lane (r, g) of a 16x16 fragment owns row r, columns 4g..4g+3;
+//     its bias and residual loads are issued before the K loop.
 // Built with MFMA results in ordinary VGPRs (see build.py).
 #include "mh_common.hpp"
 #include "mh_kernels.hpp"
@@ -57,7 +65,8 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
   constexpr int NT = WGM * WGN * 64, BK = 64;
   constexpr int WTM = BM / WGM, WTN = BN / WGN, FM = WTM / 16, FN = WTN / 16;
   constexpr int ACH = BM * 8 / NT, BCH = BN * 8 / NT;
-  static_assert(ACH >= 1 && BCH >= 1 && NT % 8 == 0, "tile too small for the thread count");
+  static_assert(ACH >= 1 && BCH >= 1 && BM * 8 % NT == 0 && BN * 8 % NT == 0 && WTM % 16 == 0 && WTN % 16 == 0,
+                "tile does not fit the thread count");
   __shared__ u32x4 lds[2][(BM + BN) * 8];  // [buf][A rows | Bt rows][8 chunks], chunk-swizzled
 
   // ---- tile scheduling: XCD band, then group-M (same order as gemm.hip) ----
@@ -74,125 +83,84 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave / WGN, wn = wave % WGN;
   const int li = lane & 15, lg = lane >> 4;
-  // each thread stages chunk c0 (8 values) of ACH rows of A and BCH rows of Bt;
-  // rows past M / N read the last valid row (their results are not stored)
-  const int c0 = tid & 7;
-  const uint16_t *ap[ACH], *bp[BCH];
-  int ast[ACH], bst[BCH];
+  // each thread stages chunk c0 (8 values) of rows r0 + RSTEP * i of A and Bt;
+  // rows past M / N read the last valid row (their results are not stored).
+  // Offsets are 32-bit element offsets from the slab base pointers As / Bs,
+  // which advance one slab per K step (the host checks they fit).
+  constexpr int RSTEP = NT / 8;
+  const int c0 = tid & 7, r0 = tid >> 3;
+  uint32_t aoff[ACH], boff[BCH];
 #pragma unroll
-  for (int i = 0; i < ACH; ++i) {
-    const int r = (tid + i * NT) >> 3;
-    ap[i] = A + long(min(m0 + r, M - 1)) * lda + c0 * 8;
-    ast[i] = r * 8 + (c0 ^ (r & 7));
-  }
+  for (int i = 0; i < ACH; ++i) aoff[i] = uint32_t(min(m0 + r0 + RSTEP * i, M - 1)) * uint32_t(lda) + c0 * 8;
 #pragma unroll
-  for (int i = 0; i < BCH; ++i) {
-    const int r = (tid + i * NT) >> 3;
-    bp[i] = Bt + long(min(n0 + r, N - 1)) * ldb + c0 * 8;
-    bst[i] = BM * 8 + r * 8 + (c0 ^ (r & 7));
+  for (int i = 0; i < BCH; ++i) boff[i] = uint32_t(min(n0 + r0 + RSTEP * i, N - 1)) * uint32_t(ldb) + c0 * 8;
+  const int sw = r0 * 8 + (c0 ^ (r0 & 7));  // row r0 + RSTEP * i sits at sw + RSTEP * 8 * i
+  const uint16_t *As = A, *Bs = Bt;
+  u32x4 ra[ACH], rb[BCH];
+#define MH_PGLOAD()                                                                                \
+  {                                                                                                \
+    _Pragma("unroll") for (int i = 0; i < ACH; ++i) ra[i] = ldg16(As + aoff[i]);                   \
+    _Pragma("unroll") for (int i = 0; i < BCH; ++i) rb[i] = ldg16(Bs + boff[i]);                   \
   }
-
-  u32x4 ra0[ACH], rb0[BCH], ra1[ACH], rb1[BCH];
-#define MH_PGLOAD(RA, RB)                                                                         \
-  {                                                                                               \
-    _Pragma("unroll") for (int i = 0; i < ACH; ++i) {                                             \
-      RA[i] = ldg16(ap[i]);                                                                       \
-      ap[i] += BK;                                                                                \
-    }                                                                                             \
-    _Pragma("unroll") for (int i = 0; i < BCH; ++i) {                                             \
-      RB[i] = ldg16(bp[i]);                                                                       \
-      bp[i] += BK;                                                                                \
-    }                                                                                             \
-  }
-#define MH_PSTORE(RA, RB, BUF)                                                                    \
-  {                                                                                               \
-    _Pragma("unroll") for (int i = 0; i < ACH; ++i) lds[BUF][ast[i]] = RA[i];                     \
-    _Pragma("unroll") for (int i = 0; i < BCH; ++i) lds[BUF][bst[i]] = RB[i];                     \
+#define MH_PSTORE(L)                                                                               \
+  {                                                                                                \
+    _Pragma("unroll") for (int i = 0; i < ACH; ++i)(L)[sw + RSTEP * 8 * i] = ra[i];                \
+    _Pragma("unroll") for (int i = 0; i < BCH; ++i)(L)[BM * 8 + sw + RSTEP * 8 * i] = rb[i];       \
   }
   f32x4 acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-#define MH_PCOMPUTE(BUF)                                                                          \
-  {                                                                                               \
-    const u32x4 *as = lds[BUF], *bs = lds[BUF] + BM * 8;                                          \
-    _Pragma("unroll") for (int ks = 0; ks < 2; ++ks) {                                            \
-      const int c = ks * 4 + lg;                                                                  \
-      u32x4 af[FM], bf[FN];                                                                       \
-      _Pragma("unroll") for (int i = 0; i < FM; ++i) {                                            \
-        const int r = wm * WTM + i * 16 + li;                                                     \
-        af[i] = as[r * 8 + (c ^ (r & 7))];                                                        \
-      }                                                                                           \
-      _Pragma("unroll") for (int j = 0; j < FN; ++j) {                                            \
-        const int r = wn * WTN + j * 16 + li;                                                     \
-        bf[j] = bs[r * 8 + (c ^ (r & 7))];                                                        \
-      }                                                                                           \
-      _Pragma("unroll") for (int i = 0; i < FM; ++i)                                              \
-        _Pragma("unroll") for (int j = 0; j < FN; ++j) PipeMfma<DT>::mma(acc[i][j], bf[j], af[i]); \
-    }                                                                                             \
+  // fragments of one 32-wide K step: lane (li, lg) holds row li, chunk ks*4+lg
+  u32x4 af0[FM], bf0[FN], af1[FM], bf1[FN];
+#define MH_PFRAG(L, KS, AF, BF)                                                                    \
+  {                                                                                                \
+    const u32x4 *as_ = (L), *bs_ = (L) + BM * 8;                                                   \
+    const int c = (KS) * 4 + lg;                                                                   \
+    _Pragma("unroll") for (int i = 0; i < FM; ++i) {                                               \
+      const int r = wm * WTM + i * 16 + li;                                                        \
+      AF[i] = as_[r * 8 + (c ^ (r & 7))];                                                          \
+    }                                                                                              \
+    _Pragma("unroll") for (int j = 0; j < FN; ++j) {                                               \
+      const int r = wn * WTN + j * 16 + li;                                                        \
+      BF[j] = bs_[r * 8 + (c ^ (r & 7))];                                                          \
+    }                                                                                              \
+  }
+#define MH_PMMA(AF, BF)                                                                            \
+  _Pragma("unroll") for (int i = 0; i < FM; ++i) _Pragma("unroll") for (int j = 0; j < FN; ++j)   \
+      PipeMfma<DT>::mma(acc[i][j], BF[j], AF[i]);
+  // Instruction interleaving for the two phases of a K step (groups are
+  // filled in order: MFMA, then the memory operation of that slot).
+  //   phase A: each of the first NWR MFMAs is followed by one LDS store of the
+  //            next slab and one global load of the slab after it, the next
+  //            NRD by one fragment read of the second K half;
+  //   phase B: each of the first NRD MFMAs is followed by one fragment read of
+  //            the next slab's first K half.
+  constexpr int NMM = FM * FN, NRD = FM + FN, NWR = ACH + BCH;
+#define MH_SCHED_A()                                                                               \
+  _Pragma("unroll") for (int t = 0; t < NMM; ++t) {                                                \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                             \
+    if (t < NWR) {                                                                                 \
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                                           \
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                           \
+    } else if (t < NWR + NRD) {                                                                    \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                           \
+    }                                                                                              \
+  }
+#define MH_SCHED_B()                                                                               \
+  _Pragma("unroll") for (int t = 0; t < NMM; ++t) {                                                \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                             \
+    if (t < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                \
   }
 
-  // slab 0 covers columns [0, K0), K0 = K % 64 (or 64): chunks at or past K0
-  // are zero; every later slab is whole
-  const int KT = (K + BK - 1) / BK, K0 = K - (KT - 1) * BK;
-  {
-    const bool cin = c0 * 8 < K0;
-#pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      ra0[i] = cin ? ldg16(ap[i]) : u32x4{0, 0, 0, 0};
-      ap[i] += K0;
-    }
-#pragma unroll
-    for (int i = 0; i < BCH; ++i) {
-      rb0[i] = cin ? ldg16(bp[i]) : u32x4{0, 0, 0, 0};
-      bp[i] += K0;
-    }
-  }
-  if (KT > 1) MH_PGLOAD(ra1, rb1);
-  MH_PSTORE(ra0, rb0, 0);
-  __syncthreads();
-  int k = 0;
-  for (; k + 3 < KT; k += 2) {  // slab k in LDS 0, slab k+1 in regs 1; slabs k+2, k+3 exist
-    MH_PGLOAD(ra0, rb0);
-    MH_PCOMPUTE(0);
-    MH_PSTORE(ra1, rb1, 1);
-    __syncthreads();
-    MH_PGLOAD(ra1, rb1);
-    MH_PCOMPUTE(1);
-    MH_PSTORE(ra0, rb0, 0);
-    __syncthreads();
-  }
-  const int rem = KT - k;  // 1, 2 or 3 slabs left
-  if (rem == 3) {
-    MH_PGLOAD(ra0, rb0);
-    MH_PCOMPUTE(0);
-    MH_PSTORE(ra1, rb1, 1);
-    __syncthreads();
-    MH_PCOMPUTE(1);
-    MH_PSTORE(ra0, rb0, 0);
-    __syncthreads();
-    MH_PCOMPUTE(0);
-  } else if (rem == 2) {
-    MH_PCOMPUTE(0);
-    MH_PSTORE(ra1, rb1, 1);
-    __syncthreads();
-    MH_PCOMPUTE(1);
-  } else {
-    MH_PCOMPUTE(0);
-  }
-#undef MH_PGLOAD
-#undef MH_PSTORE
-#undef MH_PCOMPUTE
-
-  // ---- epilogue ----
-  const long off = ep.mode == EPI_ROWMAJOR ? z * sc : 0;
-  if (DT == BF16 && ep.mode != EPI_CONVT && N % 4 == 0 && (!ep.resid || (ep.ldr & 3) == 0)) {
-    // straight from the accumulators: every fragment takes the bf16 fast
-    // path; all bias / residual quads of the tile are requested before the
-    // first is used, so their latencies overlap
+  // bf16 fast epilogue: its bias and residual quads (lane (r, g) of fragment
+  // (i, j) owns row r, columns 4g..4g+3) are requested before the K loop so
+  // that their memory latency is hidden behind it
+  const bool fast_epi = DT == BF16 && ep.mode != EPI_CONVT && N % 4 == 0 && (!ep.resid || (ep.ldr & 3) == 0);
+  uint2 bq[FN], rq[FM][FN];
+  if (fast_epi) {
     const uint16_t *bias = static_cast<const uint16_t *>(ep.bias), *resid = static_cast<const uint16_t *>(ep.resid);
-    uint2 bq[FN], rq[FM][FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int n = n0 + wn * WTN + j * 16 + lg * 4;
@@ -208,6 +176,67 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
                                              : make_uint2(0, 0);
       }
     }
+  }
+
+  // slab 0 covers columns [0, K0), K0 = K % 64 (or 64): chunks at or past K0
+  // are zero; every later slab is whole
+  const int KT = (K + BK - 1) / BK, K0 = K - (KT - 1) * BK;
+  u32x4 *L0 = lds[0], *L1 = lds[1];
+  {
+    const bool cin = c0 * 8 < K0;
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) ra[i] = cin ? ldg16(As + aoff[i]) : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) rb[i] = cin ? ldg16(Bs + boff[i]) : u32x4{0, 0, 0, 0};
+  }
+  MH_PSTORE(L0);
+  if (KT == 1) {
+    __syncthreads();
+    MH_PFRAG(L0, 0, af0, bf0);
+    MH_PFRAG(L0, 1, af1, bf1);
+    MH_PMMA(af0, bf0);
+    MH_PMMA(af1, bf1);
+  } else {
+    As += K0;
+    Bs += K0;
+    MH_PGLOAD();
+    __syncthreads();
+    MH_PFRAG(L0, 0, af0, bf0);
+    // K step k: slab k in L0 with its first-half fragments in af0 / bf0, slab
+    // k + 1 in the staging registers.  The loads of a step past the last slab
+    // re-read the last slab (always whole, so in bounds); their data is stored
+    // to the idle buffer and never read.
+    for (int k = 0; k < KT; ++k) {
+      MH_PSTORE(L1);
+      if (k + 2 < KT) {
+        As += BK;
+        Bs += BK;
+      }
+      MH_PGLOAD();
+      MH_PFRAG(L0, 1, af1, bf1);
+      MH_PMMA(af0, bf0);
+      MH_SCHED_A();
+      __syncthreads();
+      MH_PFRAG(L1, 0, af0, bf0);
+      MH_PMMA(af1, bf1);
+      MH_SCHED_B();
+      u32x4 *t = L0;
+      L0 = L1;
+      L1 = t;
+    }
+  }
+#undef MH_PGLOAD
+#undef MH_PSTORE
+#undef MH_PFRAG
+#undef MH_PMMA
+#undef MH_SCHED_A
+#undef MH_SCHED_B
+
+  // ---- epilogue ----
+  const long off = ep.mode == EPI_ROWMAJOR ? z * sc : 0;
+  if (fast_epi) {
+    // straight from the accumulators: every fragment takes the bf16 fast
+    // path (bias / residual quads were loaded before the K loop)
     // destination = column part (per fragment column) + row part (per
     // fragment row): the head-split index divisions run FM + FN times, not
     // FM * FN times
@@ -277,16 +306,20 @@ template <int DT>
 hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch, long sa,
                      long sb, long sc, const EpiArgs &ep, int tile, hipStream_t st) {
   if (tile < 0) {
-    // measured on MI355X (decoder shapes, K = 768 / 3072): 128x128 when it
-    // gives >= 2.5 tiles per CU or K is deep enough to amortise a partly
-    // filled chip, else 128x64; 64x64 for small problems
+    // measured on MI355X (decoder shapes, K = 768 / 3072): 128x128 when N
+    // tiles evenly by 128 and there are >= 2.5 tiles per CU, 128x96 when N
+    // tiles evenly by 96 (its 64x48 wave tiles fill the chip on narrow N),
+    // else 128x128 / 128x64 / 64x64 by tile count
     const long t128 = long((M + 127) / 128) * ((N + 127) / 128) * batch;
     const long t64 = long((M + 127) / 128) * ((N + 63) / 64) * batch;
-    tile = (t128 >= 640 || (K >= 2048 && t128 >= 128)) ? 0 : (t64 >= 256 ? 1 : 2);
+    if (N % 128 == 0 && t128 >= 640) tile = 0;
+    else if (N % 96 == 0) tile = 3;
+    else tile = (t128 >= 640 || (K >= 2048 && t128 >= 128)) ? 0 : (t64 >= 256 ? 1 : 2);
   }
   switch (tile) {
   case 0: launch<DT, 128, 128, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;
   case 1: launch<DT, 128, 64, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;
+  case 3: launch<DT, 128, 96, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;
   default: launch<DT, 64, 64, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;
   }
   return hipGetLastError();
@@ -294,15 +327,18 @@ hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long ld
 
 }  // namespace
 
-bool gemm_pipe_ok(int dt, const void *A, const void *Bt, int K, long lda, long ldb, long sa, long sb) {
+bool gemm_pipe_ok(int dt, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, long sa, long sb) {
+  // per-thread 32-bit element offsets: the last row's last slab must be
+  // addressable from the slab base
+  const bool fits = M > 0 && N > 0 && long(M - 1) * lda + K <= 0xffffffffL && long(N - 1) * ldb + K <= 0xffffffffL;
   return (dt == BF16 || dt == F16) && K > 0 && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && sa % 8 == 0 &&
-         sb % 8 == 0 && (uintptr_t)A % 16 == 0 && (uintptr_t)Bt % 16 == 0;
+         sb % 8 == 0 && (uintptr_t)A % 16 == 0 && (uintptr_t)Bt % 16 == 0 && fits;
 }
 
 hipError_t gemm_pipe(int dt, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch,
                      long sa, long sb, long sc, const EpiArgs &ep, int tile, hipStream_t st) {
   if (M <= 0 || N <= 0 || batch <= 0) return hipSuccess;
-  if (!gemm_pipe_ok(dt, A, Bt, K, lda, ldb, sa, sb)) return hipErrorInvalidValue;
+  if (!gemm_pipe_ok(dt, A, Bt, M, N, K, lda, ldb, sa, sb)) return hipErrorInvalidValue;
   if (dt == BF16) return launch_dt<BF16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile, st);
   return launch_dt<F16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile, st);
 }

@@ -79,8 +79,8 @@ bool gemm_dma_ok(int dt, const void *A, const void *Bt, int K, long lda, long ld
 hipError_t gemm_dma(int dt, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch, long sa,
                     long sb, long sc, const EpiArgs &ep, int tile, hipStream_t st);
 // Pipelined kernel for 16-bit aligned operands (K % 8 == 0, 16-byte aligned
-// rows); tile: 0 128x128, 1 128x64, 2 64x64, < 0 automatic.
-bool gemm_pipe_ok(int dt, const void *A, const void *Bt, int K, long lda, long ldb, long sa, long sb);
+// rows); tile: 0 128x128, 1 128x64, 2 64x64, 3 128x96, < 0 automatic.
+bool gemm_pipe_ok(int dt, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, long sa, long sb);
 hipError_t gemm_pipe(int dt, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch,
                      long sa, long sb, long sc, const EpiArgs &ep, int tile, hipStream_t st);
 hipError_t conv_nhwc(int dt, const void *x, const void *w_ohwi, const ConvArgs &cv, int oC, const EpiArgs &ep,

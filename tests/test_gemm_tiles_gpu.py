@@ -36,7 +36,7 @@ print("ok")
 '''
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 100, 101, 102, 103, 104, 105, 106, 107, 200, 201, 202])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 100, 101, 102, 103, 104, 105, 106, 107, 200, 201, 202, 203])
 def test_forced_tile(tile):
     root = os.path.dirname(HERE)
     code = SCRIPT.format(root=root, tests=HERE, tile=tile)
