@@ -186,7 +186,9 @@ def main():
         sys.exit(2)
 
     import torch
-    from munet_amd import models
+    import ctypes
+
+    from munet_amd import _lib, models
     from munet_amd.backend import HipBackend
     from munet_amd.engine import Engine
 
@@ -215,6 +217,14 @@ def main():
     ms = dt_s / args.steps * 1e3
     tokens_s = B * T * args.steps / dt_s
     log(f"bench: {ms:.3f} ms/forward, {tokens_s:,.0f} tokens/s")
+    # the timed forwards reran the resident input: no device error (token id
+    # out of range) and the same logits as the first forward, bit for bit
+    _lib.call("mh_check_device_errors")
+    again = np.empty_like(logits)
+    _lib.call("mh_copy", ctypes.c_void_p(eng.output_ptr()), again.ctypes.data_as(ctypes.c_void_p),
+              ctypes.c_size_t(again.nbytes), 1, 0, ctypes.c_void_p(eng.stream()))
+    if not np.array_equal(again.view(np.uint16), logits.view(np.uint16)):
+        raise SystemExit("bench: repeated forwards changed the logits")
 
     rows = kernel_table(hip, torch)
     for r in rows:

@@ -503,11 +503,15 @@ struct EngineImpl {
       vals[r].def = std::min(vals[r].def, t);
       vals[r].last = std::max(vals[r].last, t);
     };
+    // the input buffer is live for the whole forward (and after it): callers
+    // write it once through mh_engine_input_ptr and launch repeatedly, so no
+    // later value may reuse its memory; the output lives until read
     touch(input, -1);
     for (int i = 0; i < int(ops.size()); ++i) {
       for (int v : ops[i].out) touch(v, i);
       for (int v : ops[i].in) touch(v, i);
     }
+    touch(input, int(ops.size()));
     touch(output, int(ops.size()));
     // roots ordered by size, placed at the lowest offset free for their interval
     std::vector<int> order;

@@ -79,6 +79,27 @@ def test_decoder_small(orc, dtype):
     _argmax_check(y, ref, dt)
 
 
+def test_device_resident_input_repeated_launches():
+    """mh_engine_run_device / mh_engine_launch reuse the input already in the
+    arena: every launch after the first must see the same token ids (no later
+    value may overwrite the input buffer) and leave the error flag clear."""
+    import ctypes
+    from munet_amd import _lib
+    cfg = models.decoder_config(vocab=1000, ctx=128, d_model=256, num_heads=4, num_layers=2, ffn=1024)
+    eng, _p, ids = _build(cfg, (2, 128), "gpt")
+    y0 = eng.run(ids)
+    outs = []
+    for _ in range(3):
+        eng.run_device()
+        host = np.empty(y0.shape, dtype=y0.dtype)
+        _lib.call("mh_copy", ctypes.c_void_p(eng.output_ptr()), host.ctypes.data_as(ctypes.c_void_p),
+                  ctypes.c_size_t(host.nbytes), 1, 0, ctypes.c_void_p(eng.stream()))  # device -> host
+        outs.append(host)
+    _lib.call("mh_check_device_errors")
+    for y in outs:
+        assert np.array_equal(y.view(np.uint16), y0.view(np.uint16))
+
+
 def test_decoder_full_width_one_layer(orc):
     """GPT width (d768, h12, ffn3072, T1024) with one layer and a 4096 vocab."""
     cfg = models.decoder_config(vocab=4096, ctx=1024, d_model=768, num_heads=12, num_layers=1, ffn=3072)

@@ -55,6 +55,26 @@ def test_decoder_plan_structure_and_reuse():
     assert e.out_shape == (2, 256, 1000)
 
 
+@pytest.mark.parametrize("which", ["mlp", "decoder", "unet"])
+def test_input_buffer_is_never_reused(which):
+    """The input stays valid across repeated launches on a device-resident
+    input: no other value may share its arena bytes, at any time."""
+    if which == "mlp":
+        cfg, shape = models.mlp_config(), (64, 784)
+    elif which == "decoder":
+        cfg, shape = models.decoder_config(vocab=1000, ctx=256, d_model=128, num_heads=2, num_layers=2, ffn=512), (2, 256)
+    else:
+        cfg, shape = models.unet_config(channels=(8, 16, 32), out_channels=2), (2, 3, 32, 32)
+    _e, p = _plan(cfg, shape)
+    vals = p["values"]
+    inp = vals[p["input"]]
+    lo, hi = inp["offset"], inp["offset"] + inp["bytes"]
+    for i, v in enumerate(vals):
+        if i == p["input"] or v["alias_of"] == p["input"] or v["offset"] < 0:
+            continue
+        assert v["offset"] + v["bytes"] <= lo or hi <= v["offset"], f"value {i} reuses the input's bytes: {v}"
+
+
 def test_unet_zero_copy_concat():
     cfg = models.unet_config(channels=(8, 16, 32), out_channels=2)
     e, p = _plan(cfg, (2, 3, 32, 32))
