@@ -125,6 +125,41 @@ __device__ __forceinline__ uint2 epi_fast_bf16_value(const EpiArgs &ep, float v[
   return pk;
 }
 
+// The same chain with the epilogue kind fixed at compile time (bias added
+// after the matmul rounding, activation, residual): no runtime branches per
+// fragment, and the last rounding only packs.
+template <bool BIAS, int ACT, bool RESID>
+__device__ __forceinline__ uint2 epi_fast_bf16_fixed(float v[4], uint2 bias, uint2 resid, float gelu_c) {
+  constexpr bool more = BIAS || ACT != ACT_NONE || RESID;
+  uint2 pk = more ? round4_bf16(v) : make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+  if constexpr (BIAS) {
+    v[0] += lo_bf16(bias.x); v[1] += hi_bf16(bias.x); v[2] += lo_bf16(bias.y); v[3] += hi_bf16(bias.y);
+    pk = round4_bf16(v);
+  }
+  if constexpr (ACT == ACT_RELU) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = v[i] > 0.0f ? v[i] : 0.0f;
+    pk = round4_bf16(v);
+  } else if constexpr (ACT == ACT_GELU) {
+    float t[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[i] = v[i] * gelu_c;
+    round4_bf16(t);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[i] = sigmoidf_ref(t[i]);
+    round4_bf16(t);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] *= t[i];
+    pk = round4_bf16(v);
+  }
+  if constexpr (RESID) {
+    v[0] = lo_bf16(resid.x) + v[0]; v[1] = hi_bf16(resid.x) + v[1];
+    v[2] = lo_bf16(resid.y) + v[2]; v[3] = hi_bf16(resid.y) + v[3];
+    pk = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+  }
+  return pk;
+}
+
 // The bf16 fast path for output columns n..n+3 of row m.
 __device__ __forceinline__ void epi_fast_bf16(const EpiArgs &ep, int m, int n, float v[4], uint2 bias, uint2 resid,
                                               long off) {

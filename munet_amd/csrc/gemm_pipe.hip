@@ -50,11 +50,19 @@ template <> struct PipeMfma<BF16> {
     c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
                                                 0, 0);
   }
+  static __device__ __forceinline__ void mma0(f32x4 &c, u32x4 a, u32x4 b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+  }
 };
 template <> struct PipeMfma<F16> {
   static __device__ __forceinline__ void mma(f32x4 &c, u32x4 a, u32x4 b) {
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
                                                0);
+  }
+  static __device__ __forceinline__ void mma0(f32x4 &c, u32x4 a, u32x4 b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b),
+                                               f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
   }
 };
 
@@ -107,11 +115,10 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
     _Pragma("unroll") for (int i = 0; i < ACH; ++i)(L)[sw + RSTEP * 8 * i] = ra[i];                \
     _Pragma("unroll") for (int i = 0; i < BCH; ++i)(L)[BM * 8 + sw + RSTEP * 8 * i] = rb[i];       \
   }
+  // accumulators: the first MFMA of each starts from a zero C operand (an
+  // inline constant), so they are never initialised by VALU writes and keep
+  // one register assignment through the K loop
   f32x4 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   // fragments of one 32-wide K step: lane (li, lg) holds row li, chunk ks*4+lg
   u32x4 af0[FM], bf0[FN], af1[FM], bf1[FN];
 #define MH_PFRAG(L, KS, AF, BF)                                                                    \
@@ -130,6 +137,9 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
 #define MH_PMMA(AF, BF)                                                                            \
   _Pragma("unroll") for (int i = 0; i < FM; ++i) _Pragma("unroll") for (int j = 0; j < FN; ++j)   \
       PipeMfma<DT>::mma(acc[i][j], BF[j], AF[i]);
+#define MH_PMMA0(AF, BF)                                                                           \
+  _Pragma("unroll") for (int i = 0; i < FM; ++i) _Pragma("unroll") for (int j = 0; j < FN; ++j)   \
+      PipeMfma<DT>::mma0(acc[i][j], BF[j], AF[i]);
   // Instruction interleaving for the two phases of a K step (groups are
   // filled in order: MFMA, then the memory operation of that slot).
   //   phase A: each of the first NWR MFMAs is followed by one LDS store of the
@@ -194,7 +204,7 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
     __syncthreads();
     MH_PFRAG(L0, 0, af0, bf0);
     MH_PFRAG(L0, 1, af1, bf1);
-    MH_PMMA(af0, bf0);
+    MH_PMMA0(af0, bf0);
     MH_PMMA(af1, bf1);
   } else {
     As += K0;
@@ -205,30 +215,36 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
     // K step k: slab k in L0 with its first-half fragments in af0 / bf0, slab
     // k + 1 in the staging registers.  The loads of a step past the last slab
     // re-read the last slab (always whole, so in bounds); their data is stored
-    // to the idle buffer and never read.
-    for (int k = 0; k < KT; ++k) {
-      MH_PSTORE(L1);
-      if (k + 2 < KT) {
-        As += BK;
-        Bs += BK;
-      }
-      MH_PGLOAD();
-      MH_PFRAG(L0, 1, af1, bf1);
-      MH_PMMA(af0, bf0);
-      MH_SCHED_A();
-      __syncthreads();
-      MH_PFRAG(L1, 0, af0, bf0);
-      MH_PMMA(af1, bf1);
-      MH_SCHED_B();
-      u32x4 *t = L0;
-      L0 = L1;
-      L1 = t;
-    }
+    // to the idle buffer and never read.  Step 0 is peeled: its first MFMAs
+    // start the accumulators.
+#define MH_PSTEP(KNEXT, MMAA)                                                                      \
+  {                                                                                                \
+    MH_PSTORE(L1);                                                                                 \
+    if ((KNEXT) < KT) {                                                                            \
+      As += BK;                                                                                    \
+      Bs += BK;                                                                                    \
+    }                                                                                              \
+    MH_PGLOAD();                                                                                   \
+    MH_PFRAG(L0, 1, af1, bf1);                                                                     \
+    MMAA(af0, bf0);                                                                                \
+    MH_SCHED_A();                                                                                  \
+    __syncthreads();                                                                               \
+    MH_PFRAG(L1, 0, af0, bf0);                                                                     \
+    MH_PMMA(af1, bf1);                                                                             \
+    MH_SCHED_B();                                                                                  \
+    u32x4 *t = L0;                                                                                 \
+    L0 = L1;                                                                                       \
+    L1 = t;                                                                                        \
+  }
+    MH_PSTEP(2, MH_PMMA0);
+    for (int k = 1; k < KT; ++k) MH_PSTEP(k + 2, MH_PMMA);
+#undef MH_PSTEP
   }
 #undef MH_PGLOAD
 #undef MH_PSTORE
 #undef MH_PFRAG
 #undef MH_PMMA
+#undef MH_PMMA0
 #undef MH_SCHED_A
 #undef MH_SCHED_B
 
@@ -267,24 +283,56 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
       for (int i = 0; i < FM; ++i) roff[i] = long(m0 + wm * WTM + i * 16 + li) * ep.ldc;
       al8 = ((uintptr_t)ep.out & 7) == 0 && (ep.ldc & 3) == 0 && (off & 3) == 0;
     }
+    // the epilogue kinds the engine emits run a fragment loop with the
+    // chain fixed at compile time; any other (bias added before rounding,
+    // unaligned destination) takes the loop with runtime branches
+#define MH_EPI_FIXED(BIAS, ACT, RESID)                                                              \
+  _Pragma("unroll") for (int i = 0; i < FM; ++i) {                                                 \
+    const int m = m0 + wm * WTM + i * 16 + li;                                                     \
+    _Pragma("unroll") for (int j = 0; j < FN; ++j) {                                               \
+      const int n = n0 + wn * WTN + j * 16 + lg * 4;                                               \
+      if (m < M && n < N) {                                                                        \
+        float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};                     \
+        *reinterpret_cast<uint2 *>(cbase[j] + roff[i]) =                                           \
+            epi_fast_bf16_fixed<BIAS, ACT, RESID>(v, bq[j], rq[i][j], ep.gelu_c);                  \
+      }                                                                                            \
+    }                                                                                              \
+  }
+    const bool fixed = al8 && !(ep.bias && ep.bias_first);
+    const bool hb = ep.bias != nullptr, hr = ep.resid != nullptr;
+    if (fixed && !hb && ep.act == ACT_NONE && !hr) {
+      MH_EPI_FIXED(false, ACT_NONE, false);
+    } else if (fixed && hb && ep.act == ACT_NONE && !hr) {
+      MH_EPI_FIXED(true, ACT_NONE, false);
+    } else if (fixed && hb && ep.act == ACT_GELU && !hr) {
+      MH_EPI_FIXED(true, ACT_GELU, false);
+    } else if (fixed && hb && ep.act == ACT_RELU && !hr) {
+      MH_EPI_FIXED(true, ACT_RELU, false);
+    } else if (fixed && hb && ep.act == ACT_NONE && hr) {
+      MH_EPI_FIXED(true, ACT_NONE, true);
+    } else if (fixed && !hb && ep.act == ACT_NONE && hr) {
+      MH_EPI_FIXED(false, ACT_NONE, true);
+    } else {
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int m = m0 + wm * WTM + i * 16 + li;
+      for (int i = 0; i < FM; ++i) {
+        const int m = m0 + wm * WTM + i * 16 + li;
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int n = n0 + wn * WTN + j * 16 + lg * 4;
-        if (m < M && n < N) {
-          float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-          const uint2 pk = epi_fast_bf16_value(ep, v, bq[j], rq[i][j]);
-          uint16_t *dst = cbase[j] + roff[i];
-          if (al8) {
-            *reinterpret_cast<uint2 *>(dst) = pk;
-          } else {
-            dst[0] = uint16_t(pk.x); dst[1] = uint16_t(pk.x >> 16); dst[2] = uint16_t(pk.y); dst[3] = uint16_t(pk.y >> 16);
+        for (int j = 0; j < FN; ++j) {
+          const int n = n0 + wn * WTN + j * 16 + lg * 4;
+          if (m < M && n < N) {
+            float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+            const uint2 pk = epi_fast_bf16_value(ep, v, bq[j], rq[i][j]);
+            uint16_t *dst = cbase[j] + roff[i];
+            if (al8) {
+              *reinterpret_cast<uint2 *>(dst) = pk;
+            } else {
+              dst[0] = uint16_t(pk.x); dst[1] = uint16_t(pk.x >> 16); dst[2] = uint16_t(pk.y); dst[3] = uint16_t(pk.y >> 16);
+            }
           }
         }
       }
     }
+#undef MH_EPI_FIXED
   } else {
     // general epilogue (fp16 rounding, transposed-conv scatter, ragged N)
     // through the idle LDS

@@ -65,9 +65,11 @@ def test_matmul_closed_form(hip):
 @pytest.mark.parametrize("dt", DTS)
 @pytest.mark.parametrize("act", [0, 1, 2])
 @pytest.mark.parametrize("resid", [False, True])
-def test_linear_fused(hip, orc, dt, act, resid):
+@pytest.mark.parametrize("has_bias", [True, False])
+def test_linear_fused(hip, orc, dt, act, resid, has_bias):
     M, K, N = 96, 160, 72
-    x, w, bias = rand((M, K), dt, 5), rand((K, N), dt, 6, 0.2), rand((N,), dt, 7)
+    x, w = rand((M, K), dt, 5), rand((K, N), dt, 6, 0.2)
+    bias = rand((N,), dt, 7) if has_bias else None
     r = rand((M, N), dt, 8)
     ref = orc.linear(x, w, bias, dt)
     if act == 1:
@@ -80,8 +82,9 @@ def test_linear_fused(hip, orc, dt, act, resid):
     wt = empty((N, K), dt)
     hip.pack_linear_weight(wd, wt, K, N)
     out = empty((M, N), dt)
-    hip.linear(to_device(x, dt), wt, to_device(bias, dt), out, M, K, N, act, to_device(r, dt) if resid else None)
-    assert_close(to_host(out, dt), ref, dt, what=f"linear act={act} resid={resid}")
+    hip.linear(to_device(x, dt), wt, to_device(bias, dt) if has_bias else None, out, M, K, N, act,
+               to_device(r, dt) if resid else None)
+    assert_close(to_host(out, dt), ref, dt, what=f"linear act={act} resid={resid} bias={has_bias}")
 
 
 def _mha_params(E, dt, seed):
