@@ -168,23 +168,23 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
   // (i, j) owns row r, columns 4g..4g+3) are requested before the K loop so
   // that their memory latency is hidden behind it
   const bool fast_epi = DT == BF16 && ep.mode != EPI_CONVT && N % 4 == 0 && (!ep.resid || (ep.ldr & 3) == 0);
+  // (one uniform branch per operand; rows / columns past the edge load the
+  // last valid quad, whose results are not stored)
   uint2 bq[FN], rq[FM][FN];
-  if (fast_epi) {
-    const uint16_t *bias = static_cast<const uint16_t *>(ep.bias), *resid = static_cast<const uint16_t *>(ep.resid);
+  if (fast_epi && ep.bias) {
+    const uint16_t *bias = static_cast<const uint16_t *>(ep.bias);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int n = n0 + wn * WTN + j * 16 + lg * 4;
-      bq[j] = (bias && n < N) ? *reinterpret_cast<const uint2 *>(bias + n) : make_uint2(0, 0);
-    }
+    for (int j = 0; j < FN; ++j)
+      bq[j] = *reinterpret_cast<const uint2 *>(bias + min(n0 + wn * WTN + j * 16 + lg * 4, N - 4));
+  }
+  if (fast_epi && ep.resid) {
+    const uint16_t *resid = static_cast<const uint16_t *>(ep.resid);
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      const int m = m0 + wm * WTM + i * 16 + li;
+      const uint16_t *rrow = resid + long(min(m0 + wm * WTM + i * 16 + li, M - 1)) * ep.ldr;
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int n = n0 + wn * WTN + j * 16 + lg * 4;
-        rq[i][j] = (resid && m < M && n < N) ? *reinterpret_cast<const uint2 *>(resid + long(m) * ep.ldr + n)
-                                             : make_uint2(0, 0);
-      }
+      for (int j = 0; j < FN; ++j)
+        rq[i][j] = *reinterpret_cast<const uint2 *>(rrow + min(n0 + wn * WTN + j * 16 + lg * 4, N - 4));
     }
   }
 
@@ -286,12 +286,14 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
     // the epilogue kinds the engine emits run a fragment loop with the
     // chain fixed at compile time; any other (bias added before rounding,
     // unaligned destination) takes the loop with runtime branches
+    // interior tiles (the common case) store every fragment unconditionally
+    const bool interior = m0 + BM <= M && n0 + BN <= N;
 #define MH_EPI_FIXED(BIAS, ACT, RESID)                                                              \
   _Pragma("unroll") for (int i = 0; i < FM; ++i) {                                                 \
     const int m = m0 + wm * WTM + i * 16 + li;                                                     \
     _Pragma("unroll") for (int j = 0; j < FN; ++j) {                                               \
       const int n = n0 + wn * WTN + j * 16 + lg * 4;                                               \
-      if (m < M && n < N) {                                                                        \
+      if (interior || (m < M && n < N)) {                                                          \
         float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};                     \
         *reinterpret_cast<uint2 *>(cbase[j] + roff[i]) =                                           \
             epi_fast_bf16_fixed<BIAS, ACT, RESID>(v, bq[j], rq[i][j], ep.gelu_c);                  \
