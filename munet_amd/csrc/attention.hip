@@ -319,6 +319,8 @@ __device__ __forceinline__ uint2 lds_tr(const uint8_t *p) {
   return __builtin_bit_cast(uint2, r);
 }
 
+template <int V> struct BufIdx { static constexpr int value = V; };
+
 template <int DT> __device__ __forceinline__ void round_scores(float v[4]) {
   if (DT == BF16) {
     round4<BF16>(v);
@@ -424,8 +426,12 @@ flash_attn_tr_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict_
     for (int ks = 0; ks < 2; ++ks)
       asm volatile("" : "+v"(qf[r][ks].x), "+v"(qf[r][ks].y), "+v"(qf[r][ks].z), "+v"(qf[r][ks].w)::"memory");
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int j0 = t * KB, buf = t & 1;
+  // one K/V tile; the LDS buffer index is a compile-time constant (the loop
+  // below runs two tiles per trip) so the fragment addresses fold into
+  // instruction offsets instead of being recomputed every tile
+  auto tile = [&](int t, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
+    const int j0 = t * KB;
     if (t + 1 < ntiles) gload(j0 + KB);
 
     if (!(causal && j0 > wrow0 + 16 * RW - 1)) {  // skip tiles wholly above the diagonal
@@ -516,7 +522,13 @@ flash_attn_tr_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict_
     }
     if (t + 1 < ntiles) sstore(buf ^ 1);
     __syncthreads();
+  };
+  int t = 0;
+  for (; t + 1 < ntiles; t += 2) {
+    tile(t, BufIdx<0>{});
+    tile(t + 1, BufIdx<1>{});
   }
+  if (t < ntiles) tile(t, BufIdx<0>{});
 
   const int b = bh / H, h = bh - b * H;
   const long E = long(H) * HD;
