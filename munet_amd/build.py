@@ -24,7 +24,7 @@ LIB = os.path.join(HERE, "libmunet_hip.so")
 PLUGIN = os.path.join(HERE, "libmunet_backend_hip.so")
 ARCH = "gfx950"
 
-KERNEL_SOURCES = ["gemm.hip", "gemm_pipe.hip", "gemm_dma.hip", "attention.hip", "eltwise.hip", "norm.hip", "layout.hip"]
+KERNEL_SOURCES = ["gemm.hip", "gemm_pipe.hip", "gemm_pipe_big.hip", "gemm_dma.hip", "attention.hip", "eltwise.hip", "norm.hip", "layout.hip"]
 HOST_SOURCES = ["capi.cpp", "engine.cpp", "artifact.cpp", "backend.cpp"]
 PLUGIN_SOURCES = ["plugin.cpp"]
 

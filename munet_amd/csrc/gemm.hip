@@ -353,8 +353,9 @@ hipError_t gemm_nt(int dt, const void *A, const void *Bt, int M, int N, int K, l
   if (M <= 0 || N <= 0 || batch <= 0) return hipSuccess;
   if (tile_hint < 0) {
     // MUNET_HIP_GEMM_TILE forces a kernel and block tile for tests and tuning:
-    // 0-6 direct-to-LDS kernel, 100-107 general kernel, 200-203 pipelined kernel.
-    static const char *force = std::getenv("MUNET_HIP_GEMM_TILE");
+    // 0-6 direct-to-LDS kernel, 100-107 general kernel, 200-206 pipelined
+    // kernel.  Read at every call so a process can switch it between calls.
+    const char *force = std::getenv("MUNET_HIP_GEMM_TILE");
     if (force && *force) tile_hint = std::atoi(force);
   }
   // <0: the pipelined 16-bit kernel when the operands allow it, else the

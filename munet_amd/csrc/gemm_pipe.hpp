@@ -1,0 +1,590 @@
+// Pipelined 16-bit MFMA GEMM kernels for gfx950: C[M,N] = A[M,K] * Bt[N,K]^T
+// with the fused epilogue of gemm_common.hpp (the reference semantics are
+// those of BackendBlasCapability::matmul and nn::Linear,
+// src/core/backend.hpp:250-260, src/nn/linear.hpp:28-34).
+//
+// The hot path of the decoder's Linear layers (bf16/fp16, 16-byte aligned
+// K-contiguous operands).  Two kernels share the tile scheduler, the LDS
+// layout (128-byte K slabs, chunk c of row r at c ^ (r & 7)), the fragment
+// reads, the MFMA schedule and the epilogue:
+//
+// gemm_pipe_kernel (register staging, any K % 8 == 0):
+//   * each 64-wide K step runs in two phases split by the one barrier of the
+//     step.  Phase A multiplies the first 32-wide K half (fragments already in
+//     registers) while it reads the second half's fragments, stores the next
+//     slab (staged in registers) to the other LDS buffer and requests the
+//     slab after it from memory; phase B multiplies the second half while it
+//     reads the next slab's first-half fragments.  __builtin_amdgcn_
+//     sched_group_barrier pins that interleaving, one memory operation after
+//     each MFMA, so every LDS and global access is covered by MFMA work of the
+//     same wave;
+//   * the K loop has no conditional loads: a K % 64 remainder is taken as a
+//     short (zero-padded) first slab, every later slab is whole, and the loads
+//     of the last step re-read the last slab, so the staging registers never
+//     merge values from different control paths;
+//   * global loads use 32-bit per-thread offsets from slab base pointers that
+//     advance one slab per step.
+//
+// gemm_dma_kernel (direct-to-LDS, K % 64 == 0):
+//   * slabs go from memory straight into S LDS stages with
+//     global_load_lds_dwordx4 (one wave instruction fills 1 KB = 8 slab rows;
+//     lane l fetches the global chunk that the swizzle places at LDS slot l),
+//     so no staging registers and no LDS stores are needed: measured on
+//     MI355X, the staging stores were the largest single cost of the
+//     register-staged loop;
+//   * the loads are issued from inline assembly, which the compiler's
+//     wait-count pass does not see; the kernel waits for them itself
+//     (vmcnt before each barrier, and vmcnt(0) before the epilogue and before
+//     any LDS reuse).  Left to the compiler, every LDS fragment read would
+//     wait for every load in flight, as it cannot tell the stages apart;
+//   * step k multiplies slab k from stage k % S while slabs k + 1 .. k + S - 1
+//     are in flight; phase A issues slab k + S - 1 into the stage that slab
+//     k - 1 used (free since the previous barrier); steps past the last slab
+//     re-load the last slab into the idle stage so that the wait counts are
+//     the same on every step.
+//
+// Both: the epilogue runs on each accumulator fragment in registers (no LDS
+// staging): lane (r, g) of a 16x16 fragment owns row r, columns 4g..4g+3; its
+// bias loads (wave tiles below 128x128) and residual loads (wave tiles up to
+// 64x64) are issued before the K loop.  Instantiated by gemm_pipe.hip (block
+// tiles up to 128 rows, accumulators in VGPRs) and gemm_pipe_big.hip (256-row
+// block tiles, accumulators in AGPRs).
+#pragma once
+
+#include "mh_common.hpp"
+#include "mh_kernels.hpp"
+#include "gemm_common.hpp"
+
+namespace mh {
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// 16-byte load through a global-address-space pointer.  The loop-carried
+// staging pointers would otherwise compile to FLAT loads, which also count on
+// the LDS wait counter: every wait for an LDS fragment would then wait for the
+// in-flight prefetch as well.
+__device__ __forceinline__ u32x4 ldg16(const uint16_t *p) {
+  return *(const __attribute__((address_space(1))) u32x4 *)(p);
+}
+
+template <int DT> struct PipeMfma;
+template <> struct PipeMfma<BF16> {
+  static __device__ __forceinline__ void mma(f32x4 &c, u32x4 a, u32x4 b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                0, 0);
+  }
+  static __device__ __forceinline__ void mma0(f32x4 &c, u32x4 a, u32x4 b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+  }
+};
+template <> struct PipeMfma<F16> {
+  static __device__ __forceinline__ void mma(f32x4 &c, u32x4 a, u32x4 b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                               0);
+  }
+  static __device__ __forceinline__ void mma0(f32x4 &c, u32x4 a, u32x4 b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b),
+                                               f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+  }
+};
+
+// Output tile of this workgroup: workgroups are dealt round-robin to the 8
+// XCDs, so the tile index is remapped to give each XCD a contiguous band of
+// tiles, then grouped along M so that consecutive tiles share Bt panels in
+// that XCD's L2 (the same order as gemm.hip).
+template <int BM, int BN>
+__device__ __forceinline__ void pipe_tile(int M, int N, int &m0, int &n0) {
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, ntiles = tiles_m * tiles_n;
+  int pid = blockIdx.x;
+  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+  constexpr int GROUP = 8;
+  const int span = GROUP * tiles_n, gid = pid / span, fm = gid * GROUP, gs = min(tiles_m - fm, GROUP);
+  m0 = (fm + (pid % span) % gs) * BM;
+  n0 = ((pid % span) / gs) * BN;
+}
+
+// Wave-level geometry of a BM x BN block tile on WGM x WGN waves and the MFMA
+// fragment reads: fragments of one 32-wide K half KS of the slab in L; lane
+// (li, lg) holds row li, chunk KS*4 + lg of each 16-row fragment.
+template <int BM, int BN, int WGM, int WGN> struct PipeGeom {
+  static constexpr int NW = WGM * WGN, NT = NW * 64;
+  static constexpr int WTM = BM / WGM, WTN = BN / WGN, FM = WTM / 16, FN = WTN / 16;
+  static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave tile");
+  int wm, wn, li, lg;
+  __device__ __forceinline__ PipeGeom(int wave, int lane)
+      : wm(wave / WGN), wn(wave % WGN), li(lane & 15), lg(lane >> 4) {}
+  template <int KS>
+  __device__ __forceinline__ void frags(const u32x4 *L, u32x4 (&af)[FM], u32x4 (&bf)[FN]) const {
+    const u32x4 *as = L, *bs = L + BM * 8;
+    const int c = KS * 4 + lg;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int r = wm * WTM + i * 16 + li;
+      af[i] = as[r * 8 + (c ^ (r & 7))];
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int r = wn * WTN + j * 16 + li;
+      bf[j] = bs[r * 8 + (c ^ (r & 7))];
+    }
+  }
+};
+
+// The fused epilogue of a wave's accumulator tile.  bf16 fast path: lane
+// (r, g) of fragment (i, j) owns row r, columns 4g..4g+3.  Where they fit
+// beside the staging and fragment registers, its bias quads (wave tiles below
+// 128x128) and residual quads (wave tiles up to 64x64) are requested before
+// the K loop (prefetch()) so that their memory latency is hidden behind it;
+// larger wave tiles load them in store().  One uniform branch per operand;
+// rows / columns past the edge load the last valid quad, whose results are
+// not stored.  Other cases (fp16 rounding, transposed-conv scatter, ragged
+// N) go through the general LDS-staged store_tile.
+template <int DT, int BM, int BN, int WGM, int WGN> struct PipeEpi {
+  typedef PipeGeom<BM, BN, WGM, WGN> G;
+  static constexpr int FM = G::FM, FN = G::FN, WTM = G::WTM, WTN = G::WTN;
+  static constexpr bool PRE_B = FM * FN < 64, PRE_R = FM * FN <= 16;
+  static constexpr int RQM = PRE_R ? FM : 1, RQN = PRE_R ? FN : 1;
+  // (the epilogue arguments are passed to every method rather than held by
+  // reference: a reference to the by-value kernel argument would make the
+  // compiler copy it to scratch)
+  const G g;
+  const int M, N, m0, n0;
+  const bool fast;
+  uint2 bq[FN], rq[RQM][RQN];
+
+  __device__ __forceinline__ PipeEpi(const EpiArgs &ep, const G &g_, int M_, int N_, int m0_, int n0_)
+      : g(g_), M(M_), N(N_), m0(m0_), n0(n0_),
+        fast(DT == BF16 && ep.mode != EPI_CONVT && N_ % 4 == 0 && (!ep.resid || (ep.ldr & 3) == 0)) {}
+
+  __device__ __forceinline__ uint2 bload(const EpiArgs &ep, int j) const {
+    const uint16_t *bias = static_cast<const uint16_t *>(ep.bias);
+    return *reinterpret_cast<const uint2 *>(bias + min(n0 + g.wn * WTN + j * 16 + g.lg * 4, N - 4));
+  }
+  __device__ __forceinline__ uint2 rload(const EpiArgs &ep, int i, int j) const {
+    const uint16_t *resid = static_cast<const uint16_t *>(ep.resid);
+    return *reinterpret_cast<const uint2 *>(resid + long(min(m0 + g.wm * WTM + i * 16 + g.li, M - 1)) * ep.ldr +
+                                           min(n0 + g.wn * WTN + j * 16 + g.lg * 4, N - 4));
+  }
+
+  __device__ __forceinline__ void prefetch(const EpiArgs &ep) {
+    if (PRE_B && fast && ep.bias) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bq[j] = bload(ep, j);
+    }
+    if (PRE_R && fast && ep.resid) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) rq[i][j] = rload(ep, i, j);
+    }
+  }
+
+  // lds: the kernel's LDS (idle by now), at least 2 * (BM + BN) * 128 bytes
+  __device__ __forceinline__ void store(const EpiArgs &ep, f32x4 (&acc)[FM][FN], long off, u32x4 *lds, int wave,
+                                        int lane) {
+    const int wm = g.wm, wn = g.wn, li = g.li, lg = g.lg;
+    if (!fast) {
+      __syncthreads();
+      store_tile<DT, BM, BN, WTM, WTN, FM, FN, G::NW>(acc, reinterpret_cast<float *>(lds), ep, m0 + wm * WTM,
+                                                      n0 + wn * WTN, M, N, wave, lane, off);
+      return;
+    }
+    if (!PRE_B && ep.bias) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bq[j] = bload(ep, j);
+    }
+    // destination = column part (per fragment column) + row part (per
+    // fragment row): the head-split index divisions run FM + FN times, not
+    // FM * FN times
+    uint16_t *cbase[FN];
+    long roff[FM];
+    bool al8;
+    if (ep.mode == EPI_HEADSPLIT) {
+      // [B, T, 3E] -> q/k/v [B, H, T, hd]: row (b, t), column (which, h, dd).
+      // The three destinations are selected as integer values: a select
+      // between the addresses of ep.outs[i] would need the arguments in
+      // private memory.
+      const uintptr_t o0 = reinterpret_cast<uintptr_t>(ep.outs[0]), o1 = reinterpret_cast<uintptr_t>(ep.outs[1]),
+                      o2 = reinterpret_cast<uintptr_t>(ep.outs[2]);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = min(n0 + wn * WTN + j * 16 + lg * 4, N - 4);
+        const int which = n / ep.E, e = n - which * ep.E, h = e / ep.hd, dd = e - h * ep.hd;
+        const uintptr_t o = which == 0 ? o0 : which == 1 ? o1 : o2;
+        cbase[j] = reinterpret_cast<uint16_t *>(o) + long(h) * ep.T * ep.hd + dd;
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int m = min(m0 + wm * WTM + i * 16 + li, M - 1);
+        const int b = m / ep.T, t = m - b * ep.T;
+        roff[i] = (long(b) * ep.H * ep.T + t) * ep.hd;
+      }
+      al8 = (ep.hd & 3) == 0 && ((uintptr_t)ep.outs[0] & 7) == 0 && ((uintptr_t)ep.outs[1] & 7) == 0 &&
+            ((uintptr_t)ep.outs[2] & 7) == 0;
+    } else {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) cbase[j] = static_cast<uint16_t *>(ep.out) + off + n0 + wn * WTN + j * 16 + lg * 4;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) roff[i] = long(m0 + wm * WTM + i * 16 + li) * ep.ldc;
+      al8 = ((uintptr_t)ep.out & 7) == 0 && (ep.ldc & 3) == 0 && (off & 3) == 0;
+    }
+    // the epilogue kinds the engine emits run a fragment loop with the
+    // chain fixed at compile time; any other (bias added before rounding,
+    // unaligned destination) takes the loop with runtime branches.
+    // Interior tiles (the common case) store every fragment unconditionally.
+    const bool interior = m0 + BM <= M && n0 + BN <= N;
+#define RQ(I, J) (!ep.resid ? make_uint2(0, 0) : PRE_R ? rq[(I) % RQM][(J) % RQN] : rload(ep, I, J))
+#define MH_EPI_FIXED(BIAS, ACT, RESID)                                                              \
+  _Pragma("unroll") for (int i = 0; i < FM; ++i) {                                                 \
+    const int m = m0 + wm * WTM + i * 16 + li;                                                     \
+    _Pragma("unroll") for (int j = 0; j < FN; ++j) {                                               \
+      const int n = n0 + wn * WTN + j * 16 + lg * 4;                                               \
+      if (interior || (m < M && n < N)) {                                                          \
+        float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};                     \
+        *reinterpret_cast<uint2 *>(cbase[j] + roff[i]) =                                           \
+            epi_fast_bf16_fixed<BIAS, ACT, RESID>(v, bq[j], RQ(i, j), ep.gelu_c);                  \
+      }                                                                                            \
+    }                                                                                              \
+  }
+    const bool fixed = al8 && !(ep.bias && ep.bias_first);
+    const bool hb = ep.bias != nullptr, hr = ep.resid != nullptr;
+    if (fixed && !hb && ep.act == ACT_NONE && !hr) {
+      MH_EPI_FIXED(false, ACT_NONE, false);
+    } else if (fixed && hb && ep.act == ACT_NONE && !hr) {
+      MH_EPI_FIXED(true, ACT_NONE, false);
+    } else if (fixed && hb && ep.act == ACT_GELU && !hr) {
+      MH_EPI_FIXED(true, ACT_GELU, false);
+    } else if (fixed && hb && ep.act == ACT_RELU && !hr) {
+      MH_EPI_FIXED(true, ACT_RELU, false);
+    } else if (fixed && hb && ep.act == ACT_NONE && hr) {
+      MH_EPI_FIXED(true, ACT_NONE, true);
+    } else if (fixed && !hb && ep.act == ACT_NONE && hr) {
+      MH_EPI_FIXED(false, ACT_NONE, true);
+    } else {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int m = m0 + wm * WTM + i * 16 + li;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int n = n0 + wn * WTN + j * 16 + lg * 4;
+          if (m < M && n < N) {
+            float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+            const uint2 pk = epi_fast_bf16_value(ep, v, bq[j], RQ(i, j));
+            uint16_t *dst = cbase[j] + roff[i];
+            if (al8) {
+              *reinterpret_cast<uint2 *>(dst) = pk;
+            } else {
+              dst[0] = uint16_t(pk.x); dst[1] = uint16_t(pk.x >> 16); dst[2] = uint16_t(pk.y); dst[3] = uint16_t(pk.y >> 16);
+            }
+          }
+        }
+      }
+    }
+#undef MH_EPI_FIXED
+#undef RQ
+  }
+};
+
+// MFMAs of one 32-wide K half over the wave tile (first use: zero C operand,
+// so accumulators are never initialised by VALU writes and keep one register
+// assignment through the K loop)
+#define MH_PMMA(AF, BF)                                                                            \
+  _Pragma("unroll") for (int i = 0; i < FM; ++i) _Pragma("unroll") for (int j = 0; j < FN; ++j)   \
+      PipeMfma<DT>::mma(acc[i][j], BF[j], AF[i]);
+#define MH_PMMA0(AF, BF)                                                                           \
+  _Pragma("unroll") for (int i = 0; i < FM; ++i) _Pragma("unroll") for (int j = 0; j < FN; ++j)   \
+      PipeMfma<DT>::mma0(acc[i][j], BF[j], AF[i]);
+
+template <int DT, int BM, int BN, int WGM, int WGN>
+__global__ void __launch_bounds__(WGM * WGN * 64)
+gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt, int M, int N, int K, long lda,
+                 long ldb, long sa, long sb, long sc, EpiArgs ep) {
+  typedef PipeGeom<BM, BN, WGM, WGN> G;
+  constexpr int NT = G::NT, BK = 64, FM = G::FM, FN = G::FN;
+  constexpr int ACH = BM * 8 / NT, BCH = BN * 8 / NT;
+  static_assert(ACH >= 1 && BCH >= 1 && BM * 8 % NT == 0 && BN * 8 % NT == 0, "tile does not fit the thread count");
+  __shared__ u32x4 lds[2][(BM + BN) * 8];  // [buf][A rows | Bt rows][8 chunks], chunk-swizzled
+
+  int m0, n0;
+  pipe_tile<BM, BN>(M, N, m0, n0);
+  const int z = blockIdx.z;
+  A += z * sa;
+  Bt += z * sb;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const G g(wave, lane);
+  // each thread stages chunk c0 (8 values) of rows r0 + RSTEP * i of A and Bt;
+  // rows past M / N read the last valid row (their results are not stored).
+  // Offsets are 32-bit element offsets from the slab base pointers As / Bs,
+  // which advance one slab per K step (the host checks they fit).
+  constexpr int RSTEP = NT / 8;
+  const int c0 = tid & 7, r0 = tid >> 3;
+  uint32_t aoff[ACH], boff[BCH];
+#pragma unroll
+  for (int i = 0; i < ACH; ++i) aoff[i] = uint32_t(min(m0 + r0 + RSTEP * i, M - 1)) * uint32_t(lda) + c0 * 8;
+#pragma unroll
+  for (int i = 0; i < BCH; ++i) boff[i] = uint32_t(min(n0 + r0 + RSTEP * i, N - 1)) * uint32_t(ldb) + c0 * 8;
+  const int sw = r0 * 8 + (c0 ^ (r0 & 7));  // row r0 + RSTEP * i sits at sw + RSTEP * 8 * i
+  const uint16_t *As = A, *Bs = Bt;
+  u32x4 ra[ACH], rb[BCH];
+#define MH_PGLOAD()                                                                                \
+  {                                                                                                \
+    _Pragma("unroll") for (int i = 0; i < ACH; ++i) ra[i] = ldg16(As + aoff[i]);                   \
+    _Pragma("unroll") for (int i = 0; i < BCH; ++i) rb[i] = ldg16(Bs + boff[i]);                   \
+  }
+#define MH_PSTORE(L)                                                                               \
+  {                                                                                                \
+    _Pragma("unroll") for (int i = 0; i < ACH; ++i)(L)[sw + RSTEP * 8 * i] = ra[i];                \
+    _Pragma("unroll") for (int i = 0; i < BCH; ++i)(L)[BM * 8 + sw + RSTEP * 8 * i] = rb[i];       \
+  }
+  f32x4 acc[FM][FN];
+  u32x4 af0[FM], bf0[FN], af1[FM], bf1[FN];
+  // Instruction interleaving for the two phases of a K step (groups are
+  // filled in order: MFMA, then the memory operation of that slot).
+  //   phase A: each of the first NWR MFMAs is followed by one LDS store of the
+  //            next slab and one global load of the slab after it, the next
+  //            NRD by one fragment read of the second K half;
+  //   phase B: each of the first NRD MFMAs is followed by one fragment read of
+  //            the next slab's first K half.
+  constexpr int NMM = FM * FN, NRD = FM + FN, NWR = ACH + BCH;
+#define MH_SCHED_A()                                                                               \
+  _Pragma("unroll") for (int t = 0; t < NMM; ++t) {                                                \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                             \
+    if (t < NWR) {                                                                                 \
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                                           \
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                                           \
+    } else if (t < NWR + NRD) {                                                                    \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                           \
+    }                                                                                              \
+  }
+#define MH_SCHED_B()                                                                               \
+  _Pragma("unroll") for (int t = 0; t < NMM; ++t) {                                                \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                             \
+    if (t < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                \
+  }
+
+  PipeEpi<DT, BM, BN, WGM, WGN> epi(ep, g, M, N, m0, n0);
+  epi.prefetch(ep);
+
+  // slab 0 covers columns [0, K0), K0 = K % 64 (or 64): chunks at or past K0
+  // are zero; every later slab is whole
+  const int KT = (K + BK - 1) / BK, K0 = K - (KT - 1) * BK;
+  u32x4 *L0 = lds[0], *L1 = lds[1];
+  {
+    const bool cin = c0 * 8 < K0;
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) ra[i] = cin ? ldg16(As + aoff[i]) : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) rb[i] = cin ? ldg16(Bs + boff[i]) : u32x4{0, 0, 0, 0};
+  }
+  MH_PSTORE(L0);
+  if (KT == 1) {
+    __syncthreads();
+    g.template frags<0>(L0, af0, bf0);
+    g.template frags<1>(L0, af1, bf1);
+    MH_PMMA0(af0, bf0);
+    MH_PMMA(af1, bf1);
+  } else {
+    As += K0;
+    Bs += K0;
+    MH_PGLOAD();
+    __syncthreads();
+    g.template frags<0>(L0, af0, bf0);
+    // K step k: slab k in L0 with its first-half fragments in af0 / bf0, slab
+    // k + 1 in the staging registers.  The loads of a step past the last slab
+    // re-read the last slab (always whole, so in bounds); their data is stored
+    // to the idle buffer and never read.  Step 0 is peeled: its first MFMAs
+    // start the accumulators.
+#define MH_PSTEP(KNEXT, MMAA)                                                                      \
+  {                                                                                                \
+    MH_PSTORE(L1);                                                                                 \
+    if ((KNEXT) < KT) {                                                                            \
+      As += BK;                                                                                    \
+      Bs += BK;                                                                                    \
+    }                                                                                              \
+    MH_PGLOAD();                                                                                   \
+    g.template frags<1>(L0, af1, bf1);                                                             \
+    MMAA(af0, bf0);                                                                                \
+    MH_SCHED_A();                                                                                  \
+    __syncthreads();                                                                               \
+    g.template frags<0>(L1, af0, bf0);                                                             \
+    MH_PMMA(af1, bf1);                                                                             \
+    MH_SCHED_B();                                                                                  \
+    u32x4 *t = L0;                                                                                 \
+    L0 = L1;                                                                                       \
+    L1 = t;                                                                                        \
+  }
+    MH_PSTEP(2, MH_PMMA0);
+    for (int k = 1; k < KT; ++k) MH_PSTEP(k + 2, MH_PMMA);
+#undef MH_PSTEP
+  }
+#undef MH_PGLOAD
+#undef MH_PSTORE
+#undef MH_SCHED_A
+#undef MH_SCHED_B
+
+  epi.store(ep, acc, ep.mode == EPI_ROWMAJOR ? z * sc : 0, &lds[0][0], wave, lane);
+}
+
+// ---- direct-to-LDS kernel ----
+
+// vmcnt(N) only (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] |
+// vmcnt[5:4] in [15:14]); inline assembly so that the wait-count pass keeps it
+// exactly where it is.
+template <int N> __device__ __forceinline__ void dma_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// One wave instruction: 64 lanes x 16 bytes from base + voff (per lane) into
+// LDS bytes [m0, m0 + 1024) (lane l at m0 + 16 l).
+__device__ __forceinline__ void dma16(const uint16_t *base, uint32_t voff, uint32_t ldsaddr) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(ldsaddr)
+               : "memory", "m0");
+}
+
+template <int DT, int BM, int BN, int WGM, int WGN, int S>
+__global__ void __launch_bounds__(WGM * WGN * 64)
+gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt, int M, int N, int K, long lda,
+                long ldb, long sa, long sb, long sc, EpiArgs ep) {
+  typedef PipeGeom<BM, BN, WGM, WGN> G;
+  constexpr int NW = G::NW, FM = G::FM, FN = G::FN, BK = 64;
+  // 8-row DMA blocks per wave per slab (A, then Bt)
+  constexpr int ABLK = BM / 8 / NW, BBLK = BN / 8 / NW, NDMA = ABLK + BBLK;
+  static_assert(ABLK * NW * 8 == BM && BBLK * NW * 8 == BN, "DMA split");
+  static_assert(S >= 2 && NDMA * (S - 1) < 64, "stages");
+  constexpr uint32_t STAGE = (BM + BN) * 128;  // bytes per stage
+  __shared__ u32x4 lds[S][(BM + BN) * 8];
+
+  int m0, n0;
+  pipe_tile<BM, BN>(M, N, m0, n0);
+  const int z = blockIdx.z;
+  A += z * sa;
+  Bt += z * sb;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const G g(wave, lane);
+  // lane l of a DMA instruction fetches block row l / 8, global chunk
+  // (l % 8) ^ (l / 8): the chunk that the swizzle stores at LDS slot l.
+  // Byte offsets from the slab base (rows past M / N read the last valid row).
+  const int lr = lane >> 3, lc = (lane & 7) ^ lr;
+  uint32_t aoff[ABLK], boff[BBLK];
+#pragma unroll
+  for (int i = 0; i < ABLK; ++i)
+    aoff[i] = (uint32_t(min(m0 + (wave * ABLK + i) * 8 + lr, M - 1)) * uint32_t(lda) + lc * 8) * 2;
+#pragma unroll
+  for (int i = 0; i < BBLK; ++i)
+    boff[i] = (uint32_t(min(n0 + (wave * BBLK + i) * 8 + lr, N - 1)) * uint32_t(ldb) + lc * 8) * 2;
+  const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>((lds_void_t *)&lds[0][0]));
+  const uint32_t wa = lds0 + wave * ABLK * 1024, wb = lds0 + BM * 128 + wave * BBLK * 1024;
+  const int KT = K / BK;
+  // DMA instruction t (A blocks first) of slab kt into stage st
+#define MH_DMA(T, KT_, ST)                                                                         \
+  {                                                                                                \
+    if ((T) < ABLK)                                                                                \
+      dma16(A + (KT_) * BK, aoff[(T) % ABLK], wa + (ST) * STAGE + ((T) % ABLK) * 1024);            \
+    else                                                                                           \
+      dma16(Bt + (KT_) * BK, boff[((T) - ABLK) % BBLK], wb + (ST) * STAGE + (((T) - ABLK) % BBLK) * 1024); \
+  }
+
+  f32x4 acc[FM][FN];
+  u32x4 af0[FM], bf0[FN], af1[FM], bf1[FN];
+  PipeEpi<DT, BM, BN, WGM, WGN> epi(ep, g, M, N, m0, n0);
+  epi.prefetch(ep);
+
+  // prologue: slabs 0 .. S-2 in flight (re-loading the last slab past the
+  // end), wait for slab 0
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s) {
+    const int kt = min(s, KT - 1);
+#pragma unroll
+    for (int t = 0; t < NDMA; ++t) MH_DMA(t, kt, s);
+  }
+  dma_wait<NDMA * (S - 2)>();
+  __syncthreads();
+  g.template frags<0>(lds[0], af0, bf0);
+
+  // Step k on stage s = k % S (a wave-uniform index: one step per loop trip
+  // keeps every accumulator in one register assignment).  Phase A: each MFMA
+  // of the first K half is followed by one DMA of slab k + S - 1 (into stage
+  // (k + S - 1) % S), then by one fragment read of the second half; wait for
+  // slab k + 1; barrier.  Phase B: each MFMA of the second half is followed by
+  // one fragment read of slab k + 1's first half.  The order is written out
+  // and pinned with sched_barrier (the scheduler cannot place inline assembly
+  // in sched_group_barrier slots).
+  constexpr int NMM = FM * FN, NRD = FM + FN;
+  constexpr int STAGE4 = (BM + BN) * 8;  // u32x4 per stage
+  const int c1 = 4 + g.lg, c0f = g.lg;
+#define MH_FRAG(L, C, X, AF, BF)                                                                   \
+  {                                                                                                \
+    if ((X) < FM) {                                                                                \
+      const int r = g.wm * G::WTM + ((X) % FM) * 16 + g.li;                                        \
+      AF[(X) % FM] = (L)[r * 8 + ((C) ^ (r & 7))];                                                 \
+    } else {                                                                                       \
+      const int r = g.wn * G::WTN + (((X) - FM) % FN) * 16 + g.li;                                 \
+      BF[((X) - FM) % FN] = (L)[BM * 8 + r * 8 + ((C) ^ (r & 7))];                                 \
+    }                                                                                              \
+  }
+#define MH_DSTEP(KK, FIRST)                                                                        \
+  {                                                                                                \
+    const int s_ = (KK) % S, sn_ = s_ + 1 == S ? 0 : s_ + 1, sf_ = s_ == 0 ? S - 1 : s_ - 1;       \
+    const int kf_ = min((KK) + S - 1, KT - 1);                                                     \
+    const u32x4 *Ls_ = &lds[0][0] + s_ * STAGE4, *Ln_ = &lds[0][0] + sn_ * STAGE4;                 \
+    _Pragma("unroll") for (int t = 0; t < NMM; ++t) {                                              \
+      if (FIRST) PipeMfma<DT>::mma0(acc[t / FN][t % FN], bf0[t % FN], af0[t / FN]);                \
+      else PipeMfma<DT>::mma(acc[t / FN][t % FN], bf0[t % FN], af0[t / FN]);                       \
+      if (t < NDMA) MH_DMA(t, kf_, sf_)                                                            \
+      else if (t < NDMA + NRD) MH_FRAG(Ls_, c1, t - NDMA, af1, bf1)                                \
+      __builtin_amdgcn_sched_barrier(0);                                                           \
+    }                                                                                              \
+    _Pragma("unroll") for (int t = NMM; t < NDMA + NRD; ++t) {                                     \
+      if (t < NDMA) MH_DMA(t, kf_, sf_)                                                            \
+      else MH_FRAG(Ls_, c1, t - NDMA, af1, bf1)                                                    \
+    }                                                                                              \
+    dma_wait<NDMA * (S - 2)>();                                                                    \
+    __syncthreads();                                                                               \
+    _Pragma("unroll") for (int t = 0; t < NMM; ++t) {                                              \
+      PipeMfma<DT>::mma(acc[t / FN][t % FN], bf1[t % FN], af1[t / FN]);                            \
+      if (t < NRD) MH_FRAG(Ln_, c0f, t, af0, bf0)                                                  \
+      __builtin_amdgcn_sched_barrier(0);                                                           \
+    }                                                                                              \
+    _Pragma("unroll") for (int t = NMM; t < NRD; ++t) MH_FRAG(Ln_, c0f, t, af0, bf0)               \
+  }
+  MH_DSTEP(0, true);
+  for (int k = 1; k < KT; ++k) MH_DSTEP(k, false);
+#undef MH_DSTEP
+#undef MH_DMA
+#undef MH_FRAG
+  // every load has landed and every wave is done with the stages before the
+  // epilogue reuses the LDS or the workgroup ends
+  dma_wait<0>();
+  __syncthreads();
+  epi.store(ep, acc, ep.mode == EPI_ROWMAJOR ? z * sc : 0, &lds[0][0], wave, lane);
+}
+
+#undef MH_PMMA
+#undef MH_PMMA0
+
+template <int DT, int BM, int BN, int WGM, int WGN>
+void launch(const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch, long sa, long sb,
+            long sc, const EpiArgs &ep, hipStream_t st) {
+  const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm_pipe_kernel<DT, BM, BN, WGM, WGN>), dim3(tiles, 1, batch), dim3(WGM * WGN * 64), 0, st,
+                     (const uint16_t *)A, (const uint16_t *)Bt, M, N, K, lda, ldb, sa, sb, sc, ep);
+}
+
+template <int DT, int BM, int BN, int WGM, int WGN, int S>
+void launch_dma(const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch, long sa, long sb,
+                long sc, const EpiArgs &ep, hipStream_t st) {
+  const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm_dma_kernel<DT, BM, BN, WGM, WGN, S>), dim3(tiles, 1, batch), dim3(WGM * WGN * 64), 0,
+                     st, (const uint16_t *)A, (const uint16_t *)Bt, M, N, K, lda, ldb, sa, sb, sc, ep);
+}
+
+}  // namespace
+}  // namespace mh
