@@ -24,7 +24,8 @@ LIB = os.path.join(HERE, "libmunet_hip.so")
 PLUGIN = os.path.join(HERE, "libmunet_backend_hip.so")
 ARCH = "gfx950"
 
-KERNEL_SOURCES = ["gemm.hip", "gemm_pipe.hip", "gemm_pipe_big.hip", "gemm_dma.hip", "attention.hip", "eltwise.hip", "norm.hip", "layout.hip"]
+KERNEL_SOURCES = ["gemm.hip", "gemm_pipe.hip", "gemm_pipe_fixed_staged.hip", "gemm_pipe_fixed_dma.hip",
+                  "gemm_pipe_big.hip", "gemm_dma.hip", "attention.hip", "eltwise.hip", "norm.hip", "layout.hip"]
 HOST_SOURCES = ["capi.cpp", "engine.cpp", "artifact.cpp", "backend.cpp"]
 PLUGIN_SOURCES = ["plugin.cpp"]
 
@@ -52,7 +53,8 @@ def _flags():
 # accumulation registers would cost a copy per value) and the pipelined GEMM
 # (measured faster on MI355X).
 _VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
-SOURCE_FLAGS = {"attention.hip": _VGPR_FORM, "gemm_pipe.hip": _VGPR_FORM}
+SOURCE_FLAGS = {"attention.hip": _VGPR_FORM, "gemm_pipe.hip": _VGPR_FORM, "gemm_pipe_fixed_staged.hip": _VGPR_FORM,
+                "gemm_pipe_fixed_dma.hip": _VGPR_FORM}
 
 
 def _compile(src: str) -> str:

@@ -163,7 +163,7 @@ template <int DT, int NV>
 __global__ void __launch_bounds__(256)
 embedding_vec_kernel(const int32_t *__restrict__ ids, const typename Store<DT>::T *__restrict__ w,
                      const typename Store<DT>::T *__restrict__ pos, typename Store<DT>::T *__restrict__ out, int n,
-                     int V, int D, int T, int *__restrict__ err) {
+                     int V, int D, int T, int *__restrict__ err, float *__restrict__ stats) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= n) return;
@@ -184,15 +184,40 @@ embedding_vec_kernel(const int32_t *__restrict__ ids, const typename Store<DT>::
       if (prow) ld4<DT>(prow + c, p[k]);
     }
   }
+  // stats: the row's LayerNorm statistics over the stored (rounded) values,
+  // (mean, M2) by two wave reductions
+  float rsum = 0.f, r[NV][4];
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int c = (k * 64 + lane) * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[k][e] = 0.f;
     if (c < D) {
       float o[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = prow ? p[k][e] + v[k][e] : v[k][e];
       st4<DT>(dst + c, o);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        r[k][e] = Store<DT>::round(o[e]);
+        rsum += r[k][e];
+      }
     }
+  }
+  if (stats) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) rsum += __shfl_xor(rsum, o, 64);
+    const float mu = rsum / float(D);
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+      if ((k * 64 + lane) * 4 < D) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q += (r[k][e] - mu) * (r[k][e] - mu);
+      }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+    if (lane == 0) *reinterpret_cast<float2 *>(stats + 2 * long(row)) = make_float2(mu, q);
   }
 }
 
@@ -284,16 +309,17 @@ hipError_t convert(int sdt, const void *in, int ddt, void *out, size_t n, hipStr
 }
 
 hipError_t embedding(int dt, const int32_t *ids, const void *w, const void *pos, void *out, int n, int V, int D,
-                     int T, int *err, hipStream_t st) {
+                     int T, int *err, hipStream_t st, float *stats) {
   if (n <= 0) return hipSuccess;
   dim3 grid((n + 3) / 4);
   const size_t es = dt == F32 ? 4 : 2;
   const bool vec = D % 4 == 0 && D <= 1024 && (uintptr_t)w % (4 * es) == 0 && (uintptr_t)out % (4 * es) == 0 &&
                    (uintptr_t)pos % (4 * es) == 0;
+  if (stats && !vec) return hipErrorInvalidValue;  // LayerNorm statistics: vector path only
   if (vec) {
 #define MH_EMB(DTV, T, NV)                                                                                      \
   hipLaunchKernelGGL((embedding_vec_kernel<DTV, NV>), grid, dim3(256), 0, st, ids, (const T *)w, (const T *)pos, \
-                     (T *)out, n, V, D, T_, err)
+                     (T *)out, n, V, D, T_, err, stats)
 #define MH_EMB_NV(DTV, T) \
   { if (D <= 256) MH_EMB(DTV, T, 1); else if (D <= 512) MH_EMB(DTV, T, 2); else if (D <= 768) MH_EMB(DTV, T, 3); else MH_EMB(DTV, T, 4); }
     const int T_ = T;

@@ -10,7 +10,8 @@
 //      linear op list over SSA values;
 //   2. fuses: GEMM + bias + ReLU/GELU (+ residual) epilogues, conv + bias +
 //      ReLU, q/k/v projections into one head-splitting GEMM, token + position
-//      embedding + add, and UNet skip concats into zero-copy channel slices;
+//      embedding + add, UNet skip concats into zero-copy channel slices, and
+//      (bf16) each transformer LayerNorm into the Linear after it (fold_ln);
 //   3. plans every activation into one device arena by liveness intervals
 //      (greedy best-offset placement, largest first); weights live in a
 //      second arena packed into the kernels' K-contiguous layouts;
@@ -21,6 +22,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -88,6 +90,22 @@ struct Op {
   const void *w = nullptr, *b = nullptr, *w2 = nullptr;
   int act = ACT_NONE;
   int resid = -1;  // residual value id (GEMM)
+  // folded LayerNorm (bf16): the producer of a LayerNorm input writes its
+  // row partials into value stats_out; the consumer GEMM reads them from
+  // value ln_stats and applies the normalisation in its epilogue
+  int stats_out = -1, stats_cols = 16, ln_stats = -1, ln_parts = 0, ln_cols = 16;
+  const void *ln_cs = nullptr, *ln_bw = nullptr;
+  float ln_eps = 0.f;
+};
+
+// A LayerNorm folded into the Linear that consumes it (stats: the value that
+// holds the input's row partials, each over `cols` columns; -1 = not
+// folded, run the LayerNorm op).
+struct LnFold {
+  int stats = -1, d = 0, cols = 16;
+  float eps = 0.f;
+  std::string pfx;
+  bool on() const { return stats >= 0; }
 };
 
 struct Param {
@@ -132,7 +150,7 @@ struct EngineImpl {
 
   // stats
   double compile_ms = 0, last_run_ms = 0, last_gpu_ms = 0, load_ms = 0;
-  size_t runs = 0, fused_epilogues = 0, zero_copy_concats = 0;
+  size_t runs = 0, fused_epilogues = 0, zero_copy_concats = 0, ln_folds = 0;
 
   ~EngineImpl() {
     if (plan_only) return;
@@ -256,9 +274,91 @@ struct EngineImpl {
     return y;
   }
 
-  // y = act(x W + b) (+ resid); x [..., in]
+  // LayerNorm(x) feeding a Linear, folded across the GEMM: possible when x
+  // (bf16, row-major, d % 16 == 0) comes from a residual GEMM epilogue or the
+  // embedding gather, which then also write x's row partials.  The consumer
+  // multiplies the raw x by gamma (.) W and normalises in its epilogue:
+  //   LN(x) W = rstd (x (gamma (.) W) - mean colsum(gamma (.) W)) + beta W.
+  // (The reference rounds LN(x) to bf16 before its matmul; here the folded
+  // weights are rounded instead, an error of the same order.)
+  // consumer_n: the consuming Linear's output width.  Every column tile of
+  // the consumer re-reads its rows' partials, so a consumer much wider than
+  // d (a vocabulary head) keeps the LayerNorm kernel: measured on MI355X,
+  // the 32000-wide LM head lost more than the LayerNorm launch costs.
+  LnFold fold_ln(int x, const std::string &pfx, int d, float eps, long consumer_n) {
+    LnFold f;
+    const char *env = std::getenv("MUNET_HIP_LN_FOLD");  // "0" disables the fold (tests, comparisons)
+    if ((env && env[0] == '0') || dt != BF16 || d % 16 || d > 1024 || consumer_n > 4L * d ||
+        vals[x].layout != ROWMAJOR || vals[x].alias_of >= 0 || vals[x].shape.empty() || vals[x].shape.back() != d)
+      return f;
+    for (int i = int(ops.size()) - 1; i >= 0; --i) {
+      Op &o = ops[i];
+      if (std::find(o.out.begin(), o.out.end(), x) == o.out.end()) continue;
+      const bool gemm = o.kind == OP_GEMM && o.out[0] == x && o.a[1] == d && o.stats_out < 0;
+      const bool embed = (o.kind == OP_EMBED || o.kind == OP_EMBED_POS) && o.out[0] == x && o.a[2] == d &&
+                         o.stats_out < 0;
+      if (!gemm && !embed) return f;
+      // partial width: the embedding reduces whole rows; a GEMM producer
+      // writes one partial per group of fragment columns that its wave
+      // tiles cover whole (48 for the 128x96 tiles that N % 96 == 0 selects)
+      f.cols = embed ? d : d % 96 == 0 ? 48 : d % 32 == 0 ? 32 : 16;
+      const long M = long(numel(vals[x].shape) / d);
+      f.stats = new_val({int(M), d / f.cols, 2}, F32);
+      o.stats_out = f.stats;
+      o.stats_cols = f.cols;
+      o.out.push_back(f.stats);
+      f.d = d;
+      f.eps = eps;
+      f.pfx = pfx;
+      ++ln_folds;
+      return f;
+    }
+    return f;
+  }
+  // Fold a LayerNorm's gamma into packed bf16 weights [out][in] and return
+  // the epilogue terms: cs[o] = sum_k round(gamma_k w_ok), bw[o] = sum_k
+  // beta_k w_ok (double sums).
+  void fold_weights(std::vector<uint8_t> &packed, int in_f, int out_f, const LnFold &f, std::vector<uint8_t> &cs,
+                    std::vector<uint8_t> &bw) const {
+    const Param &gp = param(f.pfx + "weight"), &bp = param(f.pfx + "bias");
+    if (gp.host.size() != size_t(in_f) * 2 || bp.host.size() != size_t(in_f) * 2)
+      throw Error(f.pfx + ": LayerNorm parameters have the wrong size");
+    const uint16_t *gm = reinterpret_cast<const uint16_t *>(gp.host.data());
+    const uint16_t *bt = reinterpret_cast<const uint16_t *>(bp.host.data());
+    uint16_t *w = reinterpret_cast<uint16_t *>(packed.data());
+    std::vector<float> csf(out_f), bwf(out_f);
+    for (int o = 0; o < out_f; ++o) {
+      double c = 0.0, b = 0.0;
+      for (int k = 0; k < in_f; ++k) {
+        uint16_t &wk = w[size_t(o) * in_f + k];
+        const float wv = host_bf16_to_f32(wk);
+        b += double(host_bf16_to_f32(bt[k])) * wv;
+        wk = host_f32_to_bf16(host_bf16_to_f32(gm[k]) * wv);  // exact product, one rounding
+        c += host_bf16_to_f32(wk);
+      }
+      csf[o] = float(c);
+      bwf[o] = float(b);
+    }
+    cs.resize(size_t(out_f) * 4);
+    bw.resize(size_t(out_f) * 4);
+    std::memcpy(cs.data(), csf.data(), cs.size());
+    std::memcpy(bw.data(), bwf.data(), bw.size());
+  }
+  void attach_fold(Op &o, const LnFold *ln, std::vector<uint8_t> &packed, int in_f, int out_f) {
+    std::vector<uint8_t> cs, bw;
+    fold_weights(packed, in_f, out_f, *ln, cs, bw);
+    o.ln_stats = ln->stats;
+    o.in.push_back(ln->stats);
+    o.ln_cs = upload(std::move(cs));
+    o.ln_bw = upload(std::move(bw));
+    o.ln_parts = in_f / ln->cols;
+    o.ln_cols = ln->cols;
+    o.ln_eps = ln->eps;
+  }
+
+  // y = act(x W + b) (+ resid); x [..., in]; ln: a LayerNorm of x folded in
   int linear(int x, const std::string &pfx, int in_f, int out_f, bool has_bias, int act = ACT_NONE, int resid = -1,
-             int out_val = -1) {
+             int out_val = -1, const LnFold *ln = nullptr) {
     x = to_rowmajor4(x, pfx);
     const Shape s = vals[x].shape;
     if (s.empty() || s.back() != in_f) throw Error(pfx + ": input " + shape_str(s) + " does not end in " + std::to_string(in_f));
@@ -269,7 +369,12 @@ struct EngineImpl {
     o.a[0] = long(numel(s) / in_f);  // M
     o.a[1] = out_f;                  // N
     o.a[2] = in_f;                   // K
-    o.w = upload(pack_linear(param(pfx + "weight"), in_f, out_f));
+    std::vector<uint8_t> packed = pack_linear(param(pfx + "weight"), in_f, out_f);
+    if (ln) {
+      if (ln->d != in_f) throw Error(pfx + ": folded LayerNorm width mismatch");
+      attach_fold(o, ln, packed, in_f, out_f);
+    }
+    o.w = upload(std::move(packed));
     o.b = has_bias ? bias_or_zero(pfx + "bias", out_f) : nullptr;
     o.act = act;
     if (resid >= 0) {
@@ -333,7 +438,7 @@ struct EngineImpl {
 
   // nn::MultiHeadAttention (src/nn/attention.hpp:34-104) on x [B,T,E]; the
   // out-projection optionally adds a residual in its epilogue.
-  int mha(int x, const std::string &pfx, int E, int H, bool causal, int resid = -1) {
+  int mha(int x, const std::string &pfx, int E, int H, bool causal, int resid = -1, const LnFold *ln = nullptr) {
     const Shape s = vals[x].shape;
     if (s.size() != 3 || s[2] != E) throw Error(pfx + ": MultiHeadAttention expects [B,T,E]");
     const int B = s[0], T = s[1], hd = E / H;
@@ -351,6 +456,10 @@ struct EngineImpl {
     const int q = new_val({B * H, T, hd}, dt), k = new_val({B * H, T, hd}, dt), v = new_val({B * H, T, hd}, dt);
     Op &o = emit(OP_QKV, pfx + "qkv_proj", {x}, {q, k, v});
     o.a[0] = B; o.a[1] = T; o.a[2] = E; o.a[3] = H;
+    if (ln) {
+      if (ln->d != E) throw Error(pfx + ": folded LayerNorm width mismatch");
+      attach_fold(o, ln, wcat, E, 3 * E);
+    }
     o.w = upload(std::move(wcat));
     o.b = upload(std::move(bcat));
     const int ctx = new_val({B, T, E}, dt);
@@ -362,11 +471,15 @@ struct EngineImpl {
 
   // Pre-LN transformer block: x + attn(ln1(x)), then x + ff(ln2(x))
   // (demos/multigpu/gpt3_multi_gpu_demo.py:105-114).
+  // Both LayerNorms fold into the Linear that follows them when their input's
+  // producer can write row partials (fold_ln).
   int block(int x, const std::string &pfx, int d, int H, int ffn, bool causal, float eps) {
-    int h = layer_norm(x, pfx + "ln1.", d, eps);
-    int x2 = mha(h, pfx + "attn.", d, H, causal, x);
-    int h2 = layer_norm(x2, pfx + "ln2.", d, eps);
-    int f = linear(h2, pfx + "ff.0.", d, ffn, true, ACT_GELU);
+    const LnFold f1 = fold_ln(x, pfx + "ln1.", d, eps, 3L * d);
+    const int h = f1.on() ? x : layer_norm(x, pfx + "ln1.", d, eps);
+    const int x2 = mha(h, pfx + "attn.", d, H, causal, x, f1.on() ? &f1 : nullptr);
+    const LnFold f2 = fold_ln(x2, pfx + "ln2.", d, eps, ffn);
+    const int h2 = f2.on() ? x2 : layer_norm(x2, pfx + "ln2.", d, eps);
+    const int f = linear(h2, pfx + "ff.0.", d, ffn, true, ACT_GELU, -1, -1, f2.on() ? &f2 : nullptr);
     return linear(f, pfx + "ff.2.", ffn, d, true, ACT_NONE, x2);
   }
 
@@ -443,8 +556,9 @@ struct EngineImpl {
       const int L = m.at("num_layers").as_int(), H = m.at("num_heads").as_int(), ffn = m.at("ffn").as_int();
       const float eps = float(m.get_num("eps", 1e-5));
       for (int i = 0; i < L; ++i) h = block(h, pfx + "blocks." + std::to_string(i) + ".", d, H, ffn, true, eps);
-      h = layer_norm(h, pfx + "ln_f.", d, eps);
-      return linear(h, pfx + "head.", d, V, true);
+      const LnFold ff = fold_ln(h, pfx + "ln_f.", d, eps, V);
+      if (!ff.on()) h = layer_norm(h, pfx + "ln_f.", d, eps);
+      return linear(h, pfx + "head.", d, V, true, ACT_NONE, -1, -1, ff.on() ? &ff : nullptr);
     }
     if (t == "UNet") return unet(m, x, pfx);
     throw Error("unsupported module type '" + t + "'");
@@ -546,6 +660,21 @@ struct EngineImpl {
     return tag ? static_cast<const void *>(wbuf + (reinterpret_cast<uintptr_t>(tag) - 1)) : nullptr;
   }
 
+  void set_fold(const Op &o, EpiArgs &ep) const {
+    if (o.stats_out >= 0) {
+      ep.stats_out = static_cast<float *>(dptr(o.stats_out));
+      ep.stats_cols = o.stats_cols;
+    }
+    if (o.ln_stats >= 0) {
+      ep.ln_stats = static_cast<const float *>(dptr(o.ln_stats));
+      ep.ln_cs = static_cast<const float *>(wptr(o.ln_cs));
+      ep.ln_bw = static_cast<const float *>(wptr(o.ln_bw));
+      ep.ln_parts = o.ln_parts;
+      ep.ln_cols = o.ln_cols;
+      ep.ln_eps = o.ln_eps;
+    }
+  }
+
   void enqueue(const Op &o) {
     hipStream_t st = stream;
     switch (o.kind) {
@@ -560,6 +689,7 @@ struct EngineImpl {
         ep.resid = dptr(o.resid);
         ep.ldr = o.a[1];
       }
+      set_fold(o, ep);
       hip_check(gemm_nt(dt, dptr(o.in[0]), wptr(o.w), int(o.a[0]), int(o.a[1]), int(o.a[2]), o.a[2], o.a[2], 1, 0,
                         0, 0, ep, -1, st),
                 o.name.c_str());
@@ -574,6 +704,7 @@ struct EngineImpl {
       ep.outs[2] = dptr(o.out[2]);
       ep.bias = wptr(o.b);
       ep.T = T; ep.H = H; ep.hd = E / H; ep.E = E;
+      set_fold(o, ep);
       hip_check(gemm_nt(dt, dptr(o.in[0]), wptr(o.w), B * T, 3 * E, E, E, E, 1, 0, 0, 0, ep, -1, st), o.name.c_str());
       break;
     }
@@ -590,7 +721,8 @@ struct EngineImpl {
     case OP_EMBED_POS:
       hip_check(embedding(dt, static_cast<const int32_t *>(dptr(o.in[0])), wptr(o.w),
                           o.kind == OP_EMBED_POS ? wptr(o.w2) : nullptr, dptr(o.out[0]), int(o.a[0]), int(o.a[1]),
-                          int(o.a[2]), int(o.a[3]), device_error_flag(), st),
+                          int(o.a[2]), int(o.a[3]), device_error_flag(), st,
+                          o.stats_out >= 0 ? static_cast<float *>(dptr(o.stats_out)) : nullptr),
                 o.name.c_str());
       break;
     case OP_CONV: {
@@ -782,7 +914,8 @@ struct EngineImpl {
       << ",\"last_forward_gpu_ms\":" << last_gpu_ms << ",\"compiled_input_shape\":" << shape_str(in_shape)
       << ",\"compiled_output_shape\":" << (output >= 0 ? shape_str(vals[output].shape) : "[]")
       << ",\"arena_bytes\":" << arena_bytes << ",\"weight_bytes\":" << wbytes << ",\"ops\":" << ops.size()
-      << ",\"fused_epilogues\":" << fused_epilogues << ",\"zero_copy_concats\":" << zero_copy_concats
+      << ",\"fused_epilogues\":" << fused_epilogues << ",\"ln_folds\":" << ln_folds
+      << ",\"zero_copy_concats\":" << zero_copy_concats
       << ",\"current_memory_bytes\":" << (arena_bytes + wbytes) << ",\"peak_memory_bytes\":" << (arena_bytes + wbytes)
       << "}";
     return s.str();
@@ -794,7 +927,7 @@ struct EngineImpl {
     for (size_t i = 0; i < ops.size(); ++i) {
       const Op &o = ops[i];
       s << (i ? "," : "") << "{\"kind\":\"" << op_name(o.kind) << "\",\"name\":\"" << o.name << "\",\"act\":" << o.act
-        << ",\"resid\":" << o.resid << ",\"in\":[";
+        << ",\"resid\":" << o.resid << ",\"stats_out\":" << o.stats_out << ",\"ln_stats\":" << o.ln_stats << ",\"in\":[";
       for (size_t j = 0; j < o.in.size(); ++j) s << (j ? "," : "") << o.in[j];
       s << "],\"out\":[";
       for (size_t j = 0; j < o.out.size(); ++j) s << (j ? "," : "") << o.out[j];

@@ -360,9 +360,14 @@ hipError_t gemm_nt(int dt, const void *A, const void *Bt, int M, int N, int K, l
   }
   // <0: the pipelined 16-bit kernel when the operands allow it, else the
   // general kernel with an automatic tile.
+  // A folded LayerNorm (stats_out / ln_stats) exists only in the pipelined
+  // kernels: such a GEMM ignores a forced general-kernel tile, and fails when
+  // its operands do not suit the pipelined kernels.
   const bool pipe = gemm_pipe_ok(dt, A, Bt, M, N, K, lda, ldb, sa, sb);
-  if (pipe && (tile_hint < 0 || tile_hint >= 200))
-    return gemm_pipe(dt, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile_hint < 0 ? -1 : tile_hint - 200, st);
+  const bool fold = ep.stats_out || ep.ln_stats;
+  if (pipe && (tile_hint < 0 || tile_hint >= 200 || fold))
+    return gemm_pipe(dt, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile_hint >= 200 ? tile_hint - 200 : -1, st);
+  if (fold) return hipErrorInvalidValue;
   if (tile_hint >= 200) tile_hint = -1;
   if (tile_hint >= 0 && tile_hint < 100 && gemm_dma_ok(dt, A, Bt, K, lda, ldb, sa, sb))
     return gemm_dma(dt, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile_hint, st);

@@ -1,37 +1,86 @@
-// Pipelined 16-bit MFMA GEMM (gemm_pipe.hpp), block tiles up to 128 rows with
-// the accumulators in ordinary VGPRs (built with -amdgpu-mfma-vgpr-form, see
-// build.py), and the tile dispatcher for the pipelined kernels.  256-row
-// tiles are instantiated in gemm_pipe_big.hip.
+// Pipelined 16-bit MFMA GEMM (gemm_pipe.hpp): the general epilogue program
+// on block tiles up to 128 rows, with the accumulators in ordinary VGPRs
+// (built with -amdgpu-mfma-vgpr-form, see build.py), and the dispatcher that
+// picks the block tile and the epilogue program.  The fixed bf16 programs
+// are instantiated in gemm_pipe_fixed_*.hip, 256-row tiles in
+// gemm_pipe_big.hip.
 #include "gemm_pipe.hpp"
 
 namespace mh {
 
 namespace {
 
+// Width of one wave's tile (columns) for each tile code.
+int pipe_wave_cols(int tile) {
+  switch (tile) {
+  case 0: case 6: case 7: case 9: case 15: return 64;
+  case 3: case 8: case 10: case 11: return 48;
+  case 5: case 14: return 96;
+  default: return 32;  // 1 (128x64), 2 (64x64), 12 (128x64)
+  }
+}
+
+// Automatic block tile, measured on MI355X (decoder shapes, K = 768 / 3072,
+// M = 4096):
+//  * N tiling evenly by 96 with at most one tile per CU (N = 768: FFN down,
+//    attention out-projection): direct-to-LDS 128x96, 4 stages (one
+//    workgroup per CU, so deep stages hide the memory latency);
+//  * at least 8 tiles per CU at 128x128 (the LM head): direct-to-LDS 128x128,
+//    2 stages (two workgroups per CU);
+//  * otherwise register-staged: 128x128 when N tiles evenly by 128 and there
+//    are >= 2.5 tiles per CU (FFN up), 128x96 when N tiles evenly by 96
+//    (QKV), else 128x128 / 128x64 / 64x64 by tile count.
+int auto_tile(bool dma, int M, int N, int K, int batch) {
+  const long t128 = long((M + 127) / 128) * ((N + 127) / 128) * batch;
+  const long t96 = long((M + 127) / 128) * ((N + 95) / 96) * batch;
+  const long t64 = long((M + 127) / 128) * ((N + 63) / 64) * batch;
+  if (dma && N % 96 == 0 && t96 <= 256) return 8;
+  if (dma && N % 128 == 0 && t128 >= 2048) return 9;
+  if (N % 128 == 0 && t128 >= 640) return 0;
+  if (N % 96 == 0) return 3;
+  return (t128 >= 640 || (K >= 2048 && t128 >= 128)) ? 0 : (t64 >= 256 ? 1 : 2);
+}
+
+// The tiles with fixed epilogue programs (gemm_pipe_fixed_*.hip).
+bool fixed_tile(int tile) { return (tile >= 0 && tile <= 3) || tile == 8 || tile == 9; }
+
+// The epilogue program for these arguments: a fixed program for the
+// combinations the engine emits (bf16, 8-byte aligned destination, bias
+// after the matmul rounding), else PK_GENERAL; -1 for a folded LayerNorm
+// outside the fixed programs (it has no general form).
+int pipe_kind(int dt, int N, int batch, long sc, const EpiArgs &ep) {
+  const bool fold = ep.ln_stats || ep.stats_out;
+  const bool fast = dt == BF16 && N % 4 == 0 && ep.mode != EPI_CONVT && (!ep.resid || (ep.ldr & 3) == 0);
+  const bool al8 = ep.mode == EPI_HEADSPLIT
+                       ? (ep.hd & 3) == 0 && ((uintptr_t)ep.outs[0] & 7) == 0 && ((uintptr_t)ep.outs[1] & 7) == 0 &&
+                             ((uintptr_t)ep.outs[2] & 7) == 0
+                       : ((uintptr_t)ep.out & 7) == 0 && (ep.ldc & 3) == 0 && (batch == 1 || (sc & 3) == 0);
+  if (!fast || !al8 || (ep.bias && ep.bias_first)) return fold ? -1 : PK_GENERAL;
+  const bool hb = ep.bias != nullptr, hr = ep.resid != nullptr;
+  if (ep.ln_stats) {
+    if (ep.stats_out || !hb || hr) return -1;
+    return ep.act == ACT_NONE ? PK_LN_BIAS : ep.act == ACT_GELU ? PK_LN_BIAS_GELU : -1;
+  }
+  if (ep.stats_out) return hb && hr && ep.act == ACT_NONE ? PK_BIAS_RESID_ST : -1;
+  if (ep.act == ACT_NONE) return !hb && !hr ? PK_PLAIN : hb && !hr ? PK_BIAS : hb && hr ? PK_BIAS_RESID : PK_GENERAL;
+  return ep.act == ACT_GELU && hb && !hr ? PK_BIAS_GELU : PK_GENERAL;
+}
+
 template <int DT>
 hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch, long sa,
-                     long sb, long sc, const EpiArgs &ep, int tile, hipStream_t st) {
-  if (tile < 0) {
-    // measured on MI355X (decoder shapes, K = 768 / 3072, M = 4096):
-    //  * N tiling evenly by 96 with at most one tile per CU (N = 768: FFN down,
-    //    attention out-projection): direct-to-LDS 128x96, 4 stages (one
-    //    workgroup per CU, so deep stages hide the memory latency);
-    //  * at least 8 tiles per CU at 128x128 (the LM head): direct-to-LDS
-    //    128x128, 2 stages (two workgroups per CU);
-    //  * otherwise register-staged: 128x128 when N tiles evenly by 128 and
-    //    there are >= 2.5 tiles per CU (FFN up), 128x96 when N tiles evenly
-    //    by 96 (QKV), else 128x128 / 128x64 / 64x64 by tile count.
-    const bool dma = gemm_pipe_dma_ok(A, Bt, M, N, K, lda, ldb);
-    const long t128 = long((M + 127) / 128) * ((N + 127) / 128) * batch;
-    const long t96 = long((M + 127) / 128) * ((N + 95) / 96) * batch;
-    const long t64 = long((M + 127) / 128) * ((N + 63) / 64) * batch;
-    if (dma && N % 96 == 0 && t96 <= 256) tile = 8;
-    else if (dma && N % 128 == 0 && t128 >= 2048) tile = 9;
-    else if (N % 128 == 0 && t128 >= 640) tile = 0;
-    else if (N % 96 == 0) tile = 3;
-    else tile = (t128 >= 640 || (K >= 2048 && t128 >= 128)) ? 0 : (t64 >= 256 ? 1 : 2);
-  }
-  if (tile >= 7 && !gemm_pipe_dma_ok(A, Bt, M, N, K, lda, ldb)) tile = 0;
+                     long sb, long sc, const EpiArgs &ep, int tile, int kind, hipStream_t st) {
+  const bool dma = gemm_pipe_dma_ok(A, Bt, M, N, K, lda, ldb);
+  // a folded LayerNorm exists only in the fixed programs: a forced tile
+  // without them takes the automatic choice
+  if (tile < 0 || (kind >= PK_LN_BIAS && !fixed_tile(tile))) tile = auto_tile(dma, M, N, K, batch);
+  if (tile >= 7 && !dma) tile = 0;
+  // LayerNorm partials of stats_cols columns need wave tiles that cover whole
+  // groups: move to the nearest tile whose wave-tile width is a multiple
+  if (ep.stats_out && pipe_wave_cols(tile) % ep.stats_cols)
+    tile = ep.stats_cols == 48 ? (dma ? 8 : 3) : ep.stats_cols == 64 ? (dma ? 9 : 0) : 2;
+  if (kind > PK_GENERAL && fixed_tile(tile))
+    return tile <= 3 ? gemm_pipe_fixed_staged(kind, tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st)
+                     : gemm_pipe_fixed_dma(kind, tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
   if (tile >= 4 && tile <= 6) return gemm_pipe_big(DT, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile - 4, st);
   if (tile >= 13) return gemm_pipe_big(DT, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile - 4, st);
   switch (tile) {
@@ -69,8 +118,18 @@ hipError_t gemm_pipe(int dt, const void *A, const void *Bt, int M, int N, int K,
                      long sa, long sb, long sc, const EpiArgs &ep, int tile, hipStream_t st) {
   if (M <= 0 || N <= 0 || batch <= 0) return hipSuccess;
   if (!gemm_pipe_ok(dt, A, Bt, M, N, K, lda, ldb, sa, sb)) return hipErrorInvalidValue;
-  if (dt == BF16) return launch_dt<BF16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile, st);
-  return launch_dt<F16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile, st);
+  const int kind = pipe_kind(dt, N, batch, sc, ep);
+  if (kind < 0) return hipErrorInvalidValue;
+  // the folded-LayerNorm terms (fixed programs only)
+  if (ep.stats_out || ep.ln_stats) {
+    const bool cols_ok = ep.stats_cols == 16 || ep.stats_cols == 32 || ep.stats_cols == 48 || ep.stats_cols == 64;
+    if ((ep.stats_out && (!cols_ok || N % ep.stats_cols || ep.mode != EPI_ROWMAJOR || batch != 1)) ||
+        (ep.ln_stats && (ep.ln_parts <= 0 || ep.ln_parts > 64 || ep.ln_cols <= 0 || K != ep.ln_cols * ep.ln_parts ||
+                         !ep.ln_cs || !ep.ln_bw || batch != 1)))
+      return hipErrorInvalidValue;
+  }
+  if (dt == BF16) return launch_dt<BF16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile, kind, st);
+  return launch_dt<F16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile, kind, st);
 }
 
 }  // namespace mh

@@ -46,9 +46,11 @@
 // Both: the epilogue runs on each accumulator fragment in registers (no LDS
 // staging): lane (r, g) of a 16x16 fragment owns row r, columns 4g..4g+3; its
 // bias loads (wave tiles below 128x128) and residual loads (wave tiles up to
-// 64x64) are issued before the K loop.  Instantiated by gemm_pipe.hip (block
-// tiles up to 128 rows, accumulators in VGPRs) and gemm_pipe_big.hip (256-row
-// block tiles, accumulators in AGPRs).
+// 64x64) are issued before the K loop.  The epilogue program is a template
+// parameter (PipeKind).  Instantiated by gemm_pipe.hip (the general program,
+// block tiles up to 128 rows, accumulators in VGPRs), gemm_pipe_fixed_*.hip
+// (the fixed bf16 programs) and gemm_pipe_big.hip (256-row block tiles,
+// accumulators in AGPRs).
 #pragma once
 
 #include "mh_common.hpp"
@@ -134,6 +136,35 @@ template <int BM, int BN, int WGM, int WGN> struct PipeGeom {
   }
 };
 
+// Epilogue programs.  PK_GENERAL serves every EpiArgs (a fragment loop with
+// the rounding chain chosen at run time, or the LDS-staged store_tile for
+// fp16, transposed-conv scatter and ragged N).  The others are the
+// combinations the engine emits, each one fragment loop fixed at compile
+// time, so a kernel carries only its own epilogue (bf16, 8-byte aligned
+// destination, bias added after the matmul rounding; the host checks).  One
+// epilogue per kernel keeps the code small: with every variant inlined the
+// kernels grew to 30k instructions, and kernels replayed in a graph refetch
+// their code each launch.
+enum PipeKind : int {
+  PK_GENERAL = 0,
+  PK_PLAIN,          // round(acc)
+  PK_BIAS,           // + bias
+  PK_BIAS_GELU,      // + bias, GELU
+  PK_BIAS_RESID,     // + bias, + residual
+  PK_LN_BIAS,        // folded LayerNorm consumer, + bias
+  PK_LN_BIAS_GELU,   // folded LayerNorm consumer, + bias, GELU
+  PK_BIAS_RESID_ST,  // + bias, + residual, writes LayerNorm partials
+  PK_COUNT
+};
+template <int EK> struct PipeKindT {
+  static constexpr bool FIXED = EK != PK_GENERAL;
+  static constexpr bool LN = EK == PK_LN_BIAS || EK == PK_LN_BIAS_GELU;
+  static constexpr bool ST = EK == PK_BIAS_RESID_ST;
+  static constexpr bool BIAS = FIXED && EK != PK_PLAIN;
+  static constexpr int ACT = (EK == PK_BIAS_GELU || EK == PK_LN_BIAS_GELU) ? ACT_GELU : ACT_NONE;
+  static constexpr bool RESID = EK == PK_BIAS_RESID || EK == PK_BIAS_RESID_ST;
+};
+
 // The fused epilogue of a wave's accumulator tile.  bf16 fast path: lane
 // (r, g) of fragment (i, j) owns row r, columns 4g..4g+3.  Where they fit
 // beside the staging and fragment registers, its bias quads (wave tiles below
@@ -143,8 +174,9 @@ template <int BM, int BN, int WGM, int WGN> struct PipeGeom {
 // rows / columns past the edge load the last valid quad, whose results are
 // not stored.  Other cases (fp16 rounding, transposed-conv scatter, ragged
 // N) go through the general LDS-staged store_tile.
-template <int DT, int BM, int BN, int WGM, int WGN> struct PipeEpi {
+template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
   typedef PipeGeom<BM, BN, WGM, WGN> G;
+  typedef PipeKindT<EK> KT_;
   static constexpr int FM = G::FM, FN = G::FN, WTM = G::WTM, WTN = G::WTN;
   static constexpr bool PRE_B = FM * FN < 64, PRE_R = FM * FN <= 16;
   static constexpr int RQM = PRE_R ? FM : 1, RQN = PRE_R ? FN : 1;
@@ -158,7 +190,8 @@ template <int DT, int BM, int BN, int WGM, int WGN> struct PipeEpi {
 
   __device__ __forceinline__ PipeEpi(const EpiArgs &ep, const G &g_, int M_, int N_, int m0_, int n0_)
       : g(g_), M(M_), N(N_), m0(m0_), n0(n0_),
-        fast(DT == BF16 && ep.mode != EPI_CONVT && N_ % 4 == 0 && (!ep.resid || (ep.ldr & 3) == 0)) {}
+        fast(KT_::FIXED ||
+             (DT == BF16 && ep.mode != EPI_CONVT && N_ % 4 == 0 && (!ep.resid || (ep.ldr & 3) == 0))) {}
 
   __device__ __forceinline__ uint2 bload(const EpiArgs &ep, int j) const {
     const uint16_t *bias = static_cast<const uint16_t *>(ep.bias);
@@ -170,12 +203,16 @@ template <int DT, int BM, int BN, int WGM, int WGN> struct PipeEpi {
                                            min(n0 + g.wn * WTN + j * 16 + g.lg * 4, N - 4));
   }
 
+  __device__ __forceinline__ bool has_bias(const EpiArgs &ep) const { return KT_::FIXED ? KT_::BIAS : ep.bias != nullptr; }
+  __device__ __forceinline__ bool has_resid(const EpiArgs &ep) const {
+    return KT_::FIXED ? KT_::RESID : ep.resid != nullptr;
+  }
   __device__ __forceinline__ void prefetch(const EpiArgs &ep) {
-    if (PRE_B && fast && ep.bias) {
+    if (PRE_B && fast && has_bias(ep)) {
 #pragma unroll
       for (int j = 0; j < FN; ++j) bq[j] = bload(ep, j);
     }
-    if (PRE_R && fast && ep.resid) {
+    if (PRE_R && fast && has_resid(ep)) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -183,9 +220,124 @@ template <int DT, int BM, int BN, int WGM, int WGN> struct PipeEpi {
     }
   }
 
-  // lds: the kernel's LDS (idle by now), at least 2 * (BM + BN) * 128 bytes
+  // Folded LayerNorm, consumer prologue.  ln_issue() requests this tile's
+  // inputs before the kernel's first slab: NT / BM threads per row each load
+  // a contiguous share (up to LNCH) of the row's partials into registers,
+  // two partials per 16-byte load where the row length allows, and threads
+  // t < BN load column t's folded-weight sum and beta W.  ln_finish() runs
+  // once the first slab has landed (the same memory round trip): it combines
+  // the shares with Chan's parallel-variance formula, then across adjacent
+  // lanes, and writes (mean, rstd) per row and the column terms to LDS; the
+  // K loop's barriers make them visible to the epilogue.
+  static constexpr int TPR = G::NT / BM, LNCH = 32;
+  static_assert(TPR == 1 || TPR == 2 || TPR == 4, "threads per row");
+  struct LnIn {
+    float4 part[LNCH / 2];  // (mean, M2) pairs
+    float cs, bw;
+  };
+  // (loads are unconditional, at indices clamped into the row; ln_finish
+  // counts only the share's own partials)
+  __device__ __forceinline__ void ln_issue(const EpiArgs &ep, LnIn &in, int tid) const {
+    const int r = tid / TPR, q = tid % TPR, P = ep.ln_parts;
+    const int share = ((P + TPR - 1) / TPR + 1) & ~1, k0 = q * share, k1 = min(k0 + share, P);
+    const long row = min(m0 + r, M - 1);
+    if ((P & 1) == 0) {  // rows and shares start on 16-byte boundaries: two partials per load
+      const float4 *p4 = reinterpret_cast<const float4 *>(ep.ln_stats) + row * (P / 2);
+      const int last = P / 2 - 1;
+#pragma unroll
+      for (int i = 0; i < LNCH / 2; ++i)
+        if (2 * i < share) in.part[i] = p4[min(k0 / 2 + i, last)];
+    } else {
+      const float2 *p = reinterpret_cast<const float2 *>(ep.ln_stats) + row * P;
+#pragma unroll
+      for (int i = 0; i < LNCH / 2; ++i) {
+        if (2 * i < share) {
+          const float2 a = p[min(k0 + 2 * i, P - 1)], b = p[min(k0 + 2 * i + 1, P - 1)];
+          in.part[i] = make_float4(a.x, a.y, b.x, b.y);
+        }
+      }
+    }
+    const int c = min(n0 + min(tid, BN - 1), N - 1);
+    in.cs = ep.ln_cs[c];
+    in.bw = ep.ln_bw[c];
+  }
+  __device__ __forceinline__ void ln_finish(const EpiArgs &ep, const LnIn &in, float2 *lnrow, float *lncs,
+                                            float *lnbw, int tid) const {
+    const int r = tid / TPR, q = tid % TPR, P = ep.ln_parts;
+    const int share = ((P + TPR - 1) / TPR + 1) & ~1, k0 = q * share, k1 = min(k0 + share, P);
+    const float w = float(ep.ln_cols);
+    float n = 0.f, mean = 0.f, m2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < LNCH; ++i) {
+      if (k0 + i < k1) {
+        const float pm = i & 1 ? in.part[i / 2].z : in.part[i / 2].x;
+        const float p2 = i & 1 ? in.part[i / 2].w : in.part[i / 2].y;
+        const float nn = n + w, d = pm - mean;
+        mean += d * (w / nn);
+        m2 += p2 + d * d * (n * (w / nn));
+        n = nn;
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < TPR; o <<= 1) {
+      const float on = __shfl_xor(n, o), om = __shfl_xor(mean, o), o2 = __shfl_xor(m2, o);
+      const float nn = n + on, d = om - mean;
+      if (nn > 0.f) {
+        mean += d * (on / nn);
+        m2 += o2 + d * d * (n * (on / nn));
+      }
+      n = nn;
+    }
+    if (q == 0) lnrow[r] = make_float2(mean, 1.0f / sqrtf(m2 / n + ep.ln_eps));
+    if (tid < BN) {
+      lncs[tid] = in.cs;
+      lnbw[tid] = in.bw;
+    }
+  }
+
+  // Producer side: partials of stats_cols columns (whole groups of fragment
+  // columns inside a wave tile).  Each lane keeps the 4 rounded values it
+  // owns in every fragment column of the group (row li, columns 4 lg ..
+  // 4 lg + 3); when the group is complete, the row's sum and then its sum of
+  // squared deviations are reduced across the 4 lanes that share the row
+  // (lanes li, li+16, li+32, li+48) and lane group 0 stores (mean, M2).
+  struct StatAcc {
+    float y[FN][4];
+  };
+  __device__ __forceinline__ void stats_add(const EpiArgs &ep, StatAcc &a, uint2 pk, int m, int j) const {
+    a.y[j][0] = lo_bf16(pk.x);
+    a.y[j][1] = hi_bf16(pk.x);
+    a.y[j][2] = lo_bf16(pk.y);
+    a.y[j][3] = hi_bf16(pk.y);
+    const int G16 = ep.stats_cols / 16;  // fragment columns per group
+    if ((j + 1) % G16 == 0) {
+      float s = 0.f;
+#pragma unroll
+      for (int t = 0; t < FN; ++t)
+        if (t <= j && t > j - G16) s += (a.y[t][0] + a.y[t][1]) + (a.y[t][2] + a.y[t][3]);
+      s += __shfl_xor(s, 16);
+      s += __shfl_xor(s, 32);
+      const float mu = s / float(ep.stats_cols);
+      float q = 0.f;
+#pragma unroll
+      for (int t = 0; t < FN; ++t)
+        if (t <= j && t > j - G16)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) q += (a.y[t][e] - mu) * (a.y[t][e] - mu);
+      q += __shfl_xor(q, 16);
+      q += __shfl_xor(q, 32);
+      const int g0 = n0 + g.wn * WTN + (j + 1) * 16 - ep.stats_cols;  // first column of the group
+      if (g.lg == 0 && m < M && g0 < N)
+        *reinterpret_cast<float2 *>(ep.stats_out + 2 * (long(m) * (N / ep.stats_cols) + g0 / ep.stats_cols)) =
+            make_float2(mu, q);
+    }
+  }
+
+  // lds: the kernel's LDS (idle by now), at least 2 * (BM + BN) * 128 bytes;
+  // lnrow, lncs, lnbw: the folded LayerNorm's row and column terms
+  // (ln_finish)
   __device__ __forceinline__ void store(const EpiArgs &ep, f32x4 (&acc)[FM][FN], long off, u32x4 *lds, int wave,
-                                        int lane) {
+                                        int lane, const float2 *lnrow, const float *lncs, const float *lnbw) {
     const int wm = g.wm, wn = g.wn, li = g.li, lg = g.lg;
     if (!fast) {
       __syncthreads();
@@ -193,7 +345,7 @@ template <int DT, int BM, int BN, int WGM, int WGN> struct PipeEpi {
                                                       n0 + wn * WTN, M, N, wave, lane, off);
       return;
     }
-    if (!PRE_B && ep.bias) {
+    if (!PRE_B && has_bias(ep)) {
 #pragma unroll
       for (int j = 0; j < FN; ++j) bq[j] = bload(ep, j);
     }
@@ -232,39 +384,43 @@ template <int DT, int BM, int BN, int WGM, int WGN> struct PipeEpi {
       for (int i = 0; i < FM; ++i) roff[i] = long(m0 + wm * WTM + i * 16 + li) * ep.ldc;
       al8 = ((uintptr_t)ep.out & 7) == 0 && (ep.ldc & 3) == 0 && (off & 3) == 0;
     }
-    // the epilogue kinds the engine emits run a fragment loop with the
-    // chain fixed at compile time; any other (bias added before rounding,
-    // unaligned destination) takes the loop with runtime branches.
     // Interior tiles (the common case) store every fragment unconditionally.
     const bool interior = m0 + BM <= M && n0 + BN <= N;
-#define RQ(I, J) (!ep.resid ? make_uint2(0, 0) : PRE_R ? rq[(I) % RQM][(J) % RQN] : rload(ep, I, J))
-#define MH_EPI_FIXED(BIAS, ACT, RESID)                                                              \
-  _Pragma("unroll") for (int i = 0; i < FM; ++i) {                                                 \
-    const int m = m0 + wm * WTM + i * 16 + li;                                                     \
-    _Pragma("unroll") for (int j = 0; j < FN; ++j) {                                               \
-      const int n = n0 + wn * WTN + j * 16 + lg * 4;                                               \
-      if (interior || (m < M && n < N)) {                                                          \
-        float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};                     \
-        *reinterpret_cast<uint2 *>(cbase[j] + roff[i]) =                                           \
-            epi_fast_bf16_fixed<BIAS, ACT, RESID>(v, bq[j], RQ(i, j), ep.gelu_c);                  \
-      }                                                                                            \
-    }                                                                                              \
-  }
-    const bool fixed = al8 && !(ep.bias && ep.bias_first);
-    const bool hb = ep.bias != nullptr, hr = ep.resid != nullptr;
-    if (fixed && !hb && ep.act == ACT_NONE && !hr) {
-      MH_EPI_FIXED(false, ACT_NONE, false);
-    } else if (fixed && hb && ep.act == ACT_NONE && !hr) {
-      MH_EPI_FIXED(true, ACT_NONE, false);
-    } else if (fixed && hb && ep.act == ACT_GELU && !hr) {
-      MH_EPI_FIXED(true, ACT_GELU, false);
-    } else if (fixed && hb && ep.act == ACT_RELU && !hr) {
-      MH_EPI_FIXED(true, ACT_RELU, false);
-    } else if (fixed && hb && ep.act == ACT_NONE && hr) {
-      MH_EPI_FIXED(true, ACT_NONE, true);
-    } else if (fixed && !hb && ep.act == ACT_NONE && hr) {
-      MH_EPI_FIXED(false, ACT_NONE, true);
+#define RQ(I, J) (!has_resid(ep) ? make_uint2(0, 0) : PRE_R ? rq[(I) % RQM][(J) % RQN] : rload(ep, I, J))
+    if constexpr (KT_::FIXED) {
+      // folded LayerNorm: per-column terms (column sums of gamma (.) W,
+      // beta W) from LDS (ln_finish)
+      float4 lcs[FN], lbw[FN];
+      if constexpr (KT_::LN) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          lcs[j] = *reinterpret_cast<const float4 *>(lncs + wn * WTN + j * 16 + lg * 4);
+          lbw[j] = *reinterpret_cast<const float4 *>(lnbw + wn * WTN + j * 16 + lg * 4);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int m = m0 + wm * WTM + i * 16 + li;
+        float2 rs = make_float2(0.f, 0.f);
+        if constexpr (KT_::LN) rs = lnrow[wm * WTM + i * 16 + li];
+        StatAcc sa;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int n = n0 + wn * WTN + j * 16 + lg * 4;
+          float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+          if constexpr (KT_::LN) {
+            v[0] = rs.y * (v[0] - rs.x * lcs[j].x) + lbw[j].x;
+            v[1] = rs.y * (v[1] - rs.x * lcs[j].y) + lbw[j].y;
+            v[2] = rs.y * (v[2] - rs.x * lcs[j].z) + lbw[j].z;
+            v[3] = rs.y * (v[3] - rs.x * lcs[j].w) + lbw[j].w;
+          }
+          const uint2 pk = epi_fast_bf16_fixed<KT_::BIAS, KT_::ACT, KT_::RESID>(v, bq[j], RQ(i, j), ep.gelu_c);
+          if (interior || (m < M && n < N)) *reinterpret_cast<uint2 *>(cbase[j] + roff[i]) = pk;
+          if constexpr (KT_::ST) stats_add(ep, sa, pk, m, j);
+        }
+      }
     } else {
+      // any other chain (bias added before rounding, unaligned destination)
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         const int m = m0 + wm * WTM + i * 16 + li;
@@ -284,7 +440,6 @@ template <int DT, int BM, int BN, int WGM, int WGN> struct PipeEpi {
         }
       }
     }
-#undef MH_EPI_FIXED
 #undef RQ
   }
 };
@@ -299,7 +454,7 @@ template <int DT, int BM, int BN, int WGM, int WGN> struct PipeEpi {
   _Pragma("unroll") for (int i = 0; i < FM; ++i) _Pragma("unroll") for (int j = 0; j < FN; ++j)   \
       PipeMfma<DT>::mma0(acc[i][j], BF[j], AF[i]);
 
-template <int DT, int BM, int BN, int WGM, int WGN>
+template <int DT, int BM, int BN, int WGM, int WGN, int EK>
 __global__ void __launch_bounds__(WGM * WGN * 64)
 gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt, int M, int N, int K, long lda,
                  long ldb, long sa, long sb, long sc, EpiArgs ep) {
@@ -308,6 +463,8 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
   constexpr int ACH = BM * 8 / NT, BCH = BN * 8 / NT;
   static_assert(ACH >= 1 && BCH >= 1 && BM * 8 % NT == 0 && BN * 8 % NT == 0, "tile does not fit the thread count");
   __shared__ u32x4 lds[2][(BM + BN) * 8];  // [buf][A rows | Bt rows][8 chunks], chunk-swizzled
+  __shared__ float2 lnrow[BM];              // folded LayerNorm: row (mean, rstd)
+  __shared__ __attribute__((aligned(16))) float lncs[BN], lnbw[BN];  // and column terms
 
   int m0, n0;
   pipe_tile<BM, BN>(M, N, m0, n0);
@@ -367,13 +524,16 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
     if (t < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                \
   }
 
-  PipeEpi<DT, BM, BN, WGM, WGN> epi(ep, g, M, N, m0, n0);
+  typedef PipeEpi<DT, BM, BN, WGM, WGN, EK> Epi;
+  Epi epi(ep, g, M, N, m0, n0);
   epi.prefetch(ep);
 
   // slab 0 covers columns [0, K0), K0 = K % 64 (or 64): chunks at or past K0
   // are zero; every later slab is whole
   const int KT = (K + BK - 1) / BK, K0 = K - (KT - 1) * BK;
   u32x4 *L0 = lds[0], *L1 = lds[1];
+  typename Epi::LnIn lnin;
+  if constexpr (PipeKindT<EK>::LN) epi.ln_issue(ep, lnin, tid);
   {
     const bool cin = c0 * 8 < K0;
 #pragma unroll
@@ -382,6 +542,7 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
     for (int i = 0; i < BCH; ++i) rb[i] = cin ? ldg16(Bs + boff[i]) : u32x4{0, 0, 0, 0};
   }
   MH_PSTORE(L0);
+  if constexpr (PipeKindT<EK>::LN) epi.ln_finish(ep, lnin, lnrow, lncs, lnbw, tid);
   if (KT == 1) {
     __syncthreads();
     g.template frags<0>(L0, af0, bf0);
@@ -427,7 +588,9 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
 #undef MH_SCHED_A
 #undef MH_SCHED_B
 
-  epi.store(ep, acc, ep.mode == EPI_ROWMAJOR ? z * sc : 0, &lds[0][0], wave, lane);
+  epi.store(ep, acc, ep.mode == EPI_ROWMAJOR ? z * sc : 0, &lds[0][0], wave, lane,
+            PipeKindT<EK>::LN ? lnrow : nullptr, PipeKindT<EK>::LN ? lncs : nullptr,
+            PipeKindT<EK>::LN ? lnbw : nullptr);
 }
 
 // ---- direct-to-LDS kernel ----
@@ -447,7 +610,7 @@ __device__ __forceinline__ void dma16(const uint16_t *base, uint32_t voff, uint3
                : "memory", "m0");
 }
 
-template <int DT, int BM, int BN, int WGM, int WGN, int S>
+template <int DT, int BM, int BN, int WGM, int WGN, int S, int EK>
 __global__ void __launch_bounds__(WGM * WGN * 64)
 gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt, int M, int N, int K, long lda,
                 long ldb, long sa, long sb, long sc, EpiArgs ep) {
@@ -459,6 +622,8 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
   static_assert(S >= 2 && NDMA * (S - 1) < 64, "stages");
   constexpr uint32_t STAGE = (BM + BN) * 128;  // bytes per stage
   __shared__ u32x4 lds[S][(BM + BN) * 8];
+  __shared__ float2 lnrow[BM];  // folded LayerNorm: row (mean, rstd)
+  __shared__ __attribute__((aligned(16))) float lncs[BN], lnbw[BN];  // and column terms
 
   int m0, n0;
   pipe_tile<BM, BN>(M, N, m0, n0);
@@ -494,9 +659,12 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
 
   f32x4 acc[FM][FN];
   u32x4 af0[FM], bf0[FN], af1[FM], bf1[FN];
-  PipeEpi<DT, BM, BN, WGM, WGN> epi(ep, g, M, N, m0, n0);
+  typedef PipeEpi<DT, BM, BN, WGM, WGN, EK> Epi;
+  Epi epi(ep, g, M, N, m0, n0);
   epi.prefetch(ep);
 
+  typename Epi::LnIn lnin;
+  if constexpr (PipeKindT<EK>::LN) epi.ln_issue(ep, lnin, tid);
   // prologue: slabs 0 .. S-2 in flight (re-loading the last slab past the
   // end), wait for slab 0
 #pragma unroll
@@ -506,6 +674,7 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
     for (int t = 0; t < NDMA; ++t) MH_DMA(t, kt, s);
   }
   dma_wait<NDMA * (S - 2)>();
+  if constexpr (PipeKindT<EK>::LN) epi.ln_finish(ep, lnin, lnrow, lncs, lnbw, tid);
   __syncthreads();
   g.template frags<0>(lds[0], af0, bf0);
 
@@ -564,27 +733,40 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
   // epilogue reuses the LDS or the workgroup ends
   dma_wait<0>();
   __syncthreads();
-  epi.store(ep, acc, ep.mode == EPI_ROWMAJOR ? z * sc : 0, &lds[0][0], wave, lane);
+  epi.store(ep, acc, ep.mode == EPI_ROWMAJOR ? z * sc : 0, &lds[0][0], wave, lane,
+            PipeKindT<EK>::LN ? lnrow : nullptr, PipeKindT<EK>::LN ? lncs : nullptr,
+            PipeKindT<EK>::LN ? lnbw : nullptr);
 }
 
 #undef MH_PMMA
 #undef MH_PMMA0
 
-template <int DT, int BM, int BN, int WGM, int WGN>
+template <int DT, int BM, int BN, int WGM, int WGN, int EK = PK_GENERAL>
 void launch(const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch, long sa, long sb,
             long sc, const EpiArgs &ep, hipStream_t st) {
   const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_pipe_kernel<DT, BM, BN, WGM, WGN>), dim3(tiles, 1, batch), dim3(WGM * WGN * 64), 0, st,
+  hipLaunchKernelGGL((gemm_pipe_kernel<DT, BM, BN, WGM, WGN, EK>), dim3(tiles, 1, batch), dim3(WGM * WGN * 64), 0, st,
                      (const uint16_t *)A, (const uint16_t *)Bt, M, N, K, lda, ldb, sa, sb, sc, ep);
 }
 
-template <int DT, int BM, int BN, int WGM, int WGN, int S>
+template <int DT, int BM, int BN, int WGM, int WGN, int S, int EK = PK_GENERAL>
 void launch_dma(const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch, long sa, long sb,
                 long sc, const EpiArgs &ep, hipStream_t st) {
   const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_dma_kernel<DT, BM, BN, WGM, WGN, S>), dim3(tiles, 1, batch), dim3(WGM * WGN * 64), 0,
+  hipLaunchKernelGGL((gemm_dma_kernel<DT, BM, BN, WGM, WGN, S, EK>), dim3(tiles, 1, batch), dim3(WGM * WGN * 64), 0,
                      st, (const uint16_t *)A, (const uint16_t *)Bt, M, N, K, lda, ldb, sa, sb, sc, ep);
 }
 
 }  // namespace
+
+// Fixed epilogue programs (kind != PK_GENERAL) for bf16 on the tiles the
+// automatic choice uses: 0 128x128, 1 128x64, 2 64x64, 3 128x96
+// (register-staged, gemm_pipe_fixed_staged.hip) and 8 128x96 4 stages,
+// 9 128x128 2 stages (direct-to-LDS, gemm_pipe_fixed_dma.hip).  They return
+// hipErrorNotSupported for any other tile.
+hipError_t gemm_pipe_fixed_staged(int kind, int tile, const void *A, const void *Bt, int M, int N, int K, long lda,
+                                  long ldb, int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st);
+hipError_t gemm_pipe_fixed_dma(int kind, int tile, const void *A, const void *Bt, int M, int N, int K, long lda,
+                               long ldb, int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st);
+
 }  // namespace mh

@@ -44,6 +44,22 @@ struct EpiArgs {
   void *outs[3] = {nullptr, nullptr, nullptr};
   int T = 1, H = 1, hd = 1, E = 1;
   int convt_oc = 1, convt_k = 1, convt_ih = 1, convt_iw = 1;
+  // LayerNorm folded across a GEMM boundary (bf16 pipelined kernels only):
+  //   stats_out: the producer writes, for output row m and column group g of
+  //     stats_cols columns (16, 32, 48 or 64), (mean, M2) of the group's
+  //     rounded output values (M2 = sum of squared deviations from that
+  //     mean) at stats_out[2 * (m * (N / stats_cols) + g)];
+  //   ln_stats: the consumer's A rows are raw LayerNorm inputs x with
+  //     ln_parts such partials of ln_cols columns per row
+  //     (K = ln_cols * ln_parts), and its weights hold gamma (.) W; the
+  //     product becomes LN(x) W as rstd_m * (acc - mean_m * ln_cs[n]) +
+  //     ln_bw[n], with ln_cs the column sums of the folded weights and
+  //     ln_bw = beta W, before the epilogue chain.
+  float *stats_out = nullptr;
+  int stats_cols = 16;
+  const float *ln_stats = nullptr, *ln_cs = nullptr, *ln_bw = nullptr;
+  int ln_parts = 0, ln_cols = 16;
+  float ln_eps = 1e-5f;
 };
 
 // Implicit-GEMM convolution geometry (NHWC activation, ldx = pixel stride).
@@ -104,8 +120,11 @@ hipError_t binary(int dt, int op, const void *a, const void *b, void *out, const
 hipError_t unary(int dt, int op, const void *in, void *out, size_t n, float c, hipStream_t st);
 hipError_t masked_fill(int dt, const void *x, const int32_t *mask, void *out, size_t n, float value, hipStream_t st);
 hipError_t convert(int sdt, const void *in, int ddt, void *out, size_t n, hipStream_t st);
+// stats (optional): the LayerNorm statistics of each output row, one
+// (mean, M2) partial over all D columns (the stats_out layout of EpiArgs with
+// stats_cols = D).
 hipError_t embedding(int dt, const int32_t *ids, const void *w, const void *pos, void *out, int n, int V, int D,
-                     int T, int *err, hipStream_t st);
+                     int T, int *err, hipStream_t st, float *stats = nullptr);
 hipError_t argmax_rows(int dt, const void *x, int32_t *out, int rows, int cols, hipStream_t st);
 
 hipError_t layernorm(int dt, const void *x, const void *w, const void *b, void *y, int rows, int cols, float eps,

@@ -43,16 +43,57 @@ def test_mlp_plan_fuses_relu():
 
 
 def test_decoder_plan_structure_and_reuse():
+    """bf16 decoder: both LayerNorms of every block fold into the Linear
+    after them (the final one stays a kernel before the much wider vocabulary
+    head); the embedding (whole-row statistics, [M, 1, 2]) and the residual
+    GEMMs (per 32 columns at d = 128, [M, 4, 2]) write the f32 row partials
+    that the folded Linear reads."""
+    cfg = models.decoder_config(vocab=1000, ctx=256, d_model=128, num_heads=2, num_layers=3, ffn=512)
+    assert cfg["dtype"] == "bfloat16"
+    e, p = _plan(cfg, (2, 256))
+    ops = p["ops"]
+    kinds = [o["kind"] for o in ops]
+    per_layer = ["qkv_gemm", "attention", "gemm", "gemm", "gemm"]
+    assert kinds == ["embedding_pos"] + per_layer * 3 + ["layer_norm", "gemm"]
+    st = e.stats()
+    assert st["fused_epilogues"] == 3 * 3  # out_proj+resid, ffn0+gelu, ffn2+resid per layer
+    assert st["ln_folds"] == 2 * 3
+    # producers: embedding, then out_proj and ffn.2 of every layer; consumers:
+    # qkv, ffn.0 of every layer and the head; each stats value links one pair
+    producers = [i for i, o in enumerate(ops) if o["stats_out"] >= 0]
+    consumers = [i for i, o in enumerate(ops) if o["ln_stats"] >= 0]
+    assert producers == [0] + [1 + 5 * l + j for l in range(3) for j in (2, 4)][:-1]
+    assert consumers == [1 + 5 * l + j for l in range(3) for j in (0, 3)]
+    for pi, ci in zip(producers, consumers):
+        sv = ops[pi]["stats_out"]
+        assert ops[ci]["ln_stats"] == sv and sv in ops[pi]["out"] and sv in ops[ci]["in"]
+        assert p["values"][sv]["shape"] == [2 * 256, 1 if pi == 0 else 128 // 32, 2]
+        assert p["values"][sv]["dtype"] == 0
+    total = _check_arena(p)
+    assert p["arena_bytes"] < total / 2  # liveness reuse
+    assert e.out_shape == (2, 256, 1000)
+
+
+def test_decoder_plan_without_ln_fold(monkeypatch):
+    """MUNET_HIP_LN_FOLD=0 keeps the LayerNorm ops (the unfolded reference
+    structure)."""
+    monkeypatch.setenv("MUNET_HIP_LN_FOLD", "0")
     cfg = models.decoder_config(vocab=1000, ctx=256, d_model=128, num_heads=2, num_layers=3, ffn=512)
     e, p = _plan(cfg, (2, 256))
     kinds = [o["kind"] for o in p["ops"]]
     per_layer = ["layer_norm", "qkv_gemm", "attention", "gemm", "layer_norm", "gemm", "gemm"]
     assert kinds == ["embedding_pos"] + per_layer * 3 + ["layer_norm", "gemm"]
-    st = e.stats()
-    assert st["fused_epilogues"] == 3 * 3  # out_proj+resid, ffn0+gelu, ffn2+resid per layer
-    total = _check_arena(p)
-    assert p["arena_bytes"] < total / 2  # liveness reuse
-    assert e.out_shape == (2, 256, 1000)
+    assert e.stats()["ln_folds"] == 0
+    assert all(o["stats_out"] < 0 and o["ln_stats"] < 0 for o in p["ops"])
+
+
+def test_fp16_decoder_keeps_layer_norm():
+    """The fold exists only on the bf16 fast epilogue."""
+    cfg = models.decoder_config(vocab=1000, ctx=256, d_model=128, num_heads=2, num_layers=1, ffn=512,
+                                dtype="float16")
+    e, p = _plan(cfg, (2, 256))
+    assert [o["kind"] for o in p["ops"]].count("layer_norm") == 3
+    assert e.stats()["ln_folds"] == 0
 
 
 @pytest.mark.parametrize("which", ["mlp", "decoder", "unet"])
@@ -100,7 +141,8 @@ def test_full_gpt_plan_fits_and_reuses():
     cfg = models.decoder_config()
     e, p = _plan(cfg, (4, 1024))
     st = e.stats()
-    assert st["ops"] == 1 + 12 * 7 + 2
+    assert st["ops"] == 1 + 12 * 5 + 2  # embedding, 5 per layer (both LayerNorms folded), ln_f, head
+    assert st["ln_folds"] == 24
     assert e.out_shape == (4, 1024, 32000)
     _check_arena(p)
     # logits (262 MB) + a few activations; far below one buffer per op
