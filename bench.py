@@ -9,12 +9,12 @@ One step = one compiled forward (one hipGraph launch) over the resident
 [4, 1024] ids already in HBM.  W untimed warm-up steps, then exactly K timed
 steps bracketed by torch.cuda.synchronize() on both sides.
 
-Roofline: every kernel of the forward is also timed on its own with HIP
-events on the stream it runs on (20 launches captured in one graph and
-replayed, so host launch cost is excluded); the kernel with the largest time
-per forward is reported
-against the bf16 MFMA peak (GEMM / attention: algorithmic 2*M*N*K FLOPs) or
-the HBM peak (LayerNorm: unique bytes).  CPU baseline: the C++ restatement
+Roofline: every op of the compiled forward is also timed on its own with
+HIP events on the engine stream it runs on (mh_engine_op_times: 20 launches
+of the op captured in one graph and replayed, so host launch cost is
+excluded); the kernel with the largest time per forward is reported against
+the bf16 MFMA peak (GEMM / attention: algorithmic 2*M*N*K FLOPs) or the HBM
+peak (LayerNorm: unique bytes).  CPU baseline: the C++ restatement
 of MuNet's CPU backend (oracle/, "port") on a bounded sample of the same
 forward, timed on this host.
 """
@@ -42,95 +42,61 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def kernel_specs(hip, torch):
-    """(name, launch, launches per forward, FLOPs, bytes) for every distinct
-    kernel of the forward, on inputs of the forward's shapes."""
-    from munet_amd.backend import empty
-    d, H, F, V = CFG["d_model"], CFG["num_heads"], CFG["ffn"], CFG["vocab"]
-    M, hd, L = B * T, d // H, CFG["num_layers"]
-    bf = torch.bfloat16
-    g = torch.Generator(device="cuda").manual_seed(0)
-
-    def rnd(*s, scale=1.0):
-        return (torch.randn(*s, device="cuda", generator=g) * scale).to(bf)
-
-    x, w = rnd(M, d), rnd(M, F)
-    specs = []
-
-    def linear(name, K_, N_, act, resid):
-        a = x if K_ == d else w
-        wt = rnd(N_, K_, scale=0.02)
-        bias = torch.zeros(N_, device="cuda", dtype=bf)
-        out = empty((M, N_), 2)
-        r = rnd(M, N_) if resid else None
-        specs.append((name, lambda: hip.linear(a, wt, bias, out, M, K_, N_, act, r), 1 if name == "lm_head" else L,
-                      2.0 * M * N_ * K_, 0.0))
-
-    linear("ffn_up_gelu", d, F, 2, False)
-    linear("ffn_down_resid", F, d, 0, True)
-    linear("attn_out_resid", d, d, 0, True)
-    linear("lm_head", d, V, 0, False)
-    wqkv = rnd(3 * d, d, scale=0.02)
-    bq = torch.zeros(3 * d, device="cuda", dtype=bf)
-    q, k, v = (empty((M * d,), 2) for _ in range(3))
-    specs.append(("qkv_headsplit", lambda: hip.qkv_projection(x, wqkv, bq, q, k, v, B, T, d, H), L,
-                  2.0 * M * 3 * d * d, 0.0))
-    ctx = empty((M, d), 2)
-    specs.append(("attention_causal", lambda: hip.attention(q, k, v, ctx, B, H, T, hd, True), L,
-                  4.0 * B * H * T * T * hd / 2, 0.0))
-    lw, lb, ly = rnd(d), rnd(d), empty((M, d), 2)
-    specs.append(("layer_norm", lambda: hip.layer_norm(x, lw, lb, ly, M, d), 2 * L + 1, 0.0,
-                  2.0 * M * d * 2 + 2 * d * 2))
-    return specs
+# ops of the compiled forward grouped into the kernels of the roofline table
+def op_category(op):
+    name, kind = op["name"], op["kind"]
+    if kind == "qkv_gemm":
+        return "qkv_headsplit"
+    if kind == "attention":
+        return "attention_causal"
+    if kind == "layer_norm":
+        return "layer_norm"
+    if kind.startswith("embedding"):
+        return "embedding"
+    if name.endswith("out_proj"):
+        return "attn_out_resid"
+    if ".ff.0" in name:
+        return "ffn_up_gelu"
+    if ".ff.2" in name:
+        return "ffn_down_resid"
+    if name.startswith("head"):
+        return "lm_head"
+    return name
 
 
-def kernel_table(hip, torch):
-    """Per-kernel timing (graph-replayed, HIP events) of every distinct kernel
-    of the forward."""
-    rows = []
-    for name, fn, count, flops, bytes_ in kernel_specs(hip, torch):
-        # `reps` launches captured in one HIP graph on a side stream and
-        # replayed between HIP events on that stream: GPU time per launch,
-        # free of host launch overhead (the engine replays a graph too)
-        reps = 20
-        st = torch.cuda.Stream()
-        with torch.cuda.stream(st):
-            fn()
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=st):
-            for _ in range(reps):
-                fn()
-        with torch.cuda.stream(st):
-            graph.replay()
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-            graph.replay()
-            e.record()
-        torch.cuda.synchronize()
-        t = s.elapsed_time(e) / reps * 1e-3
-        rows.append(dict(name=name, t=t, count=count, flops=flops, bytes=bytes_))
-    return rows
+def kernel_table(eng, reps=20):
+    """Per-kernel timing of the compiled forward's own ops (the LayerNorm-
+    folded consumers and the statistics-producing residual GEMMs as the
+    forward runs them): mh_engine_op_times replays each op `reps` times from
+    one graph between HIP events on the engine stream, after a full forward
+    that restores its inputs.  Rows: one per kernel category with the mean
+    time per launch, launches per forward and algorithmic work per launch."""
+    cats = {}
+    for op in eng.op_times(reps):
+        c = cats.setdefault(op_category(op), dict(ts=[], flops=op["flops"], bytes=op["bytes"], first=op["name"]))
+        c["ts"].append(op["us"] * 1e-6)
+    return [dict(name=n, t=sum(c["ts"]) / len(c["ts"]), count=len(c["ts"]), flops=c["flops"], bytes=c["bytes"],
+                 op=c["first"]) for n, c in cats.items()]
 
 
 COPY_BYTES = 256 << 20  # the calibration copy of --probe
 
 
-def probe(hip, torch, name):
-    """For rocprofv3 --pmc passes: 5 eager launches of one kernel of the
-    forward, then one device-to-device copy of COPY_BYTES (the counter
+def probe(eng, torch, name):
+    """For rocprofv3 --pmc passes: one forward, then 5 replayed launches of
+    the first op of category `name` (mh_engine_op_times restricted to that
+    op), then one device-to-device copy of COPY_BYTES (the counter
     calibration: it reads and writes exactly that many bytes)."""
-    spec = {s[0]: s for s in kernel_specs(hip, torch)}[name]
+    op = next(r["op"] for r in kernel_table(eng, 1) if r["name"] == name)
     torch.cuda.synchronize()
-    for _ in range(5):
-        spec[1]()
+    eng.op_times(5, only=op)
     torch.cuda.synchronize()
     a = torch.ones(COPY_BYTES // 2, device="cuda", dtype=torch.bfloat16)
     b = torch.empty_like(a)
     torch.cuda.synchronize()
     b.copy_(a)
     torch.cuda.synchronize()
-    log(f"probe: {name} x5, copy {COPY_BYTES} bytes")
+    log(f"probe: {name} ({op}) x5 after a forward, copy {COPY_BYTES} bytes")
 
 
 def measured_traffic(name):
@@ -189,13 +155,8 @@ def main():
     import ctypes
 
     from munet_amd import _lib, models
-    from munet_amd.backend import HipBackend
     from munet_amd.engine import Engine
 
-    hip = HipBackend(0)
-    if args.probe:
-        probe(hip, torch, args.probe)
-        return
     cfg = models.decoder_config(**CFG)
     log("bench: initialising weights")
     params = models.init_params(cfg, "gpt", scope="bench")
@@ -205,6 +166,9 @@ def main():
     del params
     logits = eng.run(ids)  # places the ids in the engine's input buffer (HBM)
     assert np.isfinite(logits[:, :8].astype(np.float32)).all()
+    if args.probe:
+        probe(eng, torch, args.probe)
+        return
 
     for _ in range(args.warmup):
         eng.launch()
@@ -226,7 +190,7 @@ def main():
     if not np.array_equal(again.view(np.uint16), logits.view(np.uint16)):
         raise SystemExit("bench: repeated forwards changed the logits")
 
-    rows = kernel_table(hip, torch)
+    rows = kernel_table(eng)
     for r in rows:
         r["per_fwd"] = r["t"] * r["count"]
     dom = max(rows, key=lambda r: r["per_fwd"])

@@ -98,6 +98,13 @@ int mh_engine_pinned_io(mh_engine *engine, void **host_input, void **host_output
 int mh_engine_run_pinned(mh_engine *engine);
 /* The compiled plan (ops, fused epilogues, arena offsets) as JSON. */
 int mh_engine_plan(mh_engine *engine, char *buf, size_t len);
+/* GPU time of every op of the compiled forward (or only the ops named
+ * `only`, when not NULL or empty) on its own, as a JSON list of
+ * {name, kind, us, flops, bytes} (us per launch over `reps` launches replayed
+ * from one graph on the engine stream; flops / bytes: the op's algorithmic
+ * work).  Per-op counterpart of the reference's module Profiler
+ * (src/core/module.hpp:71-83, src/core/util/profiler.hpp). */
+int mh_engine_op_times(mh_engine *engine, int reps, const char *only, char *buf, size_t len);
 
 #ifdef __cplusplus
 }

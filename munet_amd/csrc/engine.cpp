@@ -864,6 +864,73 @@ struct EngineImpl {
     ++runs;
   }
 
+  // Algorithmic work of one op: FLOPs of its products (GEMM 2 M N K,
+  // attention 4 B H T^2 hd, halved when causal) and the unique bytes a
+  // memory-bound op reads and writes (LayerNorm 2 M d s + 2 d s, embedding
+  // 3 M d s + 4 M).
+  void op_work(const Op &o, double &flops, double &bytes) const {
+    const double es = double(dt_size(dt));
+    flops = bytes = 0.0;
+    switch (o.kind) {
+    case OP_GEMM: flops = 2.0 * o.a[0] * o.a[1] * o.a[2]; break;
+    case OP_QKV: flops = 2.0 * o.a[0] * o.a[1] * 3.0 * o.a[2] * o.a[2]; break;
+    case OP_ATTN: flops = 4.0 * o.a[0] * o.a[1] * double(o.a[2]) * o.a[2] * o.a[3] * (o.a[4] ? 0.5 : 1.0); break;
+    case OP_LN: bytes = (2.0 * o.a[0] * o.a[1] + 2.0 * o.a[1]) * es; break;
+    case OP_EMBED: case OP_EMBED_POS: bytes = 3.0 * o.a[0] * o.a[2] * es + 4.0 * o.a[0]; break;
+    default: break;
+    }
+  }
+
+  // GPU time of each op of the compiled forward on its own (the per-module
+  // timings of the reference's Profiler, src/core/module.hpp:71-83, for the
+  // compiled graph): before each op a full forward restores every value, then
+  // `reps` launches of the op, captured in one graph on the engine stream, are
+  // replayed once to warm and once between events.  An op never writes the
+  // values it reads (the planner keeps them live through it), so its replays
+  // recompute the same outputs.
+  // only: time just the ops of that name (nullptr or "": every op).
+  std::string op_times_json(int reps, const char *only) {
+    require_device();
+    if (reps < 1 || reps > 1000) throw Error("op_times: reps must be in 1..1000");
+    std::ostringstream s;
+    s << "[";
+    bool first = true;
+    for (size_t i = 0; i < ops.size(); ++i) {
+      if (only && *only && ops[i].name != only) continue;
+      hip_check(hipGraphLaunch(exec, stream), "hipGraphLaunch");
+      hipGraph_t g = nullptr;
+      hipGraphExec_t x = nullptr;
+      hip_check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+      try {
+        for (int r = 0; r < reps; ++r) enqueue(ops[i]);
+      } catch (...) {
+        (void)hipStreamEndCapture(stream, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+      }
+      hip_check(hipStreamEndCapture(stream, &g), "hipStreamEndCapture");
+      float ms = 0.f;
+      hipError_t err = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+      if (err == hipSuccess) err = hipGraphLaunch(x, stream);
+      if (err == hipSuccess) err = hipEventRecord(ev0, stream);
+      if (err == hipSuccess) err = hipGraphLaunch(x, stream);
+      if (err == hipSuccess) err = hipEventRecord(ev1, stream);
+      if (err == hipSuccess) err = hipStreamSynchronize(stream);
+      if (err == hipSuccess) err = hipEventElapsedTime(&ms, ev0, ev1);
+      if (x) (void)hipGraphExecDestroy(x);
+      (void)hipGraphDestroy(g);
+      hip_check(err, "op_times replay");
+      double flops, bytes;
+      op_work(ops[i], flops, bytes);
+      s << (first ? "" : ",") << "{\"name\":\"" << ops[i].name << "\",\"kind\":\"" << op_name(ops[i].kind)
+        << "\",\"us\":" << double(ms) * 1000.0 / reps << ",\"flops\":" << flops << ",\"bytes\":" << bytes << "}";
+      first = false;
+    }
+    s << "]";
+    hip_check(hipStreamSynchronize(stream), "op_times");
+    return s.str();
+  }
+
   void check_error_flag() {
     int flag = 0;
     hip_check(hipMemcpy(&flag, device_error_flag(), sizeof(int), hipMemcpyDeviceToHost), "error flag");
@@ -1337,5 +1404,9 @@ int mh_engine_stream(mh_engine *e, void **s) {
 }
 int mh_engine_stats(mh_engine *e, char *buf, size_t len) { ENG_TRY(put_str(e->stats_json(), buf, len)) }
 int mh_engine_plan(mh_engine *e, char *buf, size_t len) { ENG_TRY(put_str(e->impl.plan_json(), buf, len)) }
+
+int mh_engine_op_times(mh_engine *e, int reps, const char *only, char *buf, size_t len) {
+  ENG_TRY(put_str(e->impl.op_times_json(reps, only), buf, len))
+}
 
 }  // extern "C"

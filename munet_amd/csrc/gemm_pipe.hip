@@ -20,22 +20,21 @@ int pipe_wave_cols(int tile) {
   }
 }
 
-// Automatic block tile, measured on MI355X (decoder shapes, K = 768 / 3072,
-// M = 4096):
+// Automatic block tile, measured on MI355X inside the decoder forward
+// (K = 768 / 3072, M = 4096):
 //  * N tiling evenly by 96 with at most one tile per CU (N = 768: FFN down,
 //    attention out-projection): direct-to-LDS 128x96, 4 stages (one
 //    workgroup per CU, so deep stages hide the memory latency);
-//  * at least 8 tiles per CU at 128x128 (the LM head): direct-to-LDS 128x128,
-//    2 stages (two workgroups per CU);
 //  * otherwise register-staged: 128x128 when N tiles evenly by 128 and there
-//    are >= 2.5 tiles per CU (FFN up), 128x96 when N tiles evenly by 96
-//    (QKV), else 128x128 / 128x64 / 64x64 by tile count.
+//    are >= 2.5 tiles per CU (FFN up, LM head), 128x96 when N tiles evenly by
+//    96 (QKV), else 128x128 / 128x64 / 64x64 by tile count.
+// (Direct-to-LDS 128x128 with 2 stages runs the LM head 5% faster replayed on
+// its own, and 20 us slower inside the forward.)
 int auto_tile(bool dma, int M, int N, int K, int batch) {
   const long t128 = long((M + 127) / 128) * ((N + 127) / 128) * batch;
   const long t96 = long((M + 127) / 128) * ((N + 95) / 96) * batch;
   const long t64 = long((M + 127) / 128) * ((N + 63) / 64) * batch;
   if (dma && N % 96 == 0 && t96 <= 256) return 8;
-  if (dma && N % 128 == 0 && t128 >= 2048) return 9;
   if (N % 128 == 0 && t128 >= 640) return 0;
   if (N % 96 == 0) return 3;
   return (t128 >= 640 || (K >= 2048 && t128 >= 128)) ? 0 : (t64 >= 256 ? 1 : 2);

@@ -265,19 +265,23 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
                                             float *lnbw, int tid) const {
     const int r = tid / TPR, q = tid % TPR, P = ep.ln_parts;
     const int share = ((P + TPR - 1) / TPR + 1) & ~1, k0 = q * share, k1 = min(k0 + share, P);
+    // every partial covers w columns, so after i partials n = i w and Chan's
+    // update weights are the constants 1 / (i + 1) and i / (i + 1)
     const float w = float(ep.ln_cols);
-    float n = 0.f, mean = 0.f, m2 = 0.f;
+    float mean = 0.f, m2 = 0.f, m2x = 0.f;  // m2x: the between-partial term / w
 #pragma unroll
     for (int i = 0; i < LNCH; ++i) {
       if (k0 + i < k1) {
         const float pm = i & 1 ? in.part[i / 2].z : in.part[i / 2].x;
         const float p2 = i & 1 ? in.part[i / 2].w : in.part[i / 2].y;
-        const float nn = n + w, d = pm - mean;
-        mean += d * (w / nn);
-        m2 += p2 + d * d * (n * (w / nn));
-        n = nn;
+        const float d = pm - mean;
+        mean += d * (1.0f / float(i + 1));
+        m2 += p2;
+        m2x += d * d * (float(i) / float(i + 1));
       }
     }
+    m2 += m2x * w;
+    float n = float(max(min(k1 - k0, LNCH), 0)) * w;
 #pragma unroll
     for (int o = 1; o < TPR; o <<= 1) {
       const float on = __shfl_xor(n, o), om = __shfl_xor(mean, o), o2 = __shfl_xor(m2, o);

@@ -183,11 +183,11 @@ class Engine:
         return p.value
 
     # -- introspection --------------------------------------------------------
-    def _json(self, fn, size=1 << 16):
+    def _json(self, fn, size=1 << 16, *args):
         while True:
             buf = ctypes.create_string_buffer(size)
             try:
-                _lib.call(fn, self._h, buf, size)
+                _lib.call(fn, self._h, *args, buf, size)
                 return json.loads(buf.value.decode())
             except _lib.HipError as e:
                 if "buffer too small" not in str(e):
@@ -199,6 +199,12 @@ class Engine:
 
     def plan(self) -> dict:
         return self._json("mh_engine_plan", 1 << 20)
+
+    def op_times(self, reps: int = 20, only: str | None = None) -> list:
+        """GPU time of every op of the compiled forward (or only the ops named
+        ``only``) on its own: a list of {name, kind, us, flops, bytes}
+        (mh_engine_op_times)."""
+        return self._json("mh_engine_op_times", 1 << 20, reps, (only or "").encode())
 
     def close(self):
         if self._h is not None:
