@@ -4,6 +4,8 @@
 // picks the block tile and the epilogue program.  The fixed bf16 programs
 // are instantiated in gemm_pipe_fixed_*.hip, 256-row tiles in
 // gemm_pipe_big.hip.
+#include <algorithm>
+#include <cstdlib>
 #include "gemm_pipe.hpp"
 
 namespace mh {
@@ -127,8 +129,16 @@ hipError_t gemm_pipe(int dt, const void *A, const void *Bt, int M, int N, int K,
                          !ep.ln_cs || !ep.ln_bw || batch != 1)))
       return hipErrorInvalidValue;
   }
-  if (dt == BF16) return launch_dt<BF16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile, kind, st);
-  return launch_dt<F16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile, kind, st);
+  // tile enumeration: column groups once W is at least half of A (measured
+  // on the decoder's forward, cold weights: QKV and FFN up -2.5 to -3.5 us
+  // with 8 columns, the vocabulary head -45 us with 16; FFN down and
+  // out-proj, whose A is 4-5x W, stay on row groups); MUNET_HIP_XCD_GN
+  // overrides it for every GEMM
+  EpiArgs e = ep;
+  e.xcd_gn = 2L * N >= M ? (N >= 4L * M ? 16 : 8) : 0;
+  if (const char *gn = std::getenv("MUNET_HIP_XCD_GN")) e.xcd_gn = std::max(0, std::atoi(gn));
+  if (dt == BF16) return launch_dt<BF16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, e, tile, kind, st);
+  return launch_dt<F16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, e, tile, kind, st);
 }
 
 }  // namespace mh

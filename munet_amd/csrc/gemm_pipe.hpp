@@ -94,16 +94,28 @@ template <> struct PipeMfma<F16> {
   }
 };
 
-// Output tile of this workgroup: workgroups are dealt round-robin to the 8
-// XCDs, so the tile index is remapped to give each XCD a contiguous band of
-// tiles, then grouped along M so that consecutive tiles share Bt panels in
-// that XCD's L2 (the same order as gemm.hip).
+// Output tile of this workgroup.  Workgroups are dealt round-robin to the 8
+// XCDs (pid & 7), each with its own L2, so the tile index is first remapped
+// to give each XCD a contiguous eighth of an enumeration of the tile grid.
+// gn = 0: the enumeration walks groups of GROUP tile rows across all
+// columns, so an XCD holds a band of A rows and about half of W (A is read
+// about twice, W about four times; best when A is the larger operand).
+// gn > 0: it walks groups of gn tile columns, row by row across the group,
+// so an XCD holds about 1/8 of W and A is re-read once per group (best when W
+// is as large as A or larger: the weights arrive cold from HBM in a forward).
 template <int BM, int BN>
-__device__ __forceinline__ void pipe_tile(int M, int N, int &m0, int &n0) {
+__device__ __forceinline__ void pipe_tile(int M, int N, int gn, int &m0, int &n0) {
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, ntiles = tiles_m * tiles_n;
   int pid = blockIdx.x;
-  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
   constexpr int GROUP = 8;
+  if (gn > 0 && (ntiles & 7) == 0) {
+    const int t = (pid & 7) * (ntiles >> 3) + (pid >> 3), span = gn * tiles_m;
+    const int g = t / span, r = t - g * span, w = min(gn, tiles_n - g * gn);
+    m0 = (r / w) * BM;
+    n0 = (g * gn + r % w) * BN;
+    return;
+  }
+  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
   const int span = GROUP * tiles_n, gid = pid / span, fm = gid * GROUP, gs = min(tiles_m - fm, GROUP);
   m0 = (fm + (pid % span) % gs) * BM;
   n0 = ((pid % span) / gs) * BN;
@@ -471,7 +483,7 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
   __shared__ __attribute__((aligned(16))) float lncs[BN], lnbw[BN];  // and column terms
 
   int m0, n0;
-  pipe_tile<BM, BN>(M, N, m0, n0);
+  pipe_tile<BM, BN>(M, N, ep.xcd_gn, m0, n0);
   const int z = blockIdx.z;
   A += z * sa;
   Bt += z * sb;
@@ -630,7 +642,7 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
   __shared__ __attribute__((aligned(16))) float lncs[BN], lnbw[BN];  // and column terms
 
   int m0, n0;
-  pipe_tile<BM, BN>(M, N, m0, n0);
+  pipe_tile<BM, BN>(M, N, ep.xcd_gn, m0, n0);
   const int z = blockIdx.z;
   A += z * sa;
   Bt += z * sb;

@@ -60,6 +60,9 @@ struct EpiArgs {
   const float *ln_stats = nullptr, *ln_cs = nullptr, *ln_bw = nullptr;
   int ln_parts = 0, ln_cols = 16;
   float ln_eps = 1e-5f;
+  // pipelined GEMMs: tile columns per group of the per-XCD tile enumeration
+  // (0: groups of 8 tile rows instead); set by the GEMM launcher
+  int xcd_gn = 0;
 };
 
 // Implicit-GEMM convolution geometry (NHWC activation, ldx = pixel stride).

@@ -73,3 +73,33 @@ def test_tiles_bit_identical_to_128(tile, hip, monkeypatch):
         torch.cuda.synchronize()
         res.append(torch.cat([q, k, v]).view(torch.int16).clone())
     assert torch.equal(res[0], res[1]), f"tile {tile} head split"
+
+
+@pytest.mark.parametrize("tile", [None, 200, 203, 208, 209])
+def test_xcd_tile_enumeration_bit_identical(tile, hip, monkeypatch):
+    """The per-XCD tile enumeration (row groups, or column groups of any width,
+    a ragged last group included) only reorders the tiles: every output is
+    computed by the same tile code, so the outputs are bit-identical.  Shapes
+    have a tile count divisible by 8 (the enumeration applies) at 128x128,
+    128x96 and both; None is the automatic tile."""
+    import torch
+    from munet_amd.backend import empty
+    if tile is not None:
+        monkeypatch.setenv("MUNET_HIP_GEMM_TILE", str(tile))
+    g = torch.Generator(device="cuda").manual_seed(9)
+    bf = torch.bfloat16
+    for (M, K, N) in [(1024, 192, 768), (512, 128, 1536), (256, 320, 3072), (2048, 64, 384)]:
+        x = torch.randn(M, K, device="cuda", generator=g).to(bf)
+        wt = (torch.randn(N, K, device="cuda", generator=g) * 0.1).to(bf)
+        bias = (torch.randn(N, device="cuda", generator=g) * 0.1).to(bf)
+        r = torch.randn(M, N, device="cuda", generator=g).to(bf)
+        for act, resid in [(2, None), (0, r)]:
+            outs = []
+            for gn in ("0", "1", "3", "8", "16", "64"):
+                monkeypatch.setenv("MUNET_HIP_XCD_GN", gn)
+                out = empty((M, N), 2)
+                hip.linear(x, wt, bias, out, M, K, N, act, resid)
+                torch.cuda.synchronize()
+                outs.append(out.view(torch.int16).clone())
+            for gn, o in zip(("1", "3", "8", "16", "64"), outs[1:]):
+                assert torch.equal(outs[0], o), f"tile {tile} gn {gn} {M}x{K}x{N} act={act}"
