@@ -11,10 +11,16 @@ steps bracketed by torch.cuda.synchronize() on both sides.
 
 Roofline: every op of the compiled forward is also timed on its own with
 HIP events on the engine stream it runs on (mh_engine_op_times: 20 launches
-of the op captured in one graph and replayed, so host launch cost is
-excluded); the kernel with the largest time per forward is reported against
-the bf16 MFMA peak (GEMM / attention: algorithmic 2*M*N*K FLOPs) or the HBM
-peak (LayerNorm: unique bytes).  CPU baseline: the C++ restatement
+of the op captured in one graph and replayed between events, so host launch
+cost is excluded; the rocprofv3 kernel trace of the same command shows the
+same per-dispatch durations); the kernel with the largest time per forward
+is reported against the bf16 MFMA peak (GEMM / attention: algorithmic
+2*M*N*K FLOPs) or the HBM peak (LayerNorm: unique bytes).  Inside the
+forward the kernels run with colder caches: "kernels_in_forward_avg_us"
+(mh_engine_forward_op_times: differences of prefix-graph times, each over 20
+replays; an op's figure also carries what it costs the ops after it, such as
+the write-back of its output, and the first op carries the graph launch).
+CPU baseline: the C++ restatement
 of MuNet's CPU backend (oracle/, "port") on a bounded sample of the same
 forward, timed on this host.
 """
@@ -64,15 +70,17 @@ def op_category(op):
     return name
 
 
-def kernel_table(eng, reps=20):
+def kernel_table(eng, reps=20, in_forward=True):
     """Per-kernel timing of the compiled forward's own ops (the LayerNorm-
     folded consumers and the statistics-producing residual GEMMs as the
-    forward runs them): mh_engine_op_times replays each op `reps` times from
-    one graph between HIP events on the engine stream, after a full forward
-    that restores its inputs.  Rows: one per kernel category with the mean
-    time per launch, launches per forward and algorithmic work per launch."""
+    forward runs them).  in_forward: mh_engine_forward_op_times, differences
+    of prefix-graph times, each over `reps` replays (the forward's own caches
+    and transitions); otherwise mh_engine_op_times, each op replayed `reps`
+    times from one graph (warm caches).  Rows: one per kernel
+    category with the mean time per launch, launches per forward and
+    algorithmic work per launch."""
     cats = {}
-    for op in eng.op_times(reps):
+    for op in (eng.forward_op_times(reps) if in_forward else eng.op_times(reps)):
         c = cats.setdefault(op_category(op), dict(ts=[], flops=op["flops"], bytes=op["bytes"], first=op["name"]))
         c["ts"].append(op["us"] * 1e-6)
     return [dict(name=n, t=sum(c["ts"]) / len(c["ts"]), count=len(c["ts"]), flops=c["flops"], bytes=c["bytes"],
@@ -87,7 +95,7 @@ def probe(eng, torch, name):
     the first op of category `name` (mh_engine_op_times restricted to that
     op), then one device-to-device copy of COPY_BYTES (the counter
     calibration: it reads and writes exactly that many bytes)."""
-    op = next(r["op"] for r in kernel_table(eng, 1) if r["name"] == name)
+    op = next(r["op"] for r in kernel_table(eng, 1, in_forward=False) if r["name"] == name)
     torch.cuda.synchronize()
     eng.op_times(5, only=op)
     torch.cuda.synchronize()
@@ -190,7 +198,8 @@ def main():
     if not np.array_equal(again.view(np.uint16), logits.view(np.uint16)):
         raise SystemExit("bench: repeated forwards changed the logits")
 
-    rows = kernel_table(eng)
+    rows = kernel_table(eng, in_forward=False)
+    fwd = {r["name"]: round(r["t"] * 1e6, 2) for r in kernel_table(eng, in_forward=True)}
     for r in rows:
         r["per_fwd"] = r["t"] * r["count"]
     dom = max(rows, key=lambda r: r["per_fwd"])
@@ -232,6 +241,7 @@ def main():
         "gemm_mfma_frac": gemm_frac,
         "layernorm_hbm_frac": (ln["bytes"] / ln["t"]) / PEAK_HBM,
         "kernels": kernels,
+        "kernels_in_forward_avg_us": fwd,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -105,6 +105,13 @@ int mh_engine_plan(mh_engine *engine, char *buf, size_t len);
  * work).  Per-op counterpart of the reference's module Profiler
  * (src/core/module.hpp:71-83, src/core/util/profiler.hpp). */
 int mh_engine_op_times(mh_engine *engine, int reps, const char *only, char *buf, size_t len);
+/* GPU time of every op inside the compiled forward, as the same JSON list:
+ * for each prefix ops[0..i] of the forward, a graph of that prefix is
+ * replayed `reps` times between events, and op i's time is the difference of
+ * consecutive prefix times (the caches and transitions of the graph; op 0
+ * also holds the graph launch overhead).  The in-graph side of the same
+ * Profiler (src/core/module.hpp:71-83). */
+int mh_engine_forward_op_times(mh_engine *engine, int reps, char *buf, size_t len);
 
 #ifdef __cplusplus
 }

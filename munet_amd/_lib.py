@@ -87,6 +87,7 @@ _SIGS = {
     "mh_engine_stats": [_vp, ctypes.c_char_p, _sz],
     "mh_engine_plan": [_vp, ctypes.c_char_p, _sz],
     "mh_engine_op_times": [_vp, ctypes.c_int, ctypes.c_char_p, ctypes.c_char_p, _sz],
+    "mh_engine_forward_op_times": [_vp, ctypes.c_int, ctypes.c_char_p, _sz],
     "mh_engine_stream": [_vp, ctypes.POINTER(_vp)],
     "mh_engine_compile_expected": [_vp, _ip, _i, _ip],
     "mh_engine_output_shape_for": [_vp, _ip, _i, _ip, _ip],

@@ -26,6 +26,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <iomanip>
 #include <sstream>
 #include <string>
 #include <vector>
@@ -134,6 +135,7 @@ struct EngineImpl {
   std::vector<Val> vals;
   std::vector<Op> ops;
   int input = -1, output = -1;
+  bool stream_out = false;  // the final GEMM stores the output non-temporally
   Shape in_shape;
 
   // device state
@@ -690,6 +692,7 @@ struct EngineImpl {
         ep.ldr = o.a[1];
       }
       set_fold(o, ep);
+      ep.stream_out = o.out[0] == output && stream_out;
       hip_check(gemm_nt(dt, dptr(o.in[0]), wptr(o.w), int(o.a[0]), int(o.a[1]), int(o.a[2]), o.a[2], o.a[2], 1, 0,
                         0, 0, ep, -1, st),
                 o.name.c_str());
@@ -801,6 +804,10 @@ struct EngineImpl {
     int y = lower(cfg, input, "");
     y = to_rowmajor4(y, "output");
     output = y;
+    // a final output larger than the L2s and most of the last-level cache is
+    // written with non-temporal stores (MUNET_HIP_STREAM_OUT=0 turns it off)
+    const char *so = std::getenv("MUNET_HIP_STREAM_OUT");
+    stream_out = vals[output].bytes() >= (size_t(64) << 20) && !(so && std::string(so) == "0");
     plan();
     if (!plan_only) {
       hip_check(hipSetDevice(device), "hipSetDevice");
@@ -893,6 +900,7 @@ struct EngineImpl {
     require_device();
     if (reps < 1 || reps > 1000) throw Error("op_times: reps must be in 1..1000");
     std::ostringstream s;
+    s << std::setprecision(15);
     s << "[";
     bool first = true;
     for (size_t i = 0; i < ops.size(); ++i) {
@@ -928,6 +936,56 @@ struct EngineImpl {
     }
     s << "]";
     hip_check(hipStreamSynchronize(stream), "op_times");
+    return s.str();
+  }
+
+  // GPU time of each op inside the forward, with the caches and transitions
+  // of the graph: for every prefix ops[0..i] of the forward, a graph of that
+  // prefix is launched once to warm and then `reps` times back to back
+  // between events; op i's time is T(i) - T(i-1).  Events inside a graph or
+  // between eager launches would add their own packets (about 3 us per op);
+  // differences of whole-graph times add nothing.  Op 0's time also holds
+  // the graph launch overhead.
+  std::string forward_op_times_json(int reps) {
+    require_device();
+    if (reps < 1 || reps > 1000) throw Error("forward_op_times: reps must be in 1..1000");
+    const size_t n = ops.size();
+    std::vector<double> prefix_ms(n, 0.0);
+    for (size_t i = 0; i < n; ++i) {
+      hipGraph_t g = nullptr;
+      hipGraphExec_t x = nullptr;
+      hip_check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+      try {
+        for (size_t j = 0; j <= i; ++j) enqueue(ops[j]);
+      } catch (...) {
+        (void)hipStreamEndCapture(stream, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+      }
+      hip_check(hipStreamEndCapture(stream, &g), "hipStreamEndCapture");
+      float ms = 0.f;
+      hipError_t err = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+      if (err == hipSuccess) err = hipGraphLaunch(x, stream);
+      if (err == hipSuccess) err = hipEventRecord(ev0, stream);
+      for (int r = 0; r < reps && err == hipSuccess; ++r) err = hipGraphLaunch(x, stream);
+      if (err == hipSuccess) err = hipEventRecord(ev1, stream);
+      if (err == hipSuccess) err = hipStreamSynchronize(stream);
+      if (err == hipSuccess) err = hipEventElapsedTime(&ms, ev0, ev1);
+      if (x) (void)hipGraphExecDestroy(x);
+      (void)hipGraphDestroy(g);
+      hip_check(err, "forward_op_times");
+      prefix_ms[i] = double(ms) / reps;
+    }
+    std::ostringstream s;
+    s << std::setprecision(15) << "[";
+    for (size_t i = 0; i < n; ++i) {
+      double flops, bytes;
+      op_work(ops[i], flops, bytes);
+      const double us = (prefix_ms[i] - (i ? prefix_ms[i - 1] : 0.0)) * 1000.0;
+      s << (i ? "," : "") << "{\"name\":\"" << ops[i].name << "\",\"kind\":\"" << op_name(ops[i].kind)
+        << "\",\"us\":" << us << ",\"flops\":" << flops << ",\"bytes\":" << bytes << "}";
+    }
+    s << "]";
     return s.str();
   }
 
@@ -981,7 +1039,7 @@ struct EngineImpl {
       << ",\"last_forward_gpu_ms\":" << last_gpu_ms << ",\"compiled_input_shape\":" << shape_str(in_shape)
       << ",\"compiled_output_shape\":" << (output >= 0 ? shape_str(vals[output].shape) : "[]")
       << ",\"arena_bytes\":" << arena_bytes << ",\"weight_bytes\":" << wbytes << ",\"ops\":" << ops.size()
-      << ",\"fused_epilogues\":" << fused_epilogues << ",\"ln_folds\":" << ln_folds
+      << ",\"fused_epilogues\":" << fused_epilogues << ",\"ln_folds\":" << ln_folds << ",\"stream_out\":" << (stream_out ? "true" : "false")
       << ",\"zero_copy_concats\":" << zero_copy_concats
       << ",\"current_memory_bytes\":" << (arena_bytes + wbytes) << ",\"peak_memory_bytes\":" << (arena_bytes + wbytes)
       << "}";
@@ -1407,6 +1465,10 @@ int mh_engine_plan(mh_engine *e, char *buf, size_t len) { ENG_TRY(put_str(e->imp
 
 int mh_engine_op_times(mh_engine *e, int reps, const char *only, char *buf, size_t len) {
   ENG_TRY(put_str(e->impl.op_times_json(reps, only), buf, len))
+}
+
+int mh_engine_forward_op_times(mh_engine *e, int reps, char *buf, size_t len) {
+  ENG_TRY(put_str(e->impl.forward_op_times_json(reps), buf, len))
 }
 
 }  // extern "C"

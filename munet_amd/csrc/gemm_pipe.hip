@@ -134,11 +134,12 @@ hipError_t gemm_pipe(int dt, const void *A, const void *Bt, int M, int N, int K,
   // with 8 columns, the vocabulary head -45 us with 16; FFN down and
   // out-proj, whose A is 4-5x W, stay on row groups); MUNET_HIP_XCD_GN
   // overrides it for every GEMM
+  const int kd = kind == PK_BIAS && ep.stream_out ? PK_BIAS_NT : kind;
   EpiArgs e = ep;
   e.xcd_gn = 2L * N >= M ? (N >= 4L * M ? 16 : 8) : 0;
   if (const char *gn = std::getenv("MUNET_HIP_XCD_GN")) e.xcd_gn = std::max(0, std::atoi(gn));
-  if (dt == BF16) return launch_dt<BF16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, e, tile, kind, st);
-  return launch_dt<F16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, e, tile, kind, st);
+  if (dt == BF16) return launch_dt<BF16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, e, tile, kd, st);
+  return launch_dt<F16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, e, tile, kd, st);
 }
 
 }  // namespace mh

@@ -166,6 +166,7 @@ enum PipeKind : int {
   PK_LN_BIAS,        // folded LayerNorm consumer, + bias
   PK_LN_BIAS_GELU,   // folded LayerNorm consumer, + bias, GELU
   PK_BIAS_RESID_ST,  // + bias, + residual, writes LayerNorm partials
+  PK_BIAS_NT,        // + bias, non-temporal stores (an output no kernel reads)
   PK_COUNT
 };
 template <int EK> struct PipeKindT {
@@ -175,6 +176,7 @@ template <int EK> struct PipeKindT {
   static constexpr bool BIAS = FIXED && EK != PK_PLAIN;
   static constexpr int ACT = (EK == PK_BIAS_GELU || EK == PK_LN_BIAS_GELU) ? ACT_GELU : ACT_NONE;
   static constexpr bool RESID = EK == PK_BIAS_RESID || EK == PK_BIAS_RESID_ST;
+  static constexpr bool NT = EK == PK_BIAS_NT;
 };
 
 // The fused epilogue of a wave's accumulator tile.  bf16 fast path: lane
@@ -431,7 +433,12 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
             v[3] = rs.y * (v[3] - rs.x * lcs[j].w) + lbw[j].w;
           }
           const uint2 pk = epi_fast_bf16_fixed<KT_::BIAS, KT_::ACT, KT_::RESID>(v, bq[j], RQ(i, j), ep.gelu_c);
-          if (interior || (m < M && n < N)) *reinterpret_cast<uint2 *>(cbase[j] + roff[i]) = pk;
+          if (interior || (m < M && n < N)) {
+            if constexpr (KT_::NT)
+              __builtin_nontemporal_store((uint64_t(pk.y) << 32) | pk.x, reinterpret_cast<uint64_t *>(cbase[j] + roff[i]));
+            else
+              *reinterpret_cast<uint2 *>(cbase[j] + roff[i]) = pk;
+          }
           if constexpr (KT_::ST) stats_add(ep, sa, pk, m, j);
         }
       }

@@ -33,6 +33,7 @@ hipError_t gemm_pipe_fixed_staged(int kind, int tile, const void *A, const void 
   case PK_LN_BIAS: MH_RUN(PK_LN_BIAS);
   case PK_LN_BIAS_GELU: MH_RUN(PK_LN_BIAS_GELU);
   case PK_BIAS_RESID_ST: MH_RUN(PK_BIAS_RESID_ST);
+  case PK_BIAS_NT: MH_RUN(PK_BIAS_NT);
   default: return hipErrorInvalidValue;
   }
 #undef MH_RUN

@@ -63,6 +63,10 @@ struct EpiArgs {
   // pipelined GEMMs: tile columns per group of the per-XCD tile enumeration
   // (0: groups of 8 tile rows instead); set by the GEMM launcher
   int xcd_gn = 0;
+  // the output is read by no kernel (the engine's final output, copied out
+  // later): the bias epilogue stores it with non-temporal stores, so it does
+  // not sit in the caches for the next forward's kernels to write back
+  int stream_out = 0;
 };
 
 // Implicit-GEMM convolution geometry (NHWC activation, ldx = pixel stride).

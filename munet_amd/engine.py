@@ -206,6 +206,12 @@ class Engine:
         (mh_engine_op_times)."""
         return self._json("mh_engine_op_times", 1 << 20, reps, (only or "").encode())
 
+    def forward_op_times(self, reps: int = 20) -> list:
+        """GPU time of every op inside the forward: a list of {name, kind, us,
+        flops, bytes}, us = difference of consecutive prefix-graph times, each
+        over ``reps`` replays (mh_engine_forward_op_times)."""
+        return self._json("mh_engine_forward_op_times", 1 << 20, reps)
+
     def close(self):
         if self._h is not None:
             _lib.call("mh_engine_destroy", self._h)

@@ -90,3 +90,53 @@ def test_pinned_io():
     pin_in[...] = ids
     e.run_pinned()
     assert np.array_equal(pin_out, ref)
+
+
+def test_per_op_timings():
+    """mh_engine_op_times (each op alone, replayed) and
+    mh_engine_forward_op_times (each op inside the forward) list every op of
+    the plan with its algorithmic work, and leave the engine's results
+    unchanged; the in-forward times add up to one forward's graph time."""
+    cfg = models.decoder_config(vocab=2000, ctx=256, d_model=256, num_heads=4, num_layers=2, ffn=1024,
+                                dtype="bfloat16")
+    p = models.init_params(cfg, "gpt", scope="optimes")
+    ids = models.make_input(cfg, (4, 256), "gpt", scope="optimes_in")
+    e = Engine(0).load(cfg, p).compile((4, 256))
+    ref = e.run(ids)
+    names = [o["name"] for o in e.plan()["ops"]]
+    iso, fwd = e.op_times(3), e.forward_op_times(5)
+    assert [o["name"] for o in iso] == names and [o["name"] for o in fwd] == names
+    for o in iso + fwd:
+        # in-forward times are differences of prefix-graph times: a tiny op
+        # may come out slightly negative from timing noise
+        assert o["us"] > (0 if o in iso else -5.0)
+        if o["kind"] in ("gemm", "qkv_gemm", "attention"):
+            assert o["flops"] > 0
+    head = next(o for o in fwd if o["name"].startswith("head"))
+    assert head["flops"] == 2.0 * 4 * 256 * 256 * 2000  # exact, not rounded to 6 digits
+    assert [o["name"] for o in e.op_times(2, only=names[1])] == [names[1]]
+    graph_ms = []
+    for _ in range(5):
+        e.run_device()
+        graph_ms.append(e.stats()["last_forward_gpu_ms"])
+    total_ms = sum(o["us"] for o in fwd) / 1e3
+    assert 0.5 * min(graph_ms) < total_ms < 3.0 * min(graph_ms) + 0.05, (total_ms, graph_ms)
+    assert np.array_equal(e.run(ids), ref)
+
+
+def test_streamed_final_output_bit_identical(monkeypatch):
+    """A final output of at least 64 MiB (here 4 x 1024 x 32000 bf16 logits) is
+    written by the head's epilogue with non-temporal stores: the same bits as
+    ordinary stores (MUNET_HIP_STREAM_OUT=0)."""
+    cfg = models.decoder_config(vocab=32000, ctx=1024, d_model=64, num_heads=2, num_layers=1, ffn=128,
+                                dtype="bfloat16")
+    p = models.init_params(cfg, "gpt", scope="nt")
+    ids = models.make_input(cfg, (4, 1024), "gpt", scope="nt_in")
+    e = Engine(0).load(cfg, p).compile((4, 1024))
+    assert e.stats()["stream_out"]
+    y = e.run(ids)
+    assert np.array_equal(y, e.run(ids))
+    monkeypatch.setenv("MUNET_HIP_STREAM_OUT", "0")
+    e0 = Engine(0).load(cfg, p).compile((4, 1024))
+    assert not e0.stats()["stream_out"]
+    assert np.array_equal(y, e0.run(ids))

@@ -58,6 +58,7 @@ def test_decoder_plan_structure_and_reuse():
     st = e.stats()
     assert st["fused_epilogues"] == 3 * 3  # out_proj+resid, ffn0+gelu, ffn2+resid per layer
     assert st["ln_folds"] == 2 * 3
+    assert not st["stream_out"]  # 2 MB of logits stay cacheable
     # producers: embedding, then out_proj and ffn.2 of every layer; consumers:
     # qkv, ffn.0 of every layer and the head; each stats value links one pair
     producers = [i for i, o in enumerate(ops) if o["stats_out"] >= 0]
@@ -143,6 +144,7 @@ def test_full_gpt_plan_fits_and_reuses():
     st = e.stats()
     assert st["ops"] == 1 + 12 * 5 + 2  # embedding, 5 per layer (both LayerNorms folded), ln_f, head
     assert st["ln_folds"] == 24
+    assert st["stream_out"]  # 262 MB of logits: the head stores them non-temporally
     assert e.out_shape == (4, 1024, 32000)
     _check_arena(p)
     # logits (262 MB) + a few activations; far below one buffer per op
