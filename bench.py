@@ -15,7 +15,9 @@ of the op captured in one graph and replayed between events, so host launch
 cost is excluded; the rocprofv3 kernel trace of the same command shows the
 same per-dispatch durations); the kernel with the largest time per forward
 is reported against the bf16 MFMA peak (GEMM / attention: algorithmic
-2*M*N*K FLOPs) or the HBM peak (LayerNorm: unique bytes).  Inside the
+2*M*N*K FLOPs) or the HBM peak (LayerNorm: unique bytes), and against the measured peaks (the
+register-only MFMA loop of mh_measure_mfma_peak; a 1 GiB device copy).
+Inside the
 forward the kernels run with colder caches: "kernels_in_forward_avg_us"
 (mh_engine_forward_op_times: differences of prefix-graph times, each over 20
 replays; an op's figure also carries what it costs the ops after it, such as
@@ -198,17 +200,39 @@ def main():
     if not np.array_equal(again.view(np.uint16), logits.view(np.uint16)):
         raise SystemExit("bench: repeated forwards changed the logits")
 
+    # measured peaks beside the datasheet ones: the MFMA loop of peak.hip,
+    # and a 1 GiB device-to-device copy (reads and writes 2 GiB)
+    from munet_amd.backend import HipBackend
+    peak_mfma = HipBackend(0).measure_mfma_peak(2, 16000)
+    src = torch.empty(1 << 29, device="cuda", dtype=torch.float16)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    peak_hbm = 5 * 2.0 * src.numel() * 2 / (e0.elapsed_time(e1) * 1e-3)
+    del src, dst
+
     rows = kernel_table(eng, in_forward=False)
-    fwd = {r["name"]: round(r["t"] * 1e6, 2) for r in kernel_table(eng, in_forward=True)}
+    # in-forward times are differences of prefix-graph times: a few us of
+    # replay-to-replay noise each, so only the per-layer categories (means over
+    # 12 ops) and the LM head (hundreds of us) are reported
+    fwd = {r["name"]: round(r["t"] * 1e6, 2) for r in kernel_table(eng, in_forward=True)
+           if r["count"] >= 12 or r["name"] == "lm_head"}
     for r in rows:
         r["per_fwd"] = r["t"] * r["count"]
     dom = max(rows, key=lambda r: r["per_fwd"])
     if dom["flops"]:
         ach = dom["flops"] / dom["t"]
-        roof = dict(bound="mfma", achieved=ach / 1e12, peak=PEAK_BF16 / 1e12, unit="TFLOP/s", frac=ach / PEAK_BF16)
+        roof = dict(bound="mfma", achieved=ach / 1e12, peak=PEAK_BF16 / 1e12, unit="TFLOP/s", frac=ach / PEAK_BF16,
+                    peak_measured=peak_mfma / 1e12, frac_of_measured=ach / peak_mfma)
     else:
         ach = dom["bytes"] / dom["t"]
-        roof = dict(bound="hbm", achieved=ach / 1e9, peak=PEAK_HBM / 1e9, unit="GB/s", frac=ach / PEAK_HBM)
+        roof = dict(bound="hbm", achieved=ach / 1e9, peak=PEAK_HBM / 1e9, unit="GB/s", frac=ach / PEAK_HBM,
+                    peak_measured=peak_hbm / 1e9, frac_of_measured=ach / peak_hbm)
     roof.update(kernel=dom["name"], avg_us=dom["t"] * 1e6, traffic=measured_traffic(dom["name"]))
     gemm = [r for r in rows if r["flops"] and r["name"] != "attention_causal"]
     gemm_frac = sum(r["flops"] * r["count"] for r in gemm) / sum(r["per_fwd"] for r in gemm) / PEAK_BF16
@@ -240,6 +264,7 @@ def main():
         "roofline": roof,
         "gemm_mfma_frac": gemm_frac,
         "layernorm_hbm_frac": (ln["bytes"] / ln["t"]) / PEAK_HBM,
+        "measured_peaks": {"mfma_bf16_tflops": peak_mfma / 1e12, "hbm_copy_gbs": peak_hbm / 1e9},
         "kernels": kernels,
         "kernels_in_forward_avg_us": fwd,
         "cpu_baseline": cpu,

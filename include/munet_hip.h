@@ -106,6 +106,12 @@ int mh_embedding_pos(int dt, const int32_t *ids, const void *tok_w, const void *
 int mh_convert(int src_dt, const void *in, int dst_dt, void *out, size_t n, void *stream);
 /* Row argmax, first index of the maximum (the demos' np.argmax). */
 int mh_argmax(int dt, const void *x, int32_t *out, int rows, int cols, void *stream);
+/* Measured matrix-core peak of this GPU in FLOP/s: a full grid of waves
+ * issuing independent 16x16x32 bf16 (dt MH_BF16) or fp16 MFMAs on registers,
+ * `iters` loop trips of 8 per wave, timed with HIP events on `stream` (the
+ * call synchronises it).  No counterpart in the reference: the measured peak
+ * that the roofline reports beside the datasheet one. */
+int mh_measure_mfma_peak(int dt, int iters, double *flops_per_s, void *stream);
 
 /* ---- BackendBlasCapability (src/core/backend.hpp:250-260) ---------------- */
 /* :253-254 matmul(a, b, out, M, K, N, transA, transB) on raw row-major storage.

@@ -231,6 +231,13 @@ class HipBackend:
     def argmax(self, x, out, rows, cols):
         call("mh_argmax", _dt(x), _p(x), _p(out), rows, cols, _stream())
 
+    def measure_mfma_peak(self, dt=2, iters=16000) -> float:
+        """Measured matrix-core peak in FLOP/s (mh_measure_mfma_peak; dt 2 =
+        bf16, 1 = fp16) on the current torch stream."""
+        v = ctypes.c_double(0.0)
+        call("mh_measure_mfma_peak", dt, iters, ctypes.byref(v), _stream())
+        return v.value
+
     # ---- blas (backend.hpp:250-260) ----------------------------------------
     def matmul(self, a, b, out, M, K, N, transA=False, transB=False):
         call("mh_matmul", _dt(a), _p(a), _p(b), _p(out), M, K, N, int(transA), int(transB), _stream())

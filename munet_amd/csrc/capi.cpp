@@ -335,6 +335,13 @@ int mh_argmax(int dt, const void *x, int32_t *out, int rows, int cols, void *str
     hip_check(argmax_rows(dt, x, out, rows, cols, S_(stream)), "argmax");
   })
 }
+int mh_measure_mfma_peak(int dt, int iters, double *flops_per_s, void *stream) {
+  MH_TRY({
+    if (dt != MH_BF16 && dt != MH_F16) throw Error("measure_mfma_peak: dtype must be bfloat16 or float16");
+    if (iters <= 0 || !flops_per_s) throw Error("measure_mfma_peak: iters must be positive and flops_per_s set");
+    hip_check(mfma_peak(dt, iters, flops_per_s, S_(stream)), "measure_mfma_peak");
+  })
+}
 
 // ---- blas ------------------------------------------------------------------
 int mh_matmul(int dt, const void *a, const void *b, void *out, int M, int K, int N, int transA, int transB,

@@ -133,6 +133,9 @@ hipError_t convert(int sdt, const void *in, int ddt, void *out, size_t n, hipStr
 hipError_t embedding(int dt, const int32_t *ids, const void *w, const void *pos, void *out, int n, int V, int D,
                      int T, int *err, hipStream_t st, float *stats = nullptr);
 hipError_t argmax_rows(int dt, const void *x, int32_t *out, int rows, int cols, hipStream_t st);
+// Measured matrix-core peak (peak.hip): FLOP/s of a full grid of independent
+// 16x16x32 MFMAs (bf16 or fp16), `iters` loop trips per wave.
+hipError_t mfma_peak(int dt, int iters, double *flops_per_s, hipStream_t st);
 
 hipError_t layernorm(int dt, const void *x, const void *w, const void *b, void *y, int rows, int cols, float eps,
                      hipStream_t st);

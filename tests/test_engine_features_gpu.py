@@ -140,3 +140,17 @@ def test_streamed_final_output_bit_identical(monkeypatch):
     e0 = Engine(0).load(cfg, p).compile((4, 1024))
     assert not e0.stats()["stream_out"]
     assert np.array_equal(y, e0.run(ids))
+
+
+def test_measured_mfma_peak():
+    """mh_measure_mfma_peak: a register-only loop of 16x16x32 MFMAs over the
+    whole GPU lands between half and 1.2x the datasheet dense peak (2.5
+    PFLOP/s bf16 and fp16) and rejects other dtypes."""
+    from munet_amd import _lib
+    from munet_amd.backend import HipBackend
+    hip = HipBackend(0)
+    for dt in (2, 1):
+        f = hip.measure_mfma_peak(dt, 4000)
+        assert 1.25e15 < f < 3.0e15, f
+    with pytest.raises(_lib.HipError, match="dtype"):
+        hip.measure_mfma_peak(0, 10)
