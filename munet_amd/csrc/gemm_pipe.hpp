@@ -789,6 +789,9 @@ void launch_dma(const void *A, const void *Bt, int M, int N, int K, long lda, lo
 // hipErrorNotSupported for any other tile.
 hipError_t gemm_pipe_fixed_staged(int kind, int tile, const void *A, const void *Bt, int M, int N, int K, long lda,
                                   long ldb, int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st);
+// Tile 16: direct-to-LDS 256x192, eight waves, every program (gemm_pipe_wide.hip).
+hipError_t gemm_pipe_wide(int dt, int kind, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb,
+                          int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st);
 hipError_t gemm_pipe_fixed_dma(int kind, int tile, const void *A, const void *Bt, int M, int N, int K, long lda,
                                long ldb, int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st);
 

@@ -1,0 +1,44 @@
+// Direct-to-LDS pipelined kernel on a 256x192 block tile with eight waves in
+// a 4x2 grid (64x96 wave tiles, two waves per SIMD), two stages: tile 16.
+// Eight waves per CU keep the matrix cores fed where the four-wave 128-row
+// tiles leave them idle, and 256x192 covers a 4096x3072 product in exactly
+// 256 tiles, one per CU.  Every epilogue program (fixed bf16 ones and the
+// general one); accumulators in VGPRs (see build.py).
+#include "gemm_pipe.hpp"
+
+namespace mh {
+
+namespace {
+
+template <int DT, int EK>
+hipError_t run(const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch, long sa, long sb,
+               long sc, const EpiArgs &ep, hipStream_t st) {
+  launch_dma<DT, 256, 192, 4, 2, 2, EK>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t gemm_pipe_wide(int dt, int kind, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb,
+                          int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st) {
+#define MH_RUN(EK) return run<BF16, EK>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st)
+  if (dt == F16) {
+    if (kind != PK_GENERAL) return hipErrorInvalidValue;
+    return run<F16, PK_GENERAL>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
+  }
+  switch (kind) {
+  case PK_GENERAL: MH_RUN(PK_GENERAL);
+  case PK_PLAIN: MH_RUN(PK_PLAIN);
+  case PK_BIAS: MH_RUN(PK_BIAS);
+  case PK_BIAS_GELU: MH_RUN(PK_BIAS_GELU);
+  case PK_BIAS_RESID: MH_RUN(PK_BIAS_RESID);
+  case PK_LN_BIAS: MH_RUN(PK_LN_BIAS);
+  case PK_LN_BIAS_GELU: MH_RUN(PK_LN_BIAS_GELU);
+  case PK_BIAS_RESID_ST: MH_RUN(PK_BIAS_RESID_ST);
+  case PK_BIAS_NT: MH_RUN(PK_BIAS_NT);
+  default: return hipErrorInvalidValue;
+  }
+#undef MH_RUN
+}
+
+}  // namespace mh

@@ -84,3 +84,19 @@ def test_encoder_block_folded_layer_norm_vs_oracle(orc):
     y = eng.run(x)
     ref = omodels.forward(orc, cfg, params, x)
     assert_close(y, ref, synth.BF16, what="encoder block (ln2 folded)")
+
+
+@pytest.mark.parametrize("tile", ["216", "208", "200"])
+def test_folded_decoder_bit_identical_across_tiles(monkeypatch, tile):
+    """Every pipelined tile accumulates in the same K order, so the folded
+    decoder (LayerNorm-consumer, statistics-producer and head-split programs)
+    gives the same bits on any forced tile as on the automatic choice; 216
+    (256x192, eight waves) is the tile the full-size FFN up and QKV take."""
+    cfg = models.decoder_config(vocab=1000, ctx=128, d_model=384, num_heads=6, num_layers=2, ffn=1536)
+    params = _perturbed(cfg, "lnfold_tiles")
+    ids = models.make_input(cfg, (2, 128), "gpt", scope="lnfold_tiles_in")
+    y = Engine(0).load(cfg, params).compile((2, 128)).run(ids)
+    monkeypatch.setenv("MUNET_HIP_GEMM_TILE", tile)
+    e = Engine(0).load(cfg, params).compile((2, 128))
+    assert e.stats()["ln_folds"] == 2 * 2 + 1
+    assert np.array_equal(e.run(ids), y)
