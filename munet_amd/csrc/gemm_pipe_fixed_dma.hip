@@ -32,6 +32,7 @@ hipError_t gemm_pipe_fixed_dma(int kind, int tile, const void *A, const void *Bt
   case PK_LN_BIAS: MH_RUN(PK_LN_BIAS);
   case PK_LN_BIAS_GELU: MH_RUN(PK_LN_BIAS_GELU);
   case PK_BIAS_RESID_ST: MH_RUN(PK_BIAS_RESID_ST);
+  case PK_BIAS_NT: MH_RUN(PK_BIAS_NT);
   default: return hipErrorInvalidValue;
   }
 #undef MH_RUN

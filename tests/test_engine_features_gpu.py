@@ -124,10 +124,14 @@ def test_per_op_timings():
     assert np.array_equal(e.run(ids), ref)
 
 
-def test_streamed_final_output_bit_identical(monkeypatch):
+@pytest.mark.parametrize("tile", [None, "209", "216"])
+def test_streamed_final_output_bit_identical(monkeypatch, tile):
     """A final output of at least 64 MiB (here 4 x 1024 x 32000 bf16 logits) is
     written by the head's epilogue with non-temporal stores: the same bits as
-    ordinary stores (MUNET_HIP_STREAM_OUT=0)."""
+    ordinary stores (MUNET_HIP_STREAM_OUT=0), on the automatic tile and forced
+    direct-to-LDS tiles (every fixed tile has the streamed program)."""
+    if tile is not None:
+        monkeypatch.setenv("MUNET_HIP_GEMM_TILE", tile)
     cfg = models.decoder_config(vocab=32000, ctx=1024, d_model=64, num_heads=2, num_layers=1, ffn=128,
                                 dtype="bfloat16")
     p = models.init_params(cfg, "gpt", scope="nt")
