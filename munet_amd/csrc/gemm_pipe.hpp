@@ -243,31 +243,59 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
   // the shares with Chan's parallel-variance formula, then across adjacent
   // lanes, and writes (mean, rstd) per row and the column terms to LDS; the
   // K loop's barriers make them visible to the epilogue.
-  static constexpr int TPR = G::NT / BM, LNCH = 32;
+  static constexpr int TPR = G::NT / BM, LNCH = 32, CH = 4 / TPR;
   static_assert(TPR == 1 || TPR == 2 || TPR == 4, "threads per row");
+  // A row's partials are split into 4 chunks of `chunk` (even) partials; each
+  // chunk is combined in order, then the chunks pairwise, (0 1) (2 3) and
+  // then the two pairs, the lower one first.  A thread owns CH consecutive
+  // chunks, so every tile combines in the same order whatever its threads
+  // per row, and gives the same bits.
+  static __device__ __forceinline__ int ln_chunk(int P) { return ((P + 3) / 4 + 1) & ~1; }
+  // (explicit fma / mul / add: HIP contracts a * b + c into an fma where the
+  // optimiser chooses, which differs between kernel instantiations; these
+  // statistics must round the same in every tile)
+  static __device__ __forceinline__ void chan_pair(float &n, float &mean, float &m2, float on, float om, float o2) {
+    const float nn = __fadd_rn(n, on), d = __fsub_rn(om, mean);
+    if (nn > 0.f) {
+      const float f = __fdiv_rn(on, nn);
+      mean = __fmaf_rn(d, f, mean);
+      m2 = __fadd_rn(m2, __fadd_rn(o2, __fmul_rn(__fmul_rn(d, d), __fmul_rn(n, f))));
+    }
+    n = nn;
+  }
   struct LnIn {
     float4 part[LNCH / 2];  // (mean, M2) pairs
     float cs, bw;
   };
   // (loads are unconditional, at indices clamped into the row; ln_finish
   // counts only the share's own partials)
+  // chunk c of this thread lands at in.part[c * LPC / 2 ..] (LPC partials
+  // per chunk slot), so every index below is a compile-time constant
+  static constexpr int LPC = LNCH / CH;
   __device__ __forceinline__ void ln_issue(const EpiArgs &ep, LnIn &in, int tid) const {
-    const int r = tid / TPR, q = tid % TPR, P = ep.ln_parts;
-    const int share = ((P + TPR - 1) / TPR + 1) & ~1, k0 = q * share, k1 = min(k0 + share, P);
+    const int r = tid / TPR, q = tid % TPR, P = ep.ln_parts, chunk = ln_chunk(P);
     const long row = min(m0 + r, M - 1);
-    if ((P & 1) == 0) {  // rows and shares start on 16-byte boundaries: two partials per load
+    if ((P & 1) == 0) {  // rows and chunks start on 16-byte boundaries: two partials per load
       const float4 *p4 = reinterpret_cast<const float4 *>(ep.ln_stats) + row * (P / 2);
       const int last = P / 2 - 1;
 #pragma unroll
-      for (int i = 0; i < LNCH / 2; ++i)
-        if (2 * i < share) in.part[i] = p4[min(k0 / 2 + i, last)];
+      for (int c = 0; c < CH; ++c) {
+        const int k0 = (q * CH + c) * chunk;
+#pragma unroll
+        for (int i = 0; i < LPC / 2; ++i)
+          if (2 * i < chunk) in.part[c * LPC / 2 + i] = p4[min(k0 / 2 + i, last)];
+      }
     } else {
       const float2 *p = reinterpret_cast<const float2 *>(ep.ln_stats) + row * P;
 #pragma unroll
-      for (int i = 0; i < LNCH / 2; ++i) {
-        if (2 * i < share) {
-          const float2 a = p[min(k0 + 2 * i, P - 1)], b = p[min(k0 + 2 * i + 1, P - 1)];
-          in.part[i] = make_float4(a.x, a.y, b.x, b.y);
+      for (int c = 0; c < CH; ++c) {
+        const int k0 = (q * CH + c) * chunk;
+#pragma unroll
+        for (int i = 0; i < LPC / 2; ++i) {
+          if (2 * i < chunk) {
+            const float2 a = p[min(k0 + 2 * i, P - 1)], b = p[min(k0 + 2 * i + 1, P - 1)];
+            in.part[c * LPC / 2 + i] = make_float4(a.x, a.y, b.x, b.y);
+          }
         }
       }
     }
@@ -277,36 +305,50 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
   }
   __device__ __forceinline__ void ln_finish(const EpiArgs &ep, const LnIn &in, float2 *lnrow, float *lncs,
                                             float *lnbw, int tid) const {
-    const int r = tid / TPR, q = tid % TPR, P = ep.ln_parts;
-    const int share = ((P + TPR - 1) / TPR + 1) & ~1, k0 = q * share, k1 = min(k0 + share, P);
-    // every partial covers w columns, so after i partials n = i w and Chan's
-    // update weights are the constants 1 / (i + 1) and i / (i + 1)
+    const int r = tid / TPR, q = tid % TPR, P = ep.ln_parts, chunk = ln_chunk(P);
+    // every partial covers w columns, so after i partials of a chunk n = i w
+    // and Chan's update weights are the constants 1 / (i + 1) and i / (i + 1)
     const float w = float(ep.ln_cols);
-    float mean = 0.f, m2 = 0.f, m2x = 0.f;  // m2x: the between-partial term / w
+    float cn[CH], cm[CH], c2[CH];
 #pragma unroll
-    for (int i = 0; i < LNCH; ++i) {
-      if (k0 + i < k1) {
-        const float pm = i & 1 ? in.part[i / 2].z : in.part[i / 2].x;
-        const float p2 = i & 1 ? in.part[i / 2].w : in.part[i / 2].y;
-        const float d = pm - mean;
-        mean += d * (1.0f / float(i + 1));
-        m2 += p2;
-        m2x += d * d * (float(i) / float(i + 1));
+    for (int c = 0; c < CH; ++c) {
+      const int k0 = (q * CH + c) * chunk, k1 = min(k0 + chunk, P);
+      float mean = 0.f, m2 = 0.f, m2x = 0.f;  // m2x: the between-partial term / w
+#pragma unroll
+      for (int i = 0; i < LPC; ++i) {
+        const int j = c * LPC + i;  // index into this thread's loaded partials
+        if (i < chunk && k0 + i < k1) {
+          const float pm = j & 1 ? in.part[j / 2].z : in.part[j / 2].x;
+          const float p2 = j & 1 ? in.part[j / 2].w : in.part[j / 2].y;
+          const float d = __fsub_rn(pm, mean);
+          mean = __fmaf_rn(d, 1.0f / float(i + 1), mean);
+          m2 = __fadd_rn(m2, p2);
+          m2x = __fmaf_rn(__fmul_rn(d, d), float(i) / float(i + 1), m2x);
+        }
       }
+      cm[c] = mean;
+      c2[c] = __fmaf_rn(m2x, w, m2);
+      cn[c] = float(max(k1 - k0, 0)) * w;
     }
-    m2 += m2x * w;
-    float n = float(max(min(k1 - k0, LNCH), 0)) * w;
+    // chunks of this thread: (0 1), (2 3), then the pairs
+#pragma unroll
+    for (int o = 1; o < CH; o <<= 1)
+#pragma unroll
+      for (int c = 0; c < CH; c += 2 * o) chan_pair(cn[c], cm[c], c2[c], cn[c + o], cm[c + o], c2[c + o]);
+    float n = cn[0], mean = cm[0], m2 = c2[0];
+    // then across the row's threads (the lower lane's values first)
 #pragma unroll
     for (int o = 1; o < TPR; o <<= 1) {
       const float on = __shfl_xor(n, o), om = __shfl_xor(mean, o), o2 = __shfl_xor(m2, o);
-      const float nn = n + on, d = om - mean;
-      if (nn > 0.f) {
-        mean += d * (on / nn);
-        m2 += o2 + d * d * (n * (on / nn));
+      if (q & o) {
+        float tn = on, tm = om, t2 = o2;
+        chan_pair(tn, tm, t2, n, mean, m2);
+        n = tn, mean = tm, m2 = t2;
+      } else {
+        chan_pair(n, mean, m2, on, om, o2);
       }
-      n = nn;
     }
-    if (q == 0) lnrow[r] = make_float2(mean, 1.0f / sqrtf(m2 / n + ep.ln_eps));
+    if (q == 0) lnrow[r] = make_float2(mean, __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(m2, n), ep.ln_eps))));
     if (tid < BN) {
       lncs[tid] = in.cs;
       lnbw[tid] = in.bw;
@@ -341,7 +383,10 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
       for (int t = 0; t < FN; ++t)
         if (t <= j && t > j - G16)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) q += (a.y[t][e] - mu) * (a.y[t][e] - mu);
+          for (int e = 0; e < 4; ++e) {
+            const float dv = __fsub_rn(a.y[t][e], mu);
+            q = __fmaf_rn(dv, dv, q);  // explicit: the same rounding in every tile
+          }
       q += __shfl_xor(q, 16);
       q += __shfl_xor(q, 32);
       const int g0 = n0 + g.wn * WTN + (j + 1) * 16 - ep.stats_cols;  // first column of the group
@@ -426,11 +471,11 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
         for (int j = 0; j < FN; ++j) {
           const int n = n0 + wn * WTN + j * 16 + lg * 4;
           float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-          if constexpr (KT_::LN) {
-            v[0] = rs.y * (v[0] - rs.x * lcs[j].x) + lbw[j].x;
-            v[1] = rs.y * (v[1] - rs.x * lcs[j].y) + lbw[j].y;
-            v[2] = rs.y * (v[2] - rs.x * lcs[j].z) + lbw[j].z;
-            v[3] = rs.y * (v[3] - rs.x * lcs[j].w) + lbw[j].w;
+          if constexpr (KT_::LN) {  // explicit fmas: the same rounding in every tile
+            v[0] = __fmaf_rn(rs.y, __fmaf_rn(-rs.x, lcs[j].x, v[0]), lbw[j].x);
+            v[1] = __fmaf_rn(rs.y, __fmaf_rn(-rs.x, lcs[j].y, v[1]), lbw[j].y);
+            v[2] = __fmaf_rn(rs.y, __fmaf_rn(-rs.x, lcs[j].z, v[2]), lbw[j].z);
+            v[3] = __fmaf_rn(rs.y, __fmaf_rn(-rs.x, lcs[j].w, v[3]), lbw[j].w);
           }
           const uint2 pk = epi_fast_bf16_fixed<KT_::BIAS, KT_::ACT, KT_::RESID>(v, bq[j], RQ(i, j), ep.gelu_c);
           if (interior || (m < M && n < N)) {
@@ -639,9 +684,17 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
                 long ldb, long sa, long sb, long sc, EpiArgs ep) {
   typedef PipeGeom<BM, BN, WGM, WGN> G;
   constexpr int NW = G::NW, FM = G::FM, FN = G::FN, BK = 64;
-  // 8-row DMA blocks per wave per slab (A, then Bt)
-  constexpr int ABLK = BM / 8 / NW, BBLK = BN / 8 / NW, NDMA = ABLK + BBLK;
-  static_assert(ABLK * NW * 8 == BM && BBLK * NW * 8 == BN, "DMA split");
+  // 8-row DMA blocks per wave per slab.  EVEN: every wave takes the same
+  // number of A blocks and of Bt blocks.  Otherwise block b of the NB blocks
+  // (A rows, then Bt rows) goes to wave b % NW, and a wave with one block
+  // fewer repeats the slab's last block (the same bytes to the same LDS
+  // address), so every wave issues NDMA instructions and waits for the same
+  // counts.
+  constexpr bool EVEN = BM % (8 * NW) == 0 && BN % (8 * NW) == 0;
+  constexpr int NB = (BM + BN) / 8, NBA = BM / 8;
+  constexpr int ABLK = EVEN ? BM / 8 / NW : 1, BBLK = EVEN ? BN / 8 / NW : 1;
+  constexpr int NDMA = EVEN ? ABLK + BBLK : (NB + NW - 1) / NW;
+  static_assert(BM % 8 == 0 && BN % 8 == 0, "DMA blocks");
   static_assert(S >= 2 && NDMA * (S - 1) < 64, "stages");
   constexpr uint32_t STAGE = (BM + BN) * 128;  // bytes per stage
   __shared__ u32x4 lds[S][(BM + BN) * 8];
@@ -662,19 +715,33 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
   // Byte offsets from the slab base (rows past M / N read the last valid row).
   const int lr = lane >> 3, lc = (lane & 7) ^ lr;
   uint32_t aoff[ABLK], boff[BBLK];
-#pragma unroll
-  for (int i = 0; i < ABLK; ++i)
-    aoff[i] = (uint32_t(min(m0 + (wave * ABLK + i) * 8 + lr, M - 1)) * uint32_t(lda) + lc * 8) * 2;
-#pragma unroll
-  for (int i = 0; i < BBLK; ++i)
-    boff[i] = (uint32_t(min(n0 + (wave * BBLK + i) * 8 + lr, N - 1)) * uint32_t(ldb) + lc * 8) * 2;
+  uint32_t uoff[EVEN ? 1 : NDMA];
   const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>((lds_void_t *)&lds[0][0]));
+  if constexpr (EVEN) {
+#pragma unroll
+    for (int i = 0; i < ABLK; ++i)
+      aoff[i] = (uint32_t(min(m0 + (wave * ABLK + i) * 8 + lr, M - 1)) * uint32_t(lda) + lc * 8) * 2;
+#pragma unroll
+    for (int i = 0; i < BBLK; ++i)
+      boff[i] = (uint32_t(min(n0 + (wave * BBLK + i) * 8 + lr, N - 1)) * uint32_t(ldb) + lc * 8) * 2;
+  } else {
+#pragma unroll
+    for (int t = 0; t < NDMA; ++t) {
+      const int b = min(wave + t * NW, NB - 1);
+      uoff[t] = b < NBA ? (uint32_t(min(m0 + b * 8 + lr, M - 1)) * uint32_t(lda) + lc * 8) * 2
+                        : (uint32_t(min(n0 + (b - NBA) * 8 + lr, N - 1)) * uint32_t(ldb) + lc * 8) * 2;
+    }
+  }
   const uint32_t wa = lds0 + wave * ABLK * 1024, wb = lds0 + BM * 128 + wave * BBLK * 1024;
   const int KT = K / BK;
-  // DMA instruction t (A blocks first) of slab kt into stage st
+  // DMA instruction t of slab kt into stage st (EVEN: A blocks first; else
+  // block min(wave + t NW, NB - 1), whose LDS rows start at 1024 b bytes)
 #define MH_DMA(T, KT_, ST)                                                                         \
   {                                                                                                \
-    if ((T) < ABLK)                                                                                \
+    if constexpr (!EVEN) {                                                                         \
+      const int b_ = min(wave + (T) * NW, NB - 1);                                                 \
+      dma16((b_ < NBA ? A : Bt) + (KT_) * BK, uoff[(T) % NDMA], lds0 + (ST) * STAGE + b_ * 1024);  \
+    } else if ((T) < ABLK)                                                                         \
       dma16(A + (KT_) * BK, aoff[(T) % ABLK], wa + (ST) * STAGE + ((T) % ABLK) * 1024);            \
     else                                                                                           \
       dma16(Bt + (KT_) * BK, boff[((T) - ABLK) % BBLK], wb + (ST) * STAGE + (((T) - ABLK) % BBLK) * 1024); \
@@ -789,8 +856,9 @@ void launch_dma(const void *A, const void *Bt, int M, int N, int K, long lda, lo
 // hipErrorNotSupported for any other tile.
 hipError_t gemm_pipe_fixed_staged(int kind, int tile, const void *A, const void *Bt, int M, int N, int K, long lda,
                                   long ldb, int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st);
-// Tile 16: direct-to-LDS 256x192, eight waves, every program (gemm_pipe_wide.hip).
-hipError_t gemm_pipe_wide(int dt, int kind, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb,
+// Eight-wave direct-to-LDS tiles, every program (gemm_pipe_wide.hip): 16
+// 256x192 two stages, 17 128x96 four stages.
+hipError_t gemm_pipe_wide(int dt, int kind, int tile, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb,
                           int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st);
 hipError_t gemm_pipe_fixed_dma(int kind, int tile, const void *A, const void *Bt, int M, int N, int K, long lda,
                                long ldb, int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st);

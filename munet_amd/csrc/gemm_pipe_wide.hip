@@ -11,20 +11,24 @@ namespace mh {
 namespace {
 
 template <int DT, int EK>
-hipError_t run(const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch, long sa, long sb,
-               long sc, const EpiArgs &ep, hipStream_t st) {
-  launch_dma<DT, 256, 192, 4, 2, 2, EK>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
+hipError_t run(int tile, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch, long sa,
+               long sb, long sc, const EpiArgs &ep, hipStream_t st) {
+  switch (tile) {
+  case 16: launch_dma<DT, 256, 192, 4, 2, 2, EK>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;
+  case 17: launch_dma<DT, 128, 96, 4, 2, 4, EK>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;
+  default: return hipErrorNotSupported;
+  }
   return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t gemm_pipe_wide(int dt, int kind, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb,
+hipError_t gemm_pipe_wide(int dt, int kind, int tile, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb,
                           int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st) {
-#define MH_RUN(EK) return run<BF16, EK>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st)
+#define MH_RUN(EK) return run<BF16, EK>(tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st)
   if (dt == F16) {
     if (kind != PK_GENERAL) return hipErrorInvalidValue;
-    return run<F16, PK_GENERAL>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
+    return run<F16, PK_GENERAL>(tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
   }
   switch (kind) {
   case PK_GENERAL: MH_RUN(PK_GENERAL);

@@ -86,12 +86,15 @@ def test_encoder_block_folded_layer_norm_vs_oracle(orc):
     assert_close(y, ref, synth.BF16, what="encoder block (ln2 folded)")
 
 
-@pytest.mark.parametrize("tile", ["216", "208", "200"])
+@pytest.mark.parametrize("tile", ["216", "217", "208", "200", "202"])
 def test_folded_decoder_bit_identical_across_tiles(monkeypatch, tile):
-    """Every pipelined tile accumulates in the same K order, so the folded
-    decoder (LayerNorm-consumer, statistics-producer and head-split programs)
-    gives the same bits on any forced tile as on the automatic choice; 216
-    (256x192, eight waves) is the tile the full-size FFN up and QKV take."""
+    """Every pipelined tile accumulates in the same K order and combines a
+    row's LayerNorm partials in the same order (four chunks, then pairwise,
+    whether a row has 2 or 4 threads), so the folded decoder
+    (LayerNorm-consumer, statistics-producer and head-split programs) gives
+    the same bits on any forced tile as on the automatic choice: 216
+    (256x192) and 217 (128x96, blocks split unevenly over eight waves) are
+    the eight-wave tiles, 202 (64x64) and 217 have 4 threads per row."""
     cfg = models.decoder_config(vocab=1000, ctx=128, d_model=384, num_heads=6, num_layers=2, ffn=1536)
     params = _perturbed(cfg, "lnfold_tiles")
     ids = models.make_input(cfg, (2, 128), "gpt", scope="lnfold_tiles_in")
