@@ -106,10 +106,12 @@ def test_per_op_timings():
     names = [o["name"] for o in e.plan()["ops"]]
     iso, fwd = e.op_times(3), e.forward_op_times(5)
     assert [o["name"] for o in iso] == names and [o["name"] for o in fwd] == names
+    # in-forward times are differences of prefix-graph times: on this small
+    # model an op's figure (a few us) is within the replay-to-replay noise, so
+    # only their sum is checked against the graph time below
+    for o in iso:
+        assert o["us"] > 0
     for o in iso + fwd:
-        # in-forward times are differences of prefix-graph times: a tiny op
-        # may come out slightly negative from timing noise
-        assert o["us"] > (0 if o in iso else -5.0)
         if o["kind"] in ("gemm", "qkv_gemm", "attention"):
             assert o["flops"] > 0
     head = next(o for o in fwd if o["name"].startswith("head"))
