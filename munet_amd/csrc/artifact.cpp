@@ -213,9 +213,14 @@ Npy parse_npy(const Member &m) {
   return a;
 }
 
+// Element count, or an error when the product of the header's dimensions
+// does not fit 64 bits (so it cannot wrap round to match a byte size).
 uint64_t elements(const Npy &a) {
   uint64_t n = 1;
-  for (uint64_t d : a.shape) n *= d;
+  for (uint64_t d : a.shape) {
+    if (d != 0 && n > UINT64_MAX / d) throw Error("member shape overflows");
+    n *= d;
+  }
   return n;
 }
 
@@ -226,7 +231,7 @@ std::string npy_string(const Npy &a, const std::string &what) {
   if (!is_scalar(a)) throw Error(what + " is not a scalar");
   if (a.descr.size() > 2 && a.descr[1] == 'U') {
     const uint64_t chars = std::stoull(a.descr.substr(2));
-    if (a.bytes < chars * 4) throw Error(what + " is truncated");
+    if (chars > a.bytes / 4) throw Error(what + " is truncated");
     std::string out;
     for (uint64_t c = 0; c < chars; ++c) {
       const uint32_t cp = uint32_t(a.data[4 * c]) | (uint32_t(a.data[4 * c + 1]) << 8) |
@@ -239,7 +244,7 @@ std::string npy_string(const Npy &a, const std::string &what) {
   }
   if (a.descr.size() > 2 && a.descr[1] == 'S') {
     const uint64_t len = std::stoull(a.descr.substr(2));
-    if (a.bytes < len) throw Error(what + " is truncated");
+    if (len > a.bytes) throw Error(what + " is truncated");
     std::string out(reinterpret_cast<const char *>(a.data), len);
     return out.substr(0, out.find('\0'));
   }
@@ -328,7 +333,8 @@ extern "C" int mh_engine_create_from_artifact(mh_engine **engine, const char *pa
     mh::expect_eq(format, "munet_model", "format name");
     if (revision != 1) throw mh::Error("unsupported format revision " + std::to_string(revision));
     if (!legacy.empty()) mh::expect_eq(legacy, "munet_model_v1", "legacy format tag");
-    if (!producer.empty() && producer.rfind("munet", 0) != 0) throw mh::Error("unsupported producer '" + producer + "'");
+    // exactly the reference's producer tag (src/inference_serialization.cpp:35, :997-1000)
+    if (!producer.empty() && producer != "munet") throw mh::Error("unsupported producer '" + producer + "'");
     mh::expect_eq(kind, "deploy_model", "artifact kind");
     mh::expect_eq(scope, "runtime_only", "artifact scope");
     mh::expect_eq(mode, "eval", "default load mode");
@@ -359,7 +365,13 @@ extern "C" int mh_engine_create_from_artifact(mh_engine **engine, const char *pa
     for (const auto &t : tensors) {
       size_t es = 0;
       const int dt = mh::tensor_dtype(t.a, t.name, &es);
-      if (mh::elements(t.a) * es != t.a.bytes) {
+      bool sized = false;
+      try {
+        sized = t.a.bytes % es == 0 && mh::elements(t.a) == t.a.bytes / es;
+      } catch (const std::exception &) {
+        sized = false;
+      }
+      if (!sized) {
         mh_engine_destroy(e);
         throw mh::Error("tensor '" + t.name + "' payload does not match its shape");
       }

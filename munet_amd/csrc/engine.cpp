@@ -25,6 +25,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <set>
 #include <memory>
 #include <iomanip>
 #include <sstream>
@@ -127,6 +128,7 @@ struct EngineImpl {
   // parameters and weight arena (the packed weights do not depend on the
   // input shape): pp points at the owning map, shared_wbuf at its arena.
   const std::map<std::string, Param> *pp = &params;
+  std::set<std::string> used_params;  // names the lowering read
   char *shared_wbuf = nullptr;
   size_t shared_wbytes = 0;
   // pinned host staging for the PCIe path (allocated on first use)
@@ -206,11 +208,22 @@ struct EngineImpl {
   }
 
   // ---------------------------------------------------------------- params
-  const Param &param(const std::string &n) const {
+  const Param &param(const std::string &n) {
     auto it = pp->find(n);
     if (it == pp->end()) throw Error("missing parameter '" + n + "'");
     if (it->second.dt != dt) throw Error("parameter '" + n + "' has the wrong dtype");
+    used_params.insert(n);
     return it->second;
+  }
+  // A parameter that must hold exactly `count` elements of the engine dtype
+  // (the reference's loader checks every shape, src/inference_serialization.cpp:
+  // 863-881; LayerNorm its weight and bias, src/core/ops/normalization.cpp:141-145).
+  const Param &param(const std::string &n, size_t count) {
+    const Param &p = param(n);
+    if (p.host.size() != count * dt_size(dt))
+      throw Error("parameter '" + n + "' has " + std::to_string(p.host.size() / dt_size(dt)) + " elements, expected " +
+                  std::to_string(count));
+    return p;
   }
   // Pending device upload of host bytes into the weights arena.
   const void *upload(std::vector<uint8_t> bytes) {
@@ -252,8 +265,7 @@ struct EngineImpl {
     return t;
   }
   const void *bias_or_zero(const std::string &n, int len) {
-    auto it = pp->find(n);
-    if (it != pp->end()) return upload(it->second.host);
+    if (pp->count(n)) return upload(param(n, size_t(len)).host);
     return upload(std::vector<uint8_t>(size_t(len) * dt_size(dt), 0));
   }
 
@@ -296,7 +308,11 @@ struct EngineImpl {
     for (int i = int(ops.size()) - 1; i >= 0; --i) {
       Op &o = ops[i];
       if (std::find(o.out.begin(), o.out.end(), x) == o.out.end()) continue;
-      const bool gemm = o.kind == OP_GEMM && o.out[0] == x && o.a[1] == d && o.stats_out < 0;
+      // a GEMM writes the partials only from its bias + residual epilogue
+      // program (no activation) on the pipelined kernel (K % 8 == 0); any
+      // other producer keeps the LayerNorm kernel
+      const bool gemm = o.kind == OP_GEMM && o.out[0] == x && o.a[1] == d && o.stats_out < 0 && o.b != nullptr &&
+                        o.resid >= 0 && o.act == ACT_NONE && o.a[2] % 8 == 0;
       const bool embed = (o.kind == OP_EMBED || o.kind == OP_EMBED_POS) && o.out[0] == x && o.a[2] == d &&
                          o.stats_out < 0;
       if (!gemm && !embed) return f;
@@ -321,10 +337,8 @@ struct EngineImpl {
   // the epilogue terms: cs[o] = sum_k round(gamma_k w_ok), bw[o] = sum_k
   // beta_k w_ok (double sums).
   void fold_weights(std::vector<uint8_t> &packed, int in_f, int out_f, const LnFold &f, std::vector<uint8_t> &cs,
-                    std::vector<uint8_t> &bw) const {
-    const Param &gp = param(f.pfx + "weight"), &bp = param(f.pfx + "bias");
-    if (gp.host.size() != size_t(in_f) * 2 || bp.host.size() != size_t(in_f) * 2)
-      throw Error(f.pfx + ": LayerNorm parameters have the wrong size");
+                    std::vector<uint8_t> &bw) {
+    const Param &gp = param(f.pfx + "weight", size_t(in_f)), &bp = param(f.pfx + "bias", size_t(in_f));
     const uint16_t *gm = reinterpret_cast<const uint16_t *>(gp.host.data());
     const uint16_t *bt = reinterpret_cast<const uint16_t *>(bp.host.data());
     uint16_t *w = reinterpret_cast<uint16_t *>(packed.data());
@@ -433,8 +447,8 @@ struct EngineImpl {
     o.a[0] = long(numel(vals[x].shape) / d);
     o.a[1] = d;
     o.f = eps;
-    o.w = upload(param(pfx + "weight").host);
-    o.b = upload(param(pfx + "bias").host);
+    o.w = upload(param(pfx + "weight", size_t(d)).host);
+    o.b = upload(param(pfx + "bias", size_t(d)).host);
     return y;
   }
 
@@ -452,7 +466,7 @@ struct EngineImpl {
     for (const char *p : {"q_proj.", "k_proj.", "v_proj."}) {
       auto w = pack_linear(param(pfx + p + "weight"), E, E);
       wcat.insert(wcat.end(), w.begin(), w.end());
-      const auto &b = param(pfx + p + "bias").host;
+      const auto &b = param(pfx + p + "bias", size_t(E)).host;
       bcat.insert(bcat.end(), b.begin(), b.end());
     }
     const int q = new_val({B * H, T, hd}, dt), k = new_val({B * H, T, hd}, dt), v = new_val({B * H, T, hd}, dt);
@@ -538,7 +552,7 @@ struct EngineImpl {
       int y = new_val({xs[0], xs[1], D}, dt);
       Op &o = emit(OP_EMBED, pfx + "embedding", {x}, {y});
       o.a[0] = long(numel(xs)); o.a[1] = V; o.a[2] = D; o.a[3] = 1;
-      o.w = upload(param(pfx + "weight").host);
+      o.w = upload(param(pfx + "weight", size_t(V) * D).host);
       return y;
     }
     if (t == "TransformerBlock")
@@ -553,8 +567,8 @@ struct EngineImpl {
       int h = new_val({xs[0], xs[1], d}, dt);
       Op &o = emit(OP_EMBED_POS, pfx + "embed", {x}, {h});
       o.a[0] = long(numel(xs)); o.a[1] = V; o.a[2] = d; o.a[3] = xs[1];
-      o.w = upload(param(pfx + "token_embed.weight").host);
-      o.w2 = upload(param(pfx + "pos_embed.weight").host);
+      o.w = upload(param(pfx + "token_embed.weight", size_t(V) * d).host);
+      o.w2 = upload(param(pfx + "pos_embed.weight", size_t(C) * d).host);
       const int L = m.at("num_layers").as_int(), H = m.at("num_heads").as_int(), ffn = m.at("ffn").as_int();
       const float eps = float(m.get_num("eps", 1e-5));
       for (int i = 0; i < L; ++i) h = block(h, pfx + "blocks." + std::to_string(i) + ".", d, H, ffn, true, eps);
@@ -801,7 +815,12 @@ struct EngineImpl {
     const std::string t = cfg.at("type").as_str();
     const bool ids = t == "DecoderLM" || t == "Embedding";
     input = new_val(ishape, ids ? I32 : dt, ROWMAJOR);
+    used_params.clear();
     int y = lower(cfg, input, "");
+    // every parameter given must belong to the model (the reference's
+    // load_state_dict rejects unknown names)
+    for (const auto &kv : *pp)
+      if (!used_params.count(kv.first)) throw Error("unknown parameter '" + kv.first + "' for this model");
     y = to_rowmajor4(y, "output");
     output = y;
     // a final output larger than the L2s and most of the last-level cache is

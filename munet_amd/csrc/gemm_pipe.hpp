@@ -273,6 +273,9 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
   // per chunk slot), so every index below is a compile-time constant
   static constexpr int LPC = LNCH / CH;
   __device__ __forceinline__ void ln_issue(const EpiArgs &ep, LnIn &in, int tid) const {
+    // a chunk holds up to ln_chunk(64) = 16 partials (the host admits 64 per
+    // row): every tile that folds a LayerNorm needs room for all of them
+    static_assert(LPC >= 16, "LayerNorm chunk slot smaller than the largest chunk");
     const int r = tid / TPR, q = tid % TPR, P = ep.ln_parts, chunk = ln_chunk(P);
     const long row = min(m0 + r, M - 1);
     if ((P & 1) == 0) {  // rows and chunks start on 16-byte boundaries: two partials per load

@@ -49,7 +49,18 @@ class Engine:
         dt = synth.DTYPE_CODES[config.get("dtype", "float32")]
         for name, arr in params.items():
             a = np.ascontiguousarray(arr)
-            _lib.call("mh_engine_set_param", h, name.encode(), a.ctypes.data_as(_vp), a.nbytes, dt)
+            # the storage dtype of each array: float32 and float16 values, uint16
+            # bit patterns of the model's 16-bit dtype, int32; the engine converts
+            # another floating dtype with MuNet's codecs and rejects the rest
+            if a.dtype == np.float16:
+                a, pdt = a.view(np.uint16), synth.F16
+            elif a.dtype == np.uint16:
+                pdt = dt if dt in (synth.F16, synth.BF16) else synth.BF16
+            else:
+                pdt = {np.dtype(np.float32): synth.F32, np.dtype(np.int32): synth.I32}.get(a.dtype)
+                if pdt is None:
+                    raise TypeError(f"parameter '{name}': unsupported array dtype {a.dtype}")
+            _lib.call("mh_engine_set_param", h, name.encode(), a.ctypes.data_as(_vp), a.nbytes, pdt)
         del lib
         return self
 

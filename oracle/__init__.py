@@ -75,6 +75,15 @@ class CpuOracle:
         fn = getattr(self.lib, "orc_threads", None)
         return int(fn()) if fn else 1
 
+    def set_threading(self, mode):
+        """Restatement only. "parity": every loop over independent outputs is
+        split over all hardware threads (fast checking). "reference": the
+        reference's own split (CPUBackend::parallel_for, inline below 1024
+        iterations, src/backend/cpu_backend.hpp:101-127; the typed fallbacks,
+        LayerNorm, masked_fill and the gathers serial), for the timed CPU
+        baseline. Results are bit-identical in both modes."""
+        self._call("set_threading", _i({"parity": 0, "reference": 1}[mode]))
+
     @staticmethod
     def _c(a, dt):
         return np.ascontiguousarray(a, dtype=storage_np(dt))
@@ -118,8 +127,25 @@ class CpuOracle:
     def add(self, a, b, dt):
         return self.binary(ADD, a, b, dt)
 
+    def sub(self, a, b, dt):
+        return self.binary(SUB, a, b, dt)
+
     def mul(self, a, b, dt):
         return self.binary(MUL, a, b, dt)
+
+    def div(self, a, b, dt):
+        return self.binary(DIV, a, b, dt)
+
+    def masked_fill(self, x, mask, value, dt):
+        """ops::masked_fill (elementwise.cpp:8-53): mask int32, same shape as x;
+        `value` is the double the op's ScalarValue carries."""
+        x = self._c(x, dt)
+        mask = np.ascontiguousarray(mask, dtype=np.int32)
+        if mask.shape != x.shape:
+            raise OracleError("masked_fill: input/mask shape mismatch")
+        out = np.empty_like(x)
+        self._call("masked_fill", _i(dt), _ptr(x), _ptr(mask), _ptr(out), _sz(x.size), ctypes.c_double(value))
+        return out
 
     def _unary(self, name, x, dt):
         x = self._c(x, dt)

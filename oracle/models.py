@@ -119,6 +119,8 @@ def layer_forward(o: CpuOracle, layer, p, prefix, x, dt):
         return o.layer_norm(x, p[prefix + "weight"], p[prefix + "bias"], dt, layer.get("eps", 1e-5))
     if t == "MultiHeadAttention":
         return o.mha(x, p, layer["num_heads"], layer.get("causal", True), dt, prefix=prefix)
+    if t == "TransformerBlock":
+        return block_forward(o, {**layer, "dtype": synth.DTYPE_NAMES[dt]}, p, x, prefix, layer.get("causal", False))
     raise ValueError(f"oracle: unsupported layer {t}")
 
 

@@ -127,10 +127,28 @@ inline void wr(void *p, int dt, size_t i, double v) {
   throw std::runtime_error("bad dtype");
 }
 
-// Independent output ranges only; per-element op order is untouched.
-void par_for(size_t n, const std::function<void(size_t, size_t)> &fn) {
+// Which threading the reference gives a loop (src/backend/cpu_backend.hpp:
+// 101-127): BACKEND loops run in CPUBackend::parallel_for (inline below 1024
+// iterations, otherwise blocks over hardware_concurrency() threads); SERIAL
+// loops are the typed fallbacks and host-side ops (ops/common.hpp:46-289,
+// ops/normalization.cpp:125-224, ops/elementwise.cpp:8-53), which never split.
+enum Path { BACKEND = 0, SERIAL = 1 };
+
+// 0 = parity mode: every loop over independent outputs is split over all
+//     hardware threads once it has 64 iterations (fast checking);
+// 1 = reference mode: the reference's own split per Path (the timed CPU
+//     baseline).  Either way each output element's operation order, and so
+//     every bit, is the reference's.
+int g_threading = 0;
+
+void par_for(size_t n, const std::function<void(size_t, size_t)> &fn, Path path = BACKEND) {
   unsigned nt = std::max(1u, std::thread::hardware_concurrency());
-  if (n < 64 || nt == 1) { fn(0, n); return; }
+  if (g_threading == 1) {
+    if (path == SERIAL || n < 1024 || nt == 1) { fn(0, n); return; }
+  } else if (n < 64 || nt == 1) {
+    fn(0, n);
+    return;
+  }
   nt = unsigned(std::min<size_t>(nt, n));
   std::vector<std::thread> th;
   size_t blk = (n + nt - 1) / nt;
@@ -152,9 +170,96 @@ std::vector<float> to_f32(const void *p, int dt, size_t n) {
 // fp32 / fp16: float accumulation in k order (cpu_backend.hpp:350-373,
 // common.hpp:276-289); fp16 rounds the float result with round-half-away.
 // bf16: double accumulation, then double->float->bf16 (common.hpp:128-165).
+
+// Parity-mode product over rows [r0, r1) of one slice: the row of A and the
+// transposed B (bt, [N, K]) are k-contiguous exact copies of the operands, and
+// eight output columns run side by side, each its own sum in k order -- the
+// operations of the reference's i-n-k loop, only laid out for the cache.
+template <typename T, typename Store>
+void product_rows(const T *a, const T *bt, int M, int K, int N, bool transA,
+                  size_t r0, size_t r1, Store store) {
+  std::vector<T> arow(K);
+  for (size_t m = r0; m < r1; ++m) {
+    for (int k = 0; k < K; ++k) arow[k] = transA ? a[size_t(k) * M + m] : a[m * K + k];
+    int n = 0;
+    for (; n + 8 <= N; n += 8) {
+      const T *b0 = bt + size_t(n) * K, *b1 = b0 + K, *b2 = b1 + K, *b3 = b2 + K;
+      const T *b4 = b3 + K, *b5 = b4 + K, *b6 = b5 + K, *b7 = b6 + K;
+      T s0 = 0, s1 = 0, s2 = 0, s3 = 0, s4 = 0, s5 = 0, s6 = 0, s7 = 0;
+      for (int k = 0; k < K; ++k) {
+        const T x = arow[k];
+        s0 += x * b0[k];
+        s1 += x * b1[k];
+        s2 += x * b2[k];
+        s3 += x * b3[k];
+        s4 += x * b4[k];
+        s5 += x * b5[k];
+        s6 += x * b6[k];
+        s7 += x * b7[k];
+      }
+      store(m, n, s0);
+      store(m, n + 1, s1);
+      store(m, n + 2, s2);
+      store(m, n + 3, s3);
+      store(m, n + 4, s4);
+      store(m, n + 5, s5);
+      store(m, n + 6, s6);
+      store(m, n + 7, s7);
+    }
+    for (; n < N; ++n) {
+      const T *b0 = bt + size_t(n) * K;
+      T s0 = 0;
+      for (int k = 0; k < K; ++k) s0 += arow[k] * b0[k];
+      store(m, n, s0);
+    }
+  }
+}
+
+// Parity mode: decode both operands once (exact) into T, B transposed.
+template <typename T>
+void matmul_parity(int dt, const void *A, const void *B, void *C, int batch, int M,
+                   int K, int N, bool b_batched, bool transA, bool transB) {
+  const size_t sa = size_t(M) * K, sb = size_t(K) * N, sc = size_t(M) * N;
+  const int nb = b_batched ? batch : 1;
+  std::vector<T> ad(sa * batch), bt(sb * nb);
+  par_for(ad.size(), [&](size_t s, size_t e) {
+    for (size_t i = s; i < e; ++i) ad[i] = T(rd(A, dt, i));
+  });
+  par_for(size_t(nb) * N, [&](size_t s, size_t e) {
+    for (size_t r = s; r < e; ++r) {
+      size_t bi = r / N, n = r % N;
+      for (int k = 0; k < K; ++k)
+        bt[bi * sb + n * K + k] =
+            T(rd(B, dt, bi * sb + (transB ? n * K + k : size_t(k) * N + n)));
+    }
+  });
+  for (int bi = 0; bi < batch; ++bi) {
+    const T *a = ad.data() + bi * sa, *b = bt.data() + (b_batched ? bi * sb : 0);
+    par_for(size_t(M), [&](size_t s, size_t e) {
+      product_rows<T>(a, b, M, K, N, transA, s, e, [&](size_t m, int n, T v) {
+        const size_t o = bi * sc + m * N + n;
+        if (dt == F32)
+          static_cast<float *>(C)[o] = float(v);
+        else if (dt == F16)
+          static_cast<uint16_t *>(C)[o] = enc_f16(float(v));
+        else
+          wr(C, dt, o, double(v));
+      });
+    });
+  }
+}
+
 void matmul_slices(int dt, const void *A, const void *B, void *C, int batch,
                    int M, int K, int N, bool b_batched, bool transA,
                    bool transB) {
+  if (g_threading == 0) {
+    if (dt == BF16)
+      matmul_parity<double>(dt, A, B, C, batch, M, K, N, b_batched, transA, transB);
+    else
+      matmul_parity<float>(dt, A, B, C, batch, M, K, N, b_batched, transA, transB);
+    return;
+  }
+  // Reference mode: the reference's loops as they run.
   const size_t sa = size_t(M) * K, sb = b_batched ? size_t(K) * N : 0,
                sc = size_t(M) * N;
   if (dt == F32 || dt == F16) {
@@ -186,28 +291,22 @@ void matmul_slices(int dt, const void *A, const void *B, void *C, int batch,
             static_cast<uint16_t *>(C)[bi * sc + m * N + n] = enc_f16(sum);
         }
       }
-    });
+    }, batch > 1 ? SERIAL : BACKEND);
     return;
   }
-  // bf16: decode operands once (exact), double accumulate.
-  std::vector<double> ad(sa * batch), bd(b_batched ? sb * batch : size_t(K) * N);
-  for (size_t i = 0; i < ad.size(); ++i) ad[i] = rd(A, dt, i);
-  for (size_t i = 0; i < bd.size(); ++i) bd[i] = rd(B, dt, i);
-  par_for(size_t(batch) * M, [&](size_t s, size_t e) {
-    for (size_t r = s; r < e; ++r) {
-      size_t bi = r / M, m = r % M;
-      const double *a = ad.data() + bi * sa, *b = bd.data() + bi * sb;
+  // bf16: the serial scalar fallback exactly as it runs (ops/common.hpp:
+  // 146-160), each operand read and decoded per product.
+  for (int bi = 0; bi < batch; ++bi)
+    for (int m = 0; m < M; ++m)
       for (int n = 0; n < N; ++n) {
         double sum = 0.0;
         for (int k = 0; k < K; ++k) {
-          double av = transA ? a[size_t(k) * M + m] : a[m * K + k];
-          double bv = transB ? b[size_t(n) * K + k] : b[size_t(k) * N + n];
-          sum += av * bv;
+          size_t ai = bi * sa + (transA ? size_t(k) * M + m : size_t(m) * K + k);
+          size_t bidx = bi * sb + (transB ? size_t(n) * K + k : size_t(k) * N + n);
+          sum += rd(A, dt, ai) * rd(B, dt, bidx);
         }
-        wr(C, dt, bi * sc + m * N + n, sum);
+        wr(C, dt, bi * sc + size_t(m) * N + n, sum);
       }
-    }
-  });
 }
 
 enum BinOp { ADD = 0, SUB = 1, MUL = 2, DIV = 3 };
@@ -268,7 +367,7 @@ void binary(int dt, int op, const void *a, const int *as, int an, const void *b,
         wr(out, dt, i, binop<double>(op, rd(a, dt, offa), rd(b, dt, offb)));
       }
     }
-  });
+  }, dt == F32 ? BACKEND : SERIAL);
 }
 
 void relu(int dt, const void *in, void *out, size_t n) {
@@ -282,7 +381,7 @@ void relu(int dt, const void *in, void *out, size_t n) {
         wr(out, dt, i, std::max(v, 0.0));
       }
     }
-  });
+  }, dt == F32 ? BACKEND : SERIAL);
 }
 
 void sigmoid(int dt, const void *in, void *out, size_t n) {
@@ -296,7 +395,7 @@ void sigmoid(int dt, const void *in, void *out, size_t n) {
         wr(out, dt, i, 1.0 / (1.0 + std::exp(-v)));
       }
     }
-  });
+  }, dt == F32 ? BACKEND : SERIAL);
 }
 
 // nn::GELU (activations.hpp:31-38): c = fill(1.702f) in dtype; x*sigmoid(x*c)
@@ -330,7 +429,7 @@ void softmax(int dt, const void *in, void *out, int rows, int cols) {
         for (int i = 0; i < cols; ++i) wr(out, dt, base + i, std::exp(rd(in, dt, base + i) - mx) / sum);
       }
     }
-  });
+  }, dt == F32 ? BACKEND : SERIAL);
 }
 
 void layer_norm(int dt, const void *x, const void *w, const void *b, void *out,
@@ -353,7 +452,7 @@ void layer_norm(int dt, const void *x, const void *w, const void *b, void *out,
         wr(out, dt, base + c, xh * rd(w, dt, c) + rd(b, dt, c));
       }
     }
-  });
+  }, SERIAL);
 }
 
 // MultiHeadAttention::forward_impl core (attention.hpp:51-99) from projected
@@ -458,7 +557,7 @@ void mha_core(int dt, const void *q2d, const void *k2d, const void *v2d,
         }
       }
     }
-  });
+  }, dt == BF16 ? SERIAL : BACKEND);
   // merge heads [B,H,T,hd] -> [B,T,H*hd]
   for (int bb = 0; bb < B; ++bb)
     for (int h = 0; h < H; ++h)
@@ -539,6 +638,14 @@ const char *orc_last_error() { return g_err.c_str(); }
 
 // Threads the restatement's parallel loops use (std::thread::hardware_concurrency).
 int orc_threads() { return int(std::max(1u, std::thread::hardware_concurrency())); }
+
+// Threading mode of every later call in this process: 0 = parity (split every
+// loop over independent outputs), 1 = reference (MuNet's own split, see Path).
+int orc_set_threading(int mode) {
+  if (mode != 0 && mode != 1) { g_err = "threading mode must be 0 or 1"; return 1; }
+  g_threading = mode;
+  return 0;
+}
 
 int orc_encode(int dt, const float *src, void *dst, size_t n) {
   ORC_GUARD(for (size_t i = 0; i < n; ++i) wr(dst, dt, i, double(src[i])))

@@ -17,6 +17,7 @@
 //   ref_max_pool2d   -> nn::MaxPool2d           (src/nn/pooling.hpp:28-35)
 //   ref_upsample2d   -> nn::Upsample            (src/nn/pooling.hpp:37-42)
 //   ref_concat       -> Tensor::cat             (src/core/ops/shape.cpp:8-48)
+//   ref_masked_fill  -> Tensor::masked_fill     (src/core/ops/elementwise.cpp:8-53)
 #include "core/grad_mode.hpp"
 #include "nn/activations.hpp"
 #include "nn/attention.hpp"
@@ -226,6 +227,20 @@ int ref_concat(int dt, const void *const *inputs, const int *shapes, int count,
     for (int j = 0; j < count; ++j)
       ts.push_back(from_host(inputs[j], mk_shape(shapes + j * ndim, ndim), to_dt(dt)));
     to_host(Tensor::cat(ts, dim), out);
+  })
+}
+
+// mask: int32 [n] (any non-zero entry selects `value`); value is the double
+// a ScalarValue carries (src/types.hpp:201-208), as the op receives it.
+int ref_masked_fill(int dt, const void *x, const int32_t *mask, void *out,
+                    size_t n, double value) {
+  REF_GUARD({
+    Tensor tx = from_host(x, Shape{int(n)}, to_dt(dt));
+    Tensor tm = from_host(mask, Shape{int(n)}, DataType::Int32);
+    ScalarValue v;
+    v.dtype = DataType::Float32;
+    v.value = value;
+    to_host(tx.masked_fill(tm, v), out);
   })
 }
 

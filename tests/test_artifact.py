@@ -116,15 +116,22 @@ def test_not_a_zip(tmp_path):
         Engine(device=-1).load_artifact(str(path))
 
 
-def test_accepts_writer_producers(tmp_path):
-    """The reference's Python writers tag 'munet_nn' / 'munet_pytorch_interop'."""
+def test_producer_must_be_munet(tmp_path):
+    """The reference's deploy loader accepts exactly the producer tag 'munet'
+    or none (src/inference_serialization.cpp:35, :997-1000); the tag its
+    Python bindings write ('munet_nn', src/bindings.cpp:2049) is refused there
+    too."""
     cfg = models.mlp_config()
-    for prod in ("munet", "munet_nn", "munet_pytorch_interop"):
-        state = _good_state(cfg, _params(cfg, "mlp"))
+    state = _good_state(cfg, _params(cfg, "mlp"))
+    state["__producer__"] = np.array("munet")
+    _write(tmp_path / "ok.npz", state)
+    Engine(device=-1).load_artifact(str(tmp_path / "ok.npz")).compile((4, 784))
+    for prod in ("munet_nn", "munetx", "munet_pytorch_interop"):
         state["__producer__"] = np.array(prod)
         path = tmp_path / f"{prod}.npz"
         _write(path, state)
-        Engine(device=-1).load_artifact(str(path)).compile((4, 784))
+        with pytest.raises(_lib.HipError, match="unsupported producer"):
+            Engine(device=-1).load_artifact(str(path))
 
 
 def test_zip64_members_parse(tmp_path):
@@ -136,3 +143,38 @@ def test_zip64_members_parse(tmp_path):
     with zipfile.ZipFile(path) as z:
         assert all(i.compress_type == zipfile.ZIP_STORED for i in z.infolist())
     Engine(device=-1).load_artifact(str(path)).compile((4, 784))
+
+
+def _npy_bytes(descr, shape, payload):
+    """A .npy member with a hand-written header (descr and shape as given)."""
+    hdr = "{'descr': '%s', 'fortran_order': False, 'shape': %s, }" % (descr, shape)
+    hdr += " " * ((64 - (10 + len(hdr) + 1) % 64) % 64) + "\n"
+    return b"\x93NUMPY\x01\x00" + len(hdr).to_bytes(2, "little") + hdr.encode() + payload
+
+
+@pytest.mark.parametrize("member,descr,shape,payload,msg", [
+    # 2^62 UTF-32 characters: chars * 4 wraps to 0 in 64 bits
+    ("__format_name__", "<U4611686018427387904", "()", b"m\0\0\0", "truncated"),
+    ("__producer__", "|S18446744073709551615", "()", b"munet", "truncated"),
+    # dimensions whose product wraps round to the payload's element count
+    ("0.bias", "<f4", "(4294967296, 4294967296, 1)", b"\0" * 1024, "payload does not match|overflow"),
+    ("0.bias", "<f4", "(256,)", b"\0" * 1023, "payload does not match"),
+])
+def test_malformed_npy_headers_are_rejected(tmp_path, member, descr, shape, payload, msg):
+    """Header fields the parser must bound-check without overflowing: string
+    lengths from the descr and the element count from the shape."""
+    cfg = models.mlp_config()
+    state = _good_state(cfg, _params(cfg, "mlp"))
+    state["__producer__"] = np.array("munet")
+    path = tmp_path / "bad.npz"
+    with zipfile.ZipFile(path, "w", zipfile.ZIP_STORED) as z:
+        for k, v in state.items():
+            if k == member:
+                z.writestr(k + ".npy", _npy_bytes(descr, shape, payload))
+            else:
+                import io
+                buf = io.BytesIO()
+                np.save(buf, v, allow_pickle=False)
+                z.writestr(k + ".npy", buf.getvalue())
+    with pytest.raises(_lib.HipError, match=msg):
+        Engine(device=-1).load_artifact(str(path)).compile((4, 784))

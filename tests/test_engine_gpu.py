@@ -4,9 +4,11 @@ hipGraph forward) against the CPU restatement of MuNet's CPU backend
 
 Tolerances (BASELINE.json north_star): normwise rel 1e-4 fp32, 2e-2 fp16/bf16;
 argmax bit-exact wherever the reference top-1/top-2 gap exceeds the tolerance.
-Full BASELINE sizes are used for the MLP, CNN and encoder block; the decoder
-and UNet run at reduced sizes the oracle finishes in seconds, and the full
-12-layer decoder is checked through size-independent properties.
+Every BASELINE config runs at full size: the MLP, CNN and encoder block
+against the oracle outright, the 12-layer decoder against the oracle and
+through size-independent properties, the UNet against the oracle per image
+(batch-1 forwards at full resolution and width) plus batch independence at
+batch 8.  Reduced sizes add dtype and shape coverage.
 """
 import numpy as np
 import pytest
@@ -110,8 +112,30 @@ def test_decoder_full_width_one_layer(orc):
     _argmax_check(y, ref, synth.BF16)
 
 
-def test_decoder_full_config_properties():
-    """BASELINE config 5 at full size (12 layers, B4 T1024 V32000).
+@pytest.fixture(scope="module")
+def gpt_full():
+    """BASELINE config 5 at full size: 12 layers, B4 T1024 V32000, bf16, the
+    engine's default LayerNorm fold."""
+    cfg = models.decoder_config()
+    eng, p, ids = _build(cfg, (4, 1024), "gpt")
+    return cfg, eng, p, ids, eng.run(ids)
+
+
+def test_decoder_full_config_vs_oracle(orc, gpt_full):
+    """The full 12-layer forward against the CPU restatement of MuNet's CPU
+    backend on the same seeded weights and ids: normwise 2e-2, argmax wherever
+    the reference top-1/top-2 gap exceeds the tolerance."""
+    cfg, _eng, p, ids, y = gpt_full
+    print(f"oracle: 12-layer decoder forward on {orc.threads()} threads", flush=True)
+    ref = omodels.forward(orc, cfg, p, ids)
+    err = assert_close(y, ref, synth.BF16, what="12-layer decoder logits")
+    clear, ties = _argmax_check(y, ref, synth.BF16)
+    print(f"full decoder: normwise error {err:.3e}, argmax equal on {clear} rows ({ties} near-ties)")
+    assert clear > 0.9 * ids.size
+
+
+def test_decoder_full_config_properties(gpt_full):
+    """Size-independent properties at full size.
 
     MuNet's attention reads K through its raw [hd, B*H*T] reinterpretation
     (src/nn/attention.hpp:64), so column j of a block mixes keys of other
@@ -120,9 +144,7 @@ def test_decoder_full_config_properties():
     softmax weight is exactly 1 whatever K holds, so logits[:, 0] depend on
     ids[:, 0] only (the reference's own causality check,
     tests/test_nn.cpp:594-629).  Plus determinism and finiteness."""
-    cfg = models.decoder_config()
-    eng, p, ids = _build(cfg, (4, 1024), "gpt")
-    y = eng.run(ids)
+    _cfg, eng, _p, ids, y = gpt_full
     assert y.shape == (4, 1024, 32000)
     assert np.all(np.isfinite(dec(y, synth.BF16)))
     ids2 = ids.copy()
@@ -131,6 +153,27 @@ def test_decoder_full_config_properties():
     assert np.array_equal(y2[:, 0], y[:, 0])
     assert not np.array_equal(y2[:, 1:], y[:, 1:])
     assert np.array_equal(eng.run(ids), y)
+
+
+def test_unet_full_config(orc):
+    """BASELINE config 4 at full size: 8x3x128x128, 64/128/256/512 channels,
+    fp16.  Every image is independent, so each image of the batch-8 forward
+    equals the batch-1 forward of that image bit for bit, and batch-1
+    forwards at full resolution and width match the oracle."""
+    cfg = models.unet_config()
+    p = models.init_params(cfg, "he", scope="unet_full")
+    x = models.make_input(cfg, (8, 3, 128, 128), "he", scope="unet_full_in")
+    y = Engine(0).load(cfg, p).compile((8, 3, 128, 128)).run(x)
+    assert y.shape == (8, 2, 128, 128)
+    assert np.all(np.isfinite(dec(y, synth.F16)))
+    one = Engine(0).load(cfg, p).compile((1, 3, 128, 128))
+    for i in (0, 5):
+        yi = one.run(np.ascontiguousarray(x[i:i + 1]))
+        assert np.array_equal(yi, y[i:i + 1]), f"image {i}: batch-8 and batch-1 forwards differ"
+    print(f"oracle: UNet forward of one 128x128 image on {orc.threads()} threads", flush=True)
+    ref = omodels.forward(orc, cfg, p, np.ascontiguousarray(x[:1]))
+    err = assert_close(y[:1], ref, synth.F16, what="unet full config")
+    print(f"unet full config: normwise error {err:.3e}")
 
 
 def test_unet_small(orc):

@@ -162,3 +162,54 @@ def test_engine_errors():
     with pytest.raises(_lib.HipError, match="unsupported module type"):
         bad = {"type": "Sequential", "dtype": "float32", "layers": [{"type": "LSTM"}]}
         Engine(device=-1).load(bad, {}).compile((2, 3))
+
+
+def test_fold_only_from_a_residual_producer():
+    """A LayerNorm folds into its consumer only when its input comes from the
+    embedding or a bias + residual GEMM with no activation (the only producer
+    epilogue that writes row partials).  A plain Linear, a Linear + ReLU or a
+    bias-free Linear before a bf16 TransformerBlock keeps ln1 as a kernel
+    (ln2's producer, the out-projection with its residual, still folds)."""
+    blk = {"type": "TransformerBlock", "d_model": 64, "num_heads": 2, "ffn": 128, "causal": False}
+    for head in ([{"type": "Linear", "in_features": 40, "out_features": 64}],
+                 [{"type": "Linear", "in_features": 40, "out_features": 64}, {"type": "ReLU"}],
+                 [{"type": "Linear", "in_features": 40, "out_features": 64, "bias": False}],
+                 [{"type": "Linear", "in_features": 36, "out_features": 64}]):
+        cfg = {"type": "Sequential", "dtype": "bfloat16", "layers": head + [blk]}
+        cfg["layers"][-1] = dict(blk)
+        in_f = head[0]["in_features"]
+        e, p = _plan(cfg, (2, 8, in_f))
+        kinds = [o["kind"] for o in p["ops"]]
+        assert kinds[1] == "layer_norm", kinds
+        assert e.stats()["ln_folds"] == 1
+
+
+def _params_for(cfg):
+    return _zero_params(cfg)
+
+
+@pytest.mark.parametrize("name,count", [
+    ("blocks.0.attn.q_proj.bias", 127), ("blocks.0.ln1.bias", 100), ("blocks.0.ff.0.bias", 511),
+    ("token_embed.weight", 999 * 128), ("pos_embed.weight", 255 * 128), ("head.bias", 999),
+    ("ln_f.weight", 129)])
+def test_wrong_sized_parameter_is_rejected(name, count):
+    """Every parameter the engine uploads is checked against the element
+    count its layer needs (the reference's loader checks every shape:
+    src/inference_serialization.cpp:863-881)."""
+    cfg = models.decoder_config(vocab=1000, ctx=256, d_model=128, num_heads=2, num_layers=1, ffn=512)
+    p = _params_for(cfg)
+    p[name] = np.zeros(count, dtype=np.uint16)
+    with pytest.raises(_lib.HipError, match=f"parameter '{name}' has {count} elements"):
+        Engine(device=-1).load(cfg, p).compile((2, 16))
+
+
+def test_unknown_or_wrong_dtype_parameter_is_rejected():
+    cfg = models.mlp_config((20, 16, 4))
+    p = _params_for(cfg)
+    p["9.weight"] = np.zeros((3, 3), np.float32)
+    with pytest.raises(_lib.HipError, match="unknown parameter '9.weight'"):
+        Engine(device=-1).load(cfg, p).compile((5, 20))
+    p = _params_for(cfg)
+    p["0.bias"] = np.zeros(16, np.int32)
+    with pytest.raises(_lib.HipError, match="0.bias"):
+        Engine(device=-1).load(cfg, p).compile((5, 20))

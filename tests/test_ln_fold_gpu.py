@@ -103,3 +103,38 @@ def test_folded_decoder_bit_identical_across_tiles(monkeypatch, tile):
     e = Engine(0).load(cfg, params).compile((2, 128))
     assert e.stats()["ln_folds"] == 2 * 2 + 1
     assert np.array_equal(e.run(ids), y)
+
+
+@pytest.mark.parametrize("head", ["linear", "linear_relu", "linear_nobias", "linear_k36"])
+def test_linear_then_block_vs_oracle(orc, head):
+    """bf16 Sequential[Linear, TransformerBlock]: a producer whose epilogue
+    cannot write row partials (no residual, an activation, no bias, K % 8 != 0)
+    leaves ln1 a kernel; the model compiles and matches the oracle."""
+    in_f = 36 if head == "linear_k36" else 40
+    lin = {"type": "Linear", "in_features": in_f, "out_features": 128, "bias": head != "linear_nobias"}
+    layers = [lin] + ([{"type": "ReLU"}] if head == "linear_relu" else [])
+    layers.append({"type": "TransformerBlock", "d_model": 128, "num_heads": 2, "ffn": 256, "causal": False})
+    cfg = {"type": "Sequential", "dtype": "bfloat16", "layers": layers}
+    params = models.init_params(cfg, "xavier", scope="lin_blk_" + head)
+    x = synth.make_tensor("lin_blk_in", "x", (2, 32, in_f), synth.BF16, "normal")
+    eng = Engine(0).load(cfg, params).compile((2, 32, in_f))
+    assert eng.stats()["ln_folds"] == 1  # ln2 only
+    y = eng.run(x)
+    ref = omodels.forward(orc, cfg, params, x)
+    assert_close(y, ref, synth.BF16, what=f"Linear -> TransformerBlock ({head})")
+
+
+@pytest.mark.parametrize("d,heads", [(768, 12), (1008, 12)])
+def test_decoder_fold_partial_counts_vs_oracle(orc, d, heads):
+    """The consumer combines 16 partials per row at d = 768 (48-column
+    groups) and 63 at d = 1008 (16-column groups, an odd count loaded two
+    at a time with a clamped last pair)."""
+    cfg = models.decoder_config(vocab=512, ctx=64, d_model=d, num_heads=heads, num_layers=2, ffn=2 * d)
+    params = _perturbed(cfg, f"lnfold_parts_{d}")
+    ids = models.make_input(cfg, (2, 64), "gpt", scope=f"lnfold_parts_in_{d}")
+    eng = Engine(0).load(cfg, params).compile((2, 64))
+    assert eng.stats()["ln_folds"] == 2 * 2 + 1
+    y = eng.run(ids)
+    ref = omodels.forward(orc, cfg, params, ids)
+    assert_close(y, ref, synth.BF16, what=f"folded decoder d={d}")
+    _argmax_check(y, ref, synth.BF16)

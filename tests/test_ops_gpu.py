@@ -186,8 +186,7 @@ def test_masked_fill(hip, orc, dt):
     mask = (np.arange(n) % 3 == 0).astype(np.int32)
     out = empty((n,), dt)
     hip.masked_fill(to_device(x, dt), to_device(mask, I32), out, n, -1e9)
-    ref = np.where(mask != 0, synth.encode(np.full(n, -1e9), dt), x)
-    assert np.array_equal(to_host(out, dt), ref)
+    assert np.array_equal(to_host(out, dt), orc.masked_fill(x, mask, -1e9, dt))
 
 
 @pytest.mark.parametrize("dt", DTS)

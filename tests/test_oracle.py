@@ -175,3 +175,208 @@ def test_transposed_operand_is_rejected(orc):
     a, b = z["a"], z["b"]
     wrong = orc.matmul(a, np.ascontiguousarray(b.reshape(b.shape[1], b.shape[0]).T), synth.F32)
     assert not np.array_equal(wrong, z["out"])
+
+
+# ---- functions outside the golden set ----------------------------------------
+# concat, masked_fill, sub/div, the build-defined ConvTranspose2d and the model
+# compositions of oracle/models.py, each checked against MuNet's compiled code
+# where it can run them and against what the mathematics fixes otherwise.
+
+needs_ref = pytest.mark.skipif(not available("reference"), reason="oracle/_ref not built (needs /root/reference)")
+
+
+@pytest.mark.parametrize("dt", [synth.F32, synth.F16, synth.BF16])
+@pytest.mark.parametrize("dim", [0, 1, 3])
+def test_concat_is_np_concatenate(orc, dt, dim):
+    rng = np.random.default_rng(200 + dim)
+    shapes = [[2, 3, 4, 5], [2, 3, 4, 5], [2, 3, 4, 5]]
+    for j, extra in enumerate((1, 4, 2)):
+        shapes[j][dim] = extra
+    xs = [synth.encode(rng.standard_normal(s), dt) for s in shapes]
+    assert np.array_equal(orc.concat(xs, dim, dt), np.concatenate(xs, axis=dim))
+
+
+@needs_ref
+@pytest.mark.parametrize("dim", [0, 1, 3])
+def test_concat_matches_compiled_reference(orc, dim):
+    """fp32 against Tensor::cat (shape.cpp:8-48, cpu_backend.hpp:416-452); the
+    reference's CPU concat refuses 16-bit storages, which the UNet's fp16 skip
+    concat therefore cannot be checked against."""
+    ref = CpuOracle("reference")
+    rng = np.random.default_rng(210 + dim)
+    a, b = rng.standard_normal((2, 3, 4, 5)).astype(np.float32), None
+    shp = [2, 3, 4, 5]
+    shp[dim] = 3
+    b = rng.standard_normal(shp).astype(np.float32)
+    assert np.array_equal(orc.concat([a, b], dim, synth.F32), ref.concat([a, b], dim, synth.F32))
+    with pytest.raises(Exception):
+        ref.concat([synth.encode(a, synth.F16), synth.encode(b, synth.F16)], dim, synth.F16)
+
+
+@needs_ref
+@pytest.mark.parametrize("dt", [synth.F32, synth.F16, synth.BF16])
+def test_sub_div_match_compiled_reference(orc, dt):
+    ref = CpuOracle("reference")
+    rng = np.random.default_rng(220 + dt)
+    enc = lambda *s: synth.encode(rng.standard_normal(s), dt)  # noqa: E731
+    for sa, sb in (((7, 33), (7, 33)), ((5, 6, 7), (7,)), ((4, 1, 9), (1, 3, 9)), ((1,), (12, 2))):
+        a, b = enc(*sa), enc(*sb)
+        bd = synth.encode(np.abs(synth.decode(b, dt)) + 0.25, dt)
+        assert np.array_equal(orc.sub(a, b, dt), ref.sub(a, b, dt)), (sa, sb)
+        assert np.array_equal(orc.div(a, bd, dt), ref.div(a, bd, dt)), (sa, sb)
+        assert np.array_equal(orc.add(a, b, dt), ref.add(a, b, dt)), (sa, sb)
+        assert np.array_equal(orc.mul(a, b, dt), ref.mul(a, b, dt)), (sa, sb)
+
+
+def test_sub_div_closed_forms(orc):
+    for dt in (synth.F32, synth.F16, synth.BF16):
+        x = synth.encode(np.random.default_rng(230).standard_normal((6, 10)) * 4, dt)
+        assert np.all(synth.decode(orc.sub(x, x, dt), dt) == 0)
+        q = synth.decode(orc.div(x, x, dt), dt)
+        assert np.all(q[synth.decode(x, dt) != 0] == 1)
+        two = synth.encode(np.full((10,), 2.0), dt)
+        assert np.array_equal(synth.decode(orc.div(x, two, dt), dt), synth.decode(x, dt) / 2)
+        # operand order matters: a - b = -(b - a), a / b != b / a
+        y = synth.encode(np.random.default_rng(231).standard_normal((6, 10)), dt)
+        assert np.array_equal(synth.decode(orc.sub(x, y, dt), dt), -synth.decode(orc.sub(y, x, dt), dt))
+
+
+@pytest.mark.parametrize("dt", [synth.F32, synth.F16, synth.BF16])
+def test_masked_fill_pinned(orc, dt):
+    """Non-zero mask entries take the value written in the storage dtype
+    (-1e9 is -inf in fp16: src/types.hpp:264-266), the rest keep their bits."""
+    n = 257
+    x = synth.encode(np.random.default_rng(240).standard_normal(n), dt)
+    mask = (np.arange(n) % 3 == 0).astype(np.int32) * np.where(np.arange(n) % 2 == 0, 1, -7).astype(np.int32)
+    out = orc.masked_fill(x, mask, -1e9, dt)
+    assert np.array_equal(out[mask == 0], x[mask == 0])
+    fill = {synth.F32: np.float32(-1e9).view(np.uint32), synth.F16: 0xFC00, synth.BF16: 0xCE6E}[dt]
+    got = out[mask != 0]
+    got = got.view(np.uint32) if dt == synth.F32 else got
+    assert np.all(got == fill)
+    if available("reference"):
+        assert np.array_equal(out, CpuOracle("reference").masked_fill(x, mask, -1e9, dt))
+    with pytest.raises(Exception):
+        orc.masked_fill(x, mask[:-1], 0.0, dt)
+
+
+def _convt_torch(x, w, b, stride, dt):
+    """Transposed convolution by torch in float64 on the CPU, rounded once."""
+    import torch
+    xf = torch.from_numpy(synth.decode(x, dt).astype(np.float64))
+    wf = torch.from_numpy(synth.decode(w, dt).astype(np.float64))
+    bf = torch.from_numpy(synth.decode(b, dt).astype(np.float64))
+    y = torch.nn.functional.conv_transpose2d(xf, wf, bf, stride=stride).numpy()
+    return synth.encode(y.astype(np.float32), dt)
+
+
+@pytest.mark.parametrize("dt", [synth.F32, synth.F16, synth.BF16])
+def test_conv_transpose2d_matches_torch(orc, dt):
+    """oracle.models.conv_transpose2d (kernel == stride) equals
+    torch.nn.functional.conv_transpose2d (weight [iC, oC, k, k]) in float64,
+    one rounding."""
+    from oracle.models import conv_transpose2d
+    rng = np.random.default_rng(250 + dt)
+    for B, iC, oC, H, W in ((2, 6, 4, 3, 5), (1, 16, 16, 4, 4), (3, 5, 7, 1, 2)):
+        x = synth.encode(rng.standard_normal((B, iC, H, W)), dt)
+        w = synth.encode(rng.standard_normal((iC, oC, 2, 2)) * 0.5, dt)
+        b = synth.encode(rng.standard_normal(oC) * 0.1, dt)
+        assert np.array_equal(conv_transpose2d(orc, x, w, b, 2, dt), _convt_torch(x, w, b, 2, dt)), (B, iC, oC)
+
+
+def test_conv_transpose2d_closed_form(orc):
+    """All-ones input and weight: every output equals iC + bias[oc]."""
+    from oracle.models import conv_transpose2d
+    for dt in (synth.F32, synth.F16, synth.BF16):
+        iC, oC = 12, 3
+        x = synth.encode(np.ones((2, iC, 3, 4)), dt)
+        w = synth.encode(np.ones((iC, oC, 2, 2)), dt)
+        b = synth.encode(np.array([0.0, 1.0, -2.0]), dt)
+        y = synth.decode(conv_transpose2d(orc, x, w, b, 2, dt), dt)
+        assert y.shape == (2, oC, 6, 8)
+        assert np.all(y == (iC + np.array([0.0, 1.0, -2.0]))[None, :, None, None])
+
+
+def test_conv_transpose2d_planted_mistakes_are_rejected(orc):
+    """The torch check catches an [ic, oc] weight swap and a flipped kernel
+    (square channel counts so both still run)."""
+    from oracle.models import conv_transpose2d
+    dt = synth.F32
+    rng = np.random.default_rng(260)
+    x = synth.encode(rng.standard_normal((2, 8, 3, 3)), dt)
+    w = synth.encode(rng.standard_normal((8, 8, 2, 2)), dt)
+    b = synth.encode(rng.standard_normal(8), dt)
+    good = _convt_torch(x, w, b, 2, dt)
+    assert np.array_equal(conv_transpose2d(orc, x, w, b, 2, dt), good)
+    swapped = np.ascontiguousarray(w.transpose(1, 0, 2, 3))
+    assert not np.array_equal(conv_transpose2d(orc, x, swapped, b, 2, dt), good)
+    flipped = np.ascontiguousarray(w[:, :, ::-1, ::-1])
+    assert not np.array_equal(conv_transpose2d(orc, x, flipped, b, 2, dt), good)
+
+
+@needs_ref
+@pytest.mark.parametrize("dt", [synth.F32, synth.F16, synth.BF16])
+def test_decoder_composition_matches_compiled_reference(orc, dt):
+    """oracle.models.decoder_forward composed from the restatement's ops equals
+    the same composition over MuNet's own ops (nn::MultiHeadAttention,
+    nn::LayerNorm, nn::GELU, nn::Linear, nn::Embedding) bit for bit."""
+    from munet_amd import models
+    from oracle import models as om
+    cfg = models.decoder_config(vocab=37, ctx=8, d_model=16, num_heads=2, num_layers=2, ffn=24,
+                                dtype={0: "float32", 1: "float16", 2: "bfloat16"}[dt])
+    params = models.init_params(cfg, "gpt", scope="compose")
+    params = {k: (synth.encode(synth.decode(v, dt) * 10, dt) if "embed" in k else v) for k, v in params.items()}
+    ids = models.make_input(cfg, (2, 8), "gpt", scope="compose_in")
+    ref = CpuOracle("reference")
+    assert np.array_equal(om.forward(orc, cfg, params, ids), om.forward(ref, cfg, params, ids))
+    blk = models.block_config(d_model=16, num_heads=2, ffn=24, causal=False,
+                              dtype={0: "float32", 1: "float16", 2: "bfloat16"}[dt])
+    bp = models.init_params(blk, "xavier", scope="compose_blk")
+    x = models.make_input(blk, (2, 5, 16), "xavier", scope="compose_blk_in")
+    assert np.array_equal(om.forward(orc, blk, bp, x), om.forward(ref, blk, bp, x))
+
+
+@needs_ref
+def test_unet_and_sequential_composition_match_compiled_reference(orc):
+    """The UNet composition (fp32: the reference's concat runs only at fp32)
+    and the MLP / CNN Sequentials over the restatement equal the same
+    compositions over MuNet's own ops."""
+    from munet_amd import models
+    from oracle import models as om
+    ref = CpuOracle("reference")
+    cfg = models.unet_config(dtype="float32", channels=(4, 8, 8), out_channels=2)
+    p = models.init_params(cfg, "he", scope="compose_unet")
+    x = models.make_input(cfg, (1, 3, 8, 8), "he", scope="compose_unet_in")
+    assert np.array_equal(om.forward(orc, cfg, p, x), om.forward(ref, cfg, p, x))
+    for cfg, shape, scheme in ((models.mlp_config((20, 16, 8, 4)), (5, 20), "mlp"),
+                               (models.cnn_config(hw=8, c1=4, c2=6, hidden=10, classes=3), (2, 3, 8, 8), "he")):
+        p = models.init_params(cfg, scheme, scope="compose_seq")
+        x = models.make_input(cfg, shape, scheme, scope="compose_seq_in")
+        assert np.array_equal(om.forward(orc, cfg, p, x), om.forward(ref, cfg, p, x))
+
+
+def test_reference_threading_mode_gives_the_same_bits():
+    """The restatement's reference-threading mode (the timed CPU baseline) and
+    its parity mode compute every output element in the same operation order:
+    golden vectors and a decoder forward agree bit for bit in both."""
+    from munet_amd import models
+    from oracle import models as om
+    o = CpuOracle("restatement")
+    cfg = models.decoder_config(vocab=50, ctx=32, d_model=32, num_heads=2, num_layers=1, ffn=64)
+    p = models.init_params(cfg, "gpt", scope="thr")
+    ids = models.make_input(cfg, (2, 32), "gpt", scope="thr_in")
+    try:
+        outs = []
+        for mode in ("parity", "reference"):
+            o.set_threading(mode)
+            for path in GOLDEN:
+                name = os.path.basename(path)[:-4]
+                z = np.load(path)
+                assert np.array_equal(_run_case(o, name, z), z["out"]), (mode, name)
+            outs.append(om.forward(o, cfg, p, ids))
+            x = synth.encode(np.random.default_rng(5).standard_normal((1500, 40)), synth.F32)
+            w = synth.encode(np.random.default_rng(6).standard_normal((40, 9)), synth.F32)
+            outs.append(o.matmul(x, w, synth.F32))  # 1500 rows: split by the reference too
+        assert np.array_equal(outs[0], outs[2]) and np.array_equal(outs[1], outs[3])
+    finally:
+        o.set_threading("parity")
