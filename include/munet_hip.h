@@ -118,6 +118,18 @@ int mh_measure_mfma_peak(int dt, int iters, double *flops_per_s, void *stream);
  * Uses the workspace when transA or !transB. */
 int mh_matmul(int dt, const void *a, const void *b, void *out, int M, int K, int N, int transA, int transB,
               void *stream);
+/* No counterpart in the reference: mh_matmul for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and results as mh_matmul,
+ * but the transposed operands it stages (A when transA, B when !transB) go to
+ * a fixed 64 MiB per-device scratch array inside the library instead of the
+ * growable workspace; a call needing more fails with a message and enqueues
+ * nothing.  No hipMalloc/hipFree on any path.  The array's device address is
+ * resolved by mh_init (or on the first call on a device).  Every call on one
+ * GPU shares that GPU's array: calls that overlap on one GPU (two streams,
+ * two threads) race and must be serialised by the caller. */
+int mh_matmul_noalloc(int dt, const void *a, const void *b, void *out, int M, int K, int N, int transA, int transB,
+                      void *stream);
 /* :255-259 batched_matmul(..., stride_a, stride_b, stride_out); stride_b = 0
  * broadcasts one right operand.  Workspace as mh_matmul. */
 int mh_batched_matmul(int dt, const void *a, const void *b, void *out, int batch, int M, int K, int N, int transA,

@@ -55,6 +55,7 @@ _SIGS = {
     "mh_argmax": [_i, _vp, _vp, _i, _i, _vp],
     "mh_measure_mfma_peak": [_i, _i, ctypes.POINTER(ctypes.c_double), _vp],
     "mh_matmul": [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
+    "mh_matmul_noalloc": [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "mh_batched_matmul": [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i64, _i64, _i64, _vp],
     "mh_linear": [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp],
     "mh_pack_linear_weight": [_i, _vp, _vp, _i, _i, _vp],

@@ -242,6 +242,11 @@ class HipBackend:
     def matmul(self, a, b, out, M, K, N, transA=False, transB=False):
         call("mh_matmul", _dt(a), _p(a), _p(b), _p(out), M, K, N, int(transA), int(transB), _stream())
 
+    def matmul_noalloc(self, a, b, out, M, K, N, transA=False, transB=False):
+        """mh_matmul_noalloc: mh_matmul staging its transposes in the
+        library's fixed per-device scratch (no device allocation)."""
+        call("mh_matmul_noalloc", _dt(a), _p(a), _p(b), _p(out), M, K, N, int(transA), int(transB), _stream())
+
     def batched_matmul(self, a, b, out, batch, M, K, N, transA, transB, stride_a, stride_b, stride_out):
         call("mh_batched_matmul", _dt(a), _p(a), _p(b), _p(out), batch, M, K, N, int(transA), int(transB),
              stride_a, stride_b, stride_out, _stream())

@@ -23,6 +23,8 @@
 
 namespace mh {
 
+void hip_check(hipError_t e, const char *what);
+
 namespace {
 thread_local std::string g_last_error;
 
@@ -33,6 +35,32 @@ struct DeviceState {
 };
 std::mutex g_mu;
 std::unordered_map<int, DeviceState> g_devices;
+
+// Fixed scratch for mh_matmul_noalloc: the operand transposes that mh_matmul
+// stages in its growable workspace go here instead, so that entry point
+// never allocates.  Each GPU the library runs on holds its own copy, at its
+// own address, until the process ends.  In host code `scratch` names only
+// the host-side shadow of the symbol; device addresses come from
+// hipGetSymbolAddress, once per device, and are kept in g_scratch.
+constexpr size_t kScratchBytes = size_t(64) << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+void *g_scratch[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// The device address of `scratch` on `device` (the current device),
+// resolved on first use and kept.
+void *scratch_ptr(int device) {
+  if (device < 0 || device >= kMaxDevices) throw Error("device ordinal out of range for the scratch table");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch[device]) {
+    void *ptr = nullptr;
+    hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!ptr) throw Error("hipGetSymbolAddress(scratch) returned no address");
+    g_scratch[device] = ptr;
+  }
+  return g_scratch[device];
+}
 
 void check_dt(int dt, bool allow_int = false) {
   if (dt < 0 || dt > 3 || (!allow_int && dt == 3)) throw Error("unsupported dtype code " + std::to_string(dt));
@@ -122,19 +150,29 @@ void un_call(int dt, int op, const void *in, void *out, size_t n, void *stream, 
   hip_check(unary(dt, op, in, out, n, c, S_(stream)), "unary");
 }
 
-// A [M,K] (or [K,M] when transA) and B [K,N] (or [N,K] when transB) per
-// batch slice -> the NT GEMM's operands, transposing into the workspace.
-void matmul_call(int dt, const void *a, const void *b, void *out, int batch, int M, int K, int N, bool transA,
-                 bool transB, long sa, long sb, long sc, void *stream) {
+// Bytes of transposed operands a matmul stages: A when transA, B when not
+// transB (the NT GEMM reads A [M,K] and B as [N,K]), each slot 256-aligned.
+size_t matmul_staging_bytes(int dt, int batch, int M, int K, int N, bool transA, bool transB, long sb) {
+  const size_t es = dt_size(dt);
+  const size_t nb_b = sb == 0 ? 1 : size_t(batch);
+  size_t need = 0;
+  if (transA) need += (size_t(batch) * M * K * es + 255) & ~size_t(255);
+  if (!transB) need += (nb_b * K * N * es + 255) & ~size_t(255);
+  return need;
+}
+
+void matmul_check(int dt, int batch, int M, int K, int N) {
   check_dt(dt);
   if (M < 0 || K < 0 || N < 0 || batch < 0) throw Error("matmul: negative size");
-  if (M == 0 || N == 0 || batch == 0) return;
+}
+
+// A [M,K] (or [K,M] when transA) and B [K,N] (or [N,K] when transB) per
+// batch slice -> the NT GEMM's operands, transposing into `ws` (at least
+// matmul_staging_bytes, 256-byte aligned).
+void matmul_staged(int dt, const void *a, const void *b, void *out, int batch, int M, int K, int N, bool transA,
+                   bool transB, long sa, long sb, long sc, char *ws, void *stream) {
   const size_t es = dt_size(dt);
   const int nb_b = sb == 0 ? 1 : batch;
-  size_t need = 0;
-  if (transA) need += size_t(batch) * M * K * es;
-  if (!transB) need += size_t(nb_b) * K * N * es;
-  char *ws = need ? static_cast<char *>(workspace(need + 512)) : nullptr;
   const void *A = a, *Bt = b;
   long lsa = sa, lsb = sb;
   if (transA) {
@@ -172,6 +210,15 @@ void matmul_call(int dt, const void *a, const void *b, void *out, int batch, int
   hip_check(gemm_nt(dt, A, Bt, M, N, K, K, K, batch, lsa, lsb, sc, ep, -1, S_(stream)), "gemm");
 }
 
+void matmul_call(int dt, const void *a, const void *b, void *out, int batch, int M, int K, int N, bool transA,
+                 bool transB, long sa, long sb, long sc, void *stream) {
+  matmul_check(dt, batch, M, K, N);
+  if (M == 0 || N == 0 || batch == 0) return;
+  const size_t need = matmul_staging_bytes(dt, batch, M, K, N, transA, transB, sb);
+  char *ws = need ? static_cast<char *>(workspace(need)) : nullptr;
+  matmul_staged(dt, a, b, out, batch, M, K, N, transA, transB, sa, sb, sc, ws, stream);
+}
+
 }  // namespace
 
 extern "C" {
@@ -191,6 +238,7 @@ int mh_init(int device) {
   MH_TRY({
     hip_check(hipSetDevice(device), "hipSetDevice");
     (void)state();
+    (void)scratch_ptr(device);
   })
 }
 
@@ -347,6 +395,24 @@ int mh_measure_mfma_peak(int dt, int iters, double *flops_per_s, void *stream) {
 int mh_matmul(int dt, const void *a, const void *b, void *out, int M, int K, int N, int transA, int transB,
               void *stream) {
   MH_TRY(matmul_call(dt, a, b, out, 1, M, K, N, transA != 0, transB != 0, 0, 0, 0, stream))
+}
+int mh_matmul_noalloc(int dt, const void *a, const void *b, void *out, int M, int K, int N, int transA, int transB,
+                      void *stream) {
+  MH_TRY({
+    matmul_check(dt, 1, M, K, N);
+    if (M == 0 || N == 0) return 0;
+    const size_t need = matmul_staging_bytes(dt, 1, M, K, N, transA != 0, transB != 0, 0);
+    if (need > kScratchBytes)
+      throw Error("matmul_noalloc: the transposed operands need " + std::to_string(need) + " bytes of scratch, " +
+                  "more than its fixed " + std::to_string(kScratchBytes) + " bytes");
+    char *ws = nullptr;
+    if (need) {
+      int dev = 0;
+      hip_check(hipGetDevice(&dev), "hipGetDevice");
+      ws = static_cast<char *>(scratch_ptr(dev));
+    }
+    matmul_staged(dt, a, b, out, 1, M, K, N, transA != 0, transB != 0, 0, 0, 0, ws, stream);
+  })
 }
 int mh_batched_matmul(int dt, const void *a, const void *b, void *out, int batch, int M, int K, int N, int transA,
                       int transB, int64_t sa, int64_t sb, int64_t sc, void *stream) {
