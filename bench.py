@@ -1,30 +1,38 @@
-"""Benchmark: 12-layer GPT decoder prefill on the MI355X HIP engine.
+"""Benchmark: 12-layer GPT decoder prefill on the MI355X HIP engine, plus the
+other BASELINE workloads.
 
-BASELINE.json metric "decoder inference tokens/s at 1 GPU" on configs[4]
-(GPT-style decoder bf16: 12 layers, d_model 768, 12 heads, FFN 3072 GELU,
-vocab 32000, causal, batch 4, seq 1024, full prefill forward to logits),
-with seeded uniform token ids and N(0, 0.02) weights.
+Headline (BASELINE.json metric "decoder inference tokens/s at 1 GPU",
+configs[4]): GPT-style decoder bf16, 12 layers, d_model 768, 12 heads, FFN
+3072 GELU, vocab 32000, causal, batch 4, seq 1024, full prefill forward to
+logits, with seeded uniform token ids and N(0, 0.02) weights.  One step = one
+compiled forward (one hipGraph launch) over the resident [4, 1024] ids already
+in HBM.  W untimed warm-up steps, then exactly K timed steps bracketed by
+torch.cuda.synchronize() on both sides.
 
-One step = one compiled forward (one hipGraph launch) over the resident
-[4, 1024] ids already in HBM.  W untimed warm-up steps, then exactly K timed
-steps bracketed by torch.cuda.synchronize() on both sides.
+Roofline: every op's cost inside the forward is measured with HIP events on
+the engine stream as differences of prefix-graph times (for each prefix
+ops[0..i] of the forward, 20 back-to-back replays between two events; op i's
+time is T(i) - T(i-1): its duration where the forward runs it, with the
+forward's caches, mh_engine_forward_op_times; the kernel trace of the same
+command shows the same per-dispatch durations).  The kernel with the largest
+cost per forward is the dominant one, and its algorithmic work per launch
+(GEMM 2*M*N*K FLOPs, causal attention 4*B*H*T^2*hd/2, LayerNorm unique bytes)
+over its mean in-forward launch time is `achieved`, against the datasheet
+peak and against the measured ones (the register-only MFMA loop of
+mh_measure_mfma_peak; a read-only stream over 2 GiB, mh_measure_hbm_read; a
+1 GiB device copy).  Every op is also timed alone from its own graph (warm
+caches, "kernels_isolated").
 
-Roofline: every op of the compiled forward is also timed on its own with
-HIP events on the engine stream it runs on (mh_engine_op_times: 20 launches
-of the op captured in one graph and replayed between events, so host launch
-cost is excluded; the rocprofv3 kernel trace of the same command shows the
-same per-dispatch durations); the kernel with the largest time per forward
-is reported against the bf16 MFMA peak (GEMM / attention: algorithmic
-2*M*N*K FLOPs) or the HBM peak (LayerNorm: unique bytes), and against the measured peaks (the
-register-only MFMA loop of mh_measure_mfma_peak; a 1 GiB device copy).
-Inside the
-forward the kernels run with colder caches: "kernels_in_forward_avg_us"
-(mh_engine_forward_op_times: differences of prefix-graph times, each over 20
-replays; an op's figure also carries what it costs the ops after it, such as
-the write-back of its output, and the first op carries the graph launch).
-CPU baseline: the C++ restatement
-of MuNet's CPU backend (oracle/, "port") on a bounded sample of the same
-forward, timed on this host.
+CPU baseline: the C++ restatement of MuNet's CPU backend (oracle/, "port")
+in its reference-threading mode (MuNet's own split: CPUBackend::parallel_for
+inline below 1024 iterations, the fp16/bf16 fallbacks, LayerNorm and gathers
+serial), on a bounded sample of the same forward, on this host.  Where
+oracle/_ref (MuNet's CPU sources compiled by oracle/Makefile) is present, the
+same bf16 Linear is timed in it and in the port ("reference_check").
+
+"configs": BASELINE configs[0..3] (MLP, CNN, encoder block bf16 / fp16,
+UNet) at their full sizes: forward time, samples/s, MFMA / HBM fractions of
+their products and norms, and the CPU baseline per config.
 """
 from __future__ import annotations
 
@@ -39,7 +47,8 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-PEAK_BF16 = 2.5e15      # dense bf16 MFMA, FLOP/s
+PEAK_BF16 = 2.5e15      # dense bf16 / fp16 MFMA, FLOP/s
+PEAK_F32 = 157.3e12     # fp32 MFMA, FLOP/s
 PEAK_HBM = 8.0e12       # HBM3E, B/s
 
 CFG = dict(vocab=32000, ctx=1024, d_model=768, num_heads=12, num_layers=12, ffn=3072, dtype="bfloat16")
@@ -72,21 +81,16 @@ def op_category(op):
     return name
 
 
-def kernel_table(eng, reps=20, in_forward=True):
-    """Per-kernel timing of the compiled forward's own ops (the LayerNorm-
-    folded consumers and the statistics-producing residual GEMMs as the
-    forward runs them).  in_forward: mh_engine_forward_op_times, differences
-    of prefix-graph times, each over `reps` replays (the forward's own caches
-    and transitions); otherwise mh_engine_op_times, each op replayed `reps`
-    times from one graph (warm caches).  Rows: one per kernel
-    category with the mean time per launch, launches per forward and
-    algorithmic work per launch."""
+def categorise(ops):
+    """Rows per kernel category: mean time per launch, launches per forward,
+    algorithmic work per launch, the op names."""
     cats = {}
-    for op in (eng.forward_op_times(reps) if in_forward else eng.op_times(reps)):
-        c = cats.setdefault(op_category(op), dict(ts=[], flops=op["flops"], bytes=op["bytes"], first=op["name"]))
+    for op in ops:
+        c = cats.setdefault(op_category(op), dict(ts=[], flops=op["flops"], bytes=op["bytes"], names=[]))
         c["ts"].append(op["us"] * 1e-6)
-    return [dict(name=n, t=sum(c["ts"]) / len(c["ts"]), count=len(c["ts"]), flops=c["flops"], bytes=c["bytes"],
-                 op=c["first"]) for n, c in cats.items()]
+        c["names"].append(op["name"])
+    return {n: dict(name=n, t=sum(c["ts"]) / len(c["ts"]), count=len(c["ts"]), flops=c["flops"], bytes=c["bytes"],
+                    names=c["names"]) for n, c in cats.items()}
 
 
 COPY_BYTES = 256 << 20  # the calibration copy of --probe
@@ -97,7 +101,7 @@ def probe(eng, torch, name):
     the first op of category `name` (mh_engine_op_times restricted to that
     op), then one device-to-device copy of COPY_BYTES (the counter
     calibration: it reads and writes exactly that many bytes)."""
-    op = next(r["op"] for r in kernel_table(eng, 1, in_forward=False) if r["name"] == name)
+    op = categorise(eng.op_times(1))[name]["names"][0]
     torch.cuda.synchronize()
     eng.op_times(5, only=op)
     torch.cuda.synchronize()
@@ -121,31 +125,177 @@ def measured_traffic(name):
     return None
 
 
-def cpu_baseline():
-    """Oracle restatement on a bounded sample: 1 of the 12 decoder layers plus
-    final LayerNorm + LM head for 1 of the 4 sequences (1024 tokens), the
-    forward time extrapolated to 12 layers."""
+def timed_launches(eng, torch, steps, warmup):
+    for _ in range(warmup):
+        eng.launch()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.launch()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+# ---- CPU baseline ------------------------------------------------------------
+
+def _timed(fn):
+    t0 = time.perf_counter()
+    out = fn()
+    return out, time.perf_counter() - t0
+
+
+def reference_check():
+    """One bf16 Linear (16 x 768 -> 3072) in MuNet's own compiled CPU code
+    (oracle/_ref) and in the port's reference-threading mode, when oracle/_ref
+    is present: the port's bf16 fallback is leaner than MuNet's per-element
+    ScalarValue reads, so its times understate MuNet's."""
+    from munet_amd import synth
+    from oracle import CpuOracle, available
+    if not available("reference"):
+        return None
+    ref, port = CpuOracle("reference"), CpuOracle("restatement")
+    port.set_threading("reference")
+    rng = np.random.default_rng(7)
+    dt = synth.BF16
+    x = synth.encode(rng.standard_normal((16, 768)), dt)
+    w = synth.encode(rng.standard_normal((768, 3072)) * 0.02, dt)
+    b = synth.encode(np.zeros(3072), dt)
+    y_ref, t_ref = _timed(lambda: ref.linear(x, w, b, dt))
+    y_port, t_port = _timed(lambda: port.linear(x, w, b, dt))
+    port.set_threading("parity")
+    return dict(op="bf16 Linear 16x768 -> 3072", munet_s=round(t_ref, 4), port_s=round(t_port, 4),
+                munet_over_port=round(t_ref / t_port, 3), same_bits=bool(np.array_equal(y_ref, y_port)))
+
+
+def cpu_baseline_gpt(rows=32):
+    """Port in reference-threading mode on one 1024-token sequence: the row-
+    wise ops of one decoder layer (embedding, LayerNorms, residual adds) on all
+    1024 rows, its Linears and GELU on `rows` rows scaled to 1024, attention
+    (per (b, h) block: a lower bound on MuNet's dense [B*H*T]^2 path) on all
+    rows; the layer time x 12 plus ln_f and the LM head (on `rows` rows,
+    scaled).  In MuNet every one of these bf16 ops is a serial fallback."""
     from munet_amd import models, synth
     from oracle import CpuOracle
     from oracle import models as om
     orc = CpuOracle("restatement")
     cfg = models.decoder_config(**{**CFG, "num_layers": 1})
-    params = models.init_params(cfg, "gpt", scope="cpu")
+    p = models.init_params(cfg, "gpt", scope="cpu")
     ids = models.make_input(cfg, (1, T), "gpt", scope="cpu_in")
-    dt = synth.BF16
-    t0 = time.perf_counter()
-    x = om.decoder_embed(orc, cfg, params, ids)
-    t1 = time.perf_counter()
-    x = om.block_forward(orc, cfg, params, x, "blocks.0.", True)
-    t2 = time.perf_counter()
-    x = orc.layer_norm(x, params["ln_f.weight"], params["ln_f.bias"], dt)
-    orc.linear(x, params["head.weight"], params["head.bias"], dt)
-    t3 = time.perf_counter()
-    fwd = (t1 - t0) + CFG["num_layers"] * (t2 - t1) + (t3 - t2)
-    return dict(value=T / fwd, unit="tokens/s", cores=orc.threads(), kind="port",
-                sample=(f"1 of 12 decoder layers + ln_f + LM head on 1 sequence x {T} tokens "
-                        f"({t3 - t0:.1f} s measured: embed {t1 - t0:.2f}s, layer {t2 - t1:.2f}s, "
-                        f"head {t3 - t2:.2f}s), extrapolated to 12 layers"))
+    dt, d, H, pre = synth.BF16, CFG["d_model"], CFG["num_heads"], "blocks.0."
+    scale = T / rows
+    lin = lambda x, n: orc.linear(x, p[n + ".weight"], p[n + ".bias"], dt)  # noqa: E731
+    tm = {}
+    orc.set_threading("reference")
+    try:
+        x, tm["embed"] = _timed(lambda: om.decoder_embed(orc, cfg, p, ids).reshape(T, d))
+        h, tm["ln1"] = _timed(lambda: orc.layer_norm(x, p[pre + "ln1.weight"], p[pre + "ln1.bias"], dt))
+        tm["qkv"] = sum(_timed(lambda n=n: lin(h[:rows], pre + "attn." + n))[1] for n in ("q_proj", "k_proj", "v_proj"))
+        orc.set_threading("parity")  # full q / k / v for the attention, untimed
+        q, k, v = (lin(h, pre + "attn." + n) for n in ("q_proj", "k_proj", "v_proj"))
+        orc.set_threading("reference")
+        ctx, tm["attention"] = _timed(lambda: orc.mha_core(q, k, v, 1, T, H, True, dt))
+        a, tm["out_proj"] = _timed(lambda: lin(ctx[:rows], pre + "attn.out_proj"))
+        x2, tm["residual1"] = _timed(lambda: orc.add(x, np.resize(a, x.shape), dt))
+        h2, tm["ln2"] = _timed(lambda: orc.layer_norm(x2, p[pre + "ln2.weight"], p[pre + "ln2.bias"], dt))
+        f, tm["ffn_up"] = _timed(lambda: lin(h2[:rows], pre + "ff.0"))
+        g, tm["gelu"] = _timed(lambda: orc.gelu(f, dt))
+        f2, tm["ffn_down"] = _timed(lambda: lin(g, pre + "ff.2"))
+        _, tm["residual2"] = _timed(lambda: orc.add(x2, np.resize(f2, x2.shape), dt))
+        hf, tm["ln_f"] = _timed(lambda: orc.layer_norm(x2, p["ln_f.weight"], p["ln_f.bias"], dt))
+        _, tm["head"] = _timed(lambda: lin(hf[:rows], "head"))
+    finally:
+        orc.set_threading("parity")
+    sampled = ("qkv", "out_proj", "ffn_up", "gelu", "ffn_down", "head")
+    full = {k: v * (scale if k in sampled else 1.0) for k, v in tm.items()}
+    layer = sum(v for k, v in full.items() if k not in ("embed", "ln_f", "head"))
+    fwd = full["embed"] + CFG["num_layers"] * layer + full["ln_f"] + full["head"]
+    measured = sum(tm.values())
+    return dict(value=T / fwd, unit="tokens/s", cores=1, kind="port",
+                threading="reference (every bf16 op of this model is a serial fallback in MuNet)",
+                host_threads=orc.threads(), cpu_model=cpu_model(),
+                sample=(f"one 1024-token sequence through one decoder layer: Linears, GELU and the LM head on "
+                        f"{rows} rows scaled x{scale:.0f}, row-wise ops and per-block attention on all rows "
+                        f"({measured:.1f} s measured: layer {layer:.2f} s, head {full['head']:.2f} s as extrapolated), "
+                        f"extrapolated to 12 layers; per-block attention is a lower bound on MuNet's dense "
+                        f"[B*H*T]^2 attention"),
+                seconds_per_forward_of_one_sequence=fwd)
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_port_forward(cfg, params, x, threading):
+    """Whole-forward time of the port on `x` (a bounded sample) in the given
+    threading mode."""
+    from oracle import CpuOracle
+    from oracle import models as om
+    orc = CpuOracle("restatement")
+    orc.set_threading(threading)
+    try:
+        _, t = _timed(lambda: om.forward(orc, cfg, params, x))
+    finally:
+        orc.set_threading("parity")
+    return t
+
+
+# ---- the other BASELINE configs ---------------------------------------------
+
+CONFIG_ROWS = [
+    # key, BASELINE index, sample batch for the CPU baseline
+    ("mlp", 0, None),
+    ("cnn", 1, None),
+    ("encoder_bf16", 2, 1),
+    ("encoder_fp16", 2, 1),
+    ("unet", 3, 1),
+]
+
+
+def config_line(torch, key, idx, cpu_batch, steps, warmup, with_cpu):
+    from munet_amd import models, synth
+    from munet_amd.engine import Engine
+    w = models.baseline_workloads()[key]
+    cfg, shape, init = w["config"], w["input_shape"], w["init"]
+    dt = synth.DTYPE_CODES[cfg.get("dtype", "float32")]
+    params = models.init_params(cfg, init, scope=f"bench_{key}")
+    x = models.make_input(cfg, shape, init, scope=f"bench_{key}_in")
+    eng = Engine(0).load(cfg, params).compile(shape)
+    eng.run(x)
+    s = timed_launches(eng, torch, steps, warmup)
+    ops = eng.op_times(10)
+    peak = PEAK_F32 if dt == synth.F32 else PEAK_BF16
+    mm = [o for o in ops if o["flops"]]
+    mm_t = sum(o["us"] for o in mm) * 1e-6
+    mm_f = sum(o["flops"] for o in mm)
+    ln = [o for o in ops if o["kind"] == "layer_norm"]
+    batch = shape[0]
+    row = dict(baseline_config=idx, dtype=synth.DTYPE_NAMES[dt], input_shape=list(shape), ms=s * 1e3,
+               samples_per_s=batch / s,
+               mfma_frac=(mm_f / mm_t / peak) if mm_t else None,
+               mfma_tflops=(mm_f / mm_t / 1e12) if mm_t else None,
+               mfma_share_of_forward=mm_t / s,
+               peak_tflops=peak / 1e12,
+               layernorm_hbm_frac=(sum(o["bytes"] for o in ln) / (sum(o["us"] for o in ln) * 1e-6) / PEAK_HBM)
+               if ln else None,
+               ops=len(ops))
+    if key.startswith("encoder"):
+        row["tokens_per_s"] = shape[0] * shape[1] / s
+    if with_cpu:
+        n = cpu_batch or batch
+        xs = np.ascontiguousarray(x[:n])
+        t_ref = cpu_port_forward(cfg, params, xs, "reference")
+        row["cpu_baseline"] = dict(value=n / t_ref, unit="samples/s", kind="port", threading="reference",
+                                   sample=f"batch {n} of {batch}" + (" (samples are independent)" if n < batch else ""),
+                                   seconds=t_ref)
+        row["speedup_vs_cpu"] = row["samples_per_s"] / (n / t_ref)
+    eng.close()
+    return row
 
 
 def main():
@@ -154,6 +304,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip BASELINE configs 0-3")
     ap.add_argument("--probe", default=None, help="run one kernel of the forward for rocprofv3 --pmc and exit")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -161,10 +312,12 @@ def main():
               "the single-GPU design and how the path would shard are in DESIGN.md", file=sys.stderr)
         sys.exit(2)
 
-    import torch
     import ctypes
 
+    import torch
+
     from munet_amd import _lib, models
+    from munet_amd.backend import HipBackend
     from munet_amd.engine import Engine
 
     cfg = models.decoder_config(**CFG)
@@ -180,16 +333,9 @@ def main():
         probe(eng, torch, args.probe)
         return
 
-    for _ in range(args.warmup):
-        eng.launch()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        eng.launch()
-    torch.cuda.synchronize()
-    dt_s = time.perf_counter() - t0
-    ms = dt_s / args.steps * 1e3
-    tokens_s = B * T * args.steps / dt_s
+    s = timed_launches(eng, torch, args.steps, args.warmup)
+    ms = s * 1e3
+    tokens_s = B * T / s
     log(f"bench: {ms:.3f} ms/forward, {tokens_s:,.0f} tokens/s")
     # the timed forwards reran the resident input: no device error (token id
     # out of range) and the same logits as the first forward, bit for bit
@@ -200,11 +346,14 @@ def main():
     if not np.array_equal(again.view(np.uint16), logits.view(np.uint16)):
         raise SystemExit("bench: repeated forwards changed the logits")
 
-    # measured peaks beside the datasheet ones: the MFMA loop of peak.hip,
-    # and a 1 GiB device-to-device copy (reads and writes 2 GiB)
-    from munet_amd.backend import HipBackend
-    peak_mfma = HipBackend(0).measure_mfma_peak(2, 16000)
-    src = torch.empty(1 << 29, device="cuda", dtype=torch.float16)
+    # measured peaks beside the datasheet ones: the MFMA loop of peak.hip, a
+    # read-only stream over 2 GiB, and a 1 GiB device-to-device copy
+    hb = HipBackend(0)
+    peak_mfma = hb.measure_mfma_peak(2, 16000)
+    buf = torch.empty(1 << 30, device="cuda", dtype=torch.float16)
+    buf.fill_(1.0)
+    peak_read = hb.measure_hbm_read(buf, 5)
+    src = buf[: 1 << 29]
     dst = torch.empty_like(src)
     dst.copy_(src)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -213,38 +362,53 @@ def main():
         dst.copy_(src)
     e1.record()
     torch.cuda.synchronize()
-    peak_hbm = 5 * 2.0 * src.numel() * 2 / (e0.elapsed_time(e1) * 1e-3)
-    del src, dst
+    peak_copy = 5 * 2.0 * src.numel() * 2 / (e0.elapsed_time(e1) * 1e-3)
+    del src, dst, buf
 
-    rows = kernel_table(eng, in_forward=False)
-    # in-forward times are differences of prefix-graph times: a few us of
-    # replay-to-replay noise each, so only the per-layer categories (means over
-    # 12 ops) and the LM head (hundreds of us) are reported
-    fwd = {r["name"]: round(r["t"] * 1e6, 2) for r in kernel_table(eng, in_forward=True)
-           if r["count"] >= 12 or r["name"] == "lm_head"}
-    for r in rows:
+    # per-op cost inside the forward (prefix-graph differences) picks the
+    # dominant kernel and gives its mean launch time
+    fwd_rows = categorise(eng.forward_op_times(20))
+    for r in fwd_rows.values():
         r["per_fwd"] = r["t"] * r["count"]
-    dom = max(rows, key=lambda r: r["per_fwd"])
+    dom = max(fwd_rows.values(), key=lambda r: r["per_fwd"])
+    t_dom = dom["t"]
     if dom["flops"]:
-        ach = dom["flops"] / dom["t"]
+        ach = dom["flops"] / t_dom
         roof = dict(bound="mfma", achieved=ach / 1e12, peak=PEAK_BF16 / 1e12, unit="TFLOP/s", frac=ach / PEAK_BF16,
                     peak_measured=peak_mfma / 1e12, frac_of_measured=ach / peak_mfma)
     else:
-        ach = dom["bytes"] / dom["t"]
+        ach = dom["bytes"] / t_dom
         roof = dict(bound="hbm", achieved=ach / 1e9, peak=PEAK_HBM / 1e9, unit="GB/s", frac=ach / PEAK_HBM,
-                    peak_measured=peak_hbm / 1e9, frac_of_measured=ach / peak_hbm)
-    roof.update(kernel=dom["name"], avg_us=dom["t"] * 1e6, traffic=measured_traffic(dom["name"]))
-    gemm = [r for r in rows if r["flops"] and r["name"] != "attention_causal"]
-    gemm_frac = sum(r["flops"] * r["count"] for r in gemm) / sum(r["per_fwd"] for r in gemm) / PEAK_BF16
-    ln = next(r for r in rows if r["name"] == "layer_norm")
-    kernels = {r["name"]: dict(avg_us=round(r["t"] * 1e6, 2), per_forward=r["count"],
-                               tflops=round(r["flops"] / r["t"] / 1e12, 1) if r["flops"] else None,
-                               gbs=round(r["bytes"] / r["t"] / 1e9, 1) if r["bytes"] else None) for r in rows}
+                    peak_measured=peak_read / 1e9, frac_of_measured=ach / peak_read)
+    roof.update(kernel=dom["name"], avg_us=t_dom * 1e6, launches_per_forward=dom["count"],
+                work_per_launch=dom["flops"] or dom["bytes"], timing="in-forward: differences of prefix-graph times, HIP events on the engine stream",
+                share_of_forward=dom["per_fwd"] / s, traffic=measured_traffic(dom["name"]))
+
+    iso = categorise(eng.op_times(20))
+    kernels = {n: dict(avg_us=round(r["t"] * 1e6, 2), per_forward=r["count"],
+                       tflops=round(r["flops"] / r["t"] / 1e12, 1) if r["flops"] else None,
+                       gbs=round(r["bytes"] / r["t"] / 1e9, 1) if r["bytes"] else None) for n, r in iso.items()}
+    in_fwd = {n: dict(avg_us=round(r["t"] * 1e6, 2), per_forward=r["count"], us_per_forward=round(r["per_fwd"] * 1e6, 1),
+                      tflops=round(r["flops"] / r["t"] / 1e12, 1) if r["flops"] and r["t"] > 0 else None)
+              for n, r in fwd_rows.items()}
+    gemm_f = [r for r in fwd_rows.values() if r["flops"] and r["name"] != "attention_causal"]
+    gemm_frac_fwd = sum(r["flops"] * r["count"] for r in gemm_f) / sum(r["per_fwd"] for r in gemm_f) / PEAK_BF16
+    gemm_i = [r for r in iso.values() if r["flops"] and r["name"] != "attention_causal"]
+    gemm_frac_iso = sum(r["flops"] * r["count"] for r in gemm_i) / sum(r["t"] * r["count"] for r in gemm_i) / PEAK_BF16
+    ln = iso["layer_norm"]
 
     cpu = None
     if not args.no_cpu_baseline:
         log("bench: timing the CPU baseline sample")
-        cpu = cpu_baseline()
+        cpu = cpu_baseline_gpt()
+        cpu["reference_check"] = reference_check()
+        cpu["speedup_vs_cpu"] = tokens_s / cpu["value"]
+    configs = None
+    if not args.no_configs:
+        configs = {}
+        for key, idx, cpu_batch in CONFIG_ROWS:
+            log(f"bench: config {key}")
+            configs[key] = config_line(torch, key, idx, cpu_batch, args.steps, args.warmup, not args.no_cpu_baseline)
     line = {
         "metric": "decoder inference tokens/s at 1 GPU",
         "value": tokens_s,
@@ -262,12 +426,16 @@ def main():
                    "heads": 12, "ffn": 3072, "vocab": 32000, "batch": B, "seq_len": T, "causal": True,
                    "tokens_per_step": B * T},
         "roofline": roof,
-        "gemm_mfma_frac": gemm_frac,
+        "gemm_mfma_frac": gemm_frac_fwd,
+        "gemm_mfma_frac_isolated": gemm_frac_iso,
         "layernorm_hbm_frac": (ln["bytes"] / ln["t"]) / PEAK_HBM,
-        "measured_peaks": {"mfma_bf16_tflops": peak_mfma / 1e12, "hbm_copy_gbs": peak_hbm / 1e9},
-        "kernels": kernels,
-        "kernels_in_forward_avg_us": fwd,
+        "layernorm_frac_of_measured_read": (ln["bytes"] / ln["t"]) / peak_read,
+        "measured_peaks": {"mfma_bf16_tflops": peak_mfma / 1e12, "hbm_read_gbs": peak_read / 1e9,
+                           "hbm_copy_gbs": peak_copy / 1e9},
+        "kernels_in_forward": in_fwd,
+        "kernels_isolated": kernels,
         "cpu_baseline": cpu,
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
 

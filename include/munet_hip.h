@@ -112,6 +112,13 @@ int mh_argmax(int dt, const void *x, int32_t *out, int rows, int cols, void *str
  * call synchronises it).  No counterpart in the reference: the measured peak
  * that the roofline reports beside the datasheet one. */
 int mh_measure_mfma_peak(int dt, int iters, double *flops_per_s, void *stream);
+/* Measured HBM read rate in bytes/s: a full grid streams the caller's device
+ * buffer `buf` (16-byte aligned, `bytes` >= 1 MiB; make it several times the
+ * 256 MB last-level cache) `reps` times with 16-byte loads, timed with HIP
+ * events on `stream` (the call synchronises it).  No counterpart in the
+ * reference: the measured read peak the roofline reports beside the
+ * datasheet HBM figure. */
+int mh_measure_hbm_read(const void *buf, size_t bytes, int reps, double *bytes_per_s, void *stream);
 
 /* ---- BackendBlasCapability (src/core/backend.hpp:250-260) ---------------- */
 /* :253-254 matmul(a, b, out, M, K, N, transA, transB) on raw row-major storage.

@@ -54,6 +54,7 @@ _SIGS = {
     "mh_convert": [_i, _vp, _i, _vp, _sz, _vp],
     "mh_argmax": [_i, _vp, _vp, _i, _i, _vp],
     "mh_measure_mfma_peak": [_i, _i, ctypes.POINTER(ctypes.c_double), _vp],
+    "mh_measure_hbm_read": [_vp, _sz, _i, ctypes.POINTER(ctypes.c_double), _vp],
     "mh_matmul": [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "mh_matmul_noalloc": [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "mh_batched_matmul": [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i64, _i64, _i64, _vp],

@@ -238,6 +238,13 @@ class HipBackend:
         call("mh_measure_mfma_peak", dt, iters, ctypes.byref(v), _stream())
         return v.value
 
+    def measure_hbm_read(self, buf, reps=5) -> float:
+        """Measured HBM read rate in bytes/s over the device tensor ``buf``
+        (mh_measure_hbm_read)."""
+        v = ctypes.c_double()
+        call("mh_measure_hbm_read", _p(buf), buf.numel() * buf.element_size(), reps, ctypes.byref(v), _stream())
+        return v.value
+
     # ---- blas (backend.hpp:250-260) ----------------------------------------
     def matmul(self, a, b, out, M, K, N, transA=False, transB=False):
         call("mh_matmul", _dt(a), _p(a), _p(b), _p(out), M, K, N, int(transA), int(transB), _stream())

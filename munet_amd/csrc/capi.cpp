@@ -390,6 +390,13 @@ int mh_measure_mfma_peak(int dt, int iters, double *flops_per_s, void *stream) {
     hip_check(mfma_peak(dt, iters, flops_per_s, S_(stream)), "measure_mfma_peak");
   })
 }
+int mh_measure_hbm_read(const void *buf, size_t bytes, int reps, double *bytes_per_s, void *stream) {
+  MH_TRY({
+    if (!buf || bytes < (size_t(1) << 20) || reps <= 0 || !bytes_per_s || (uintptr_t)buf % 16)
+      throw Error("measure_hbm_read: needs a 16-byte aligned buffer of at least 1 MiB, reps > 0 and bytes_per_s");
+    hip_check(hbm_read_rate(buf, bytes, reps, bytes_per_s, S_(stream)), "measure_hbm_read");
+  })
+}
 
 // ---- blas ------------------------------------------------------------------
 int mh_matmul(int dt, const void *a, const void *b, void *out, int M, int K, int N, int transA, int transB,

@@ -891,7 +891,8 @@ struct EngineImpl {
   }
 
   // Algorithmic work of one op: FLOPs of its products (GEMM 2 M N K,
-  // attention 4 B H T^2 hd, halved when causal) and the unique bytes a
+  // attention 4 B H T^2 hd, halved when causal, convolution 2 (B oH oW) oC
+  // (k k iC), transposed convolution 2 (B iH iW k k) oC iC) and the unique bytes a
   // memory-bound op reads and writes (LayerNorm 2 M d s + 2 d s, embedding
   // 3 M d s + 4 M).
   void op_work(const Op &o, double &flops, double &bytes) const {
@@ -901,6 +902,13 @@ struct EngineImpl {
     case OP_GEMM: flops = 2.0 * o.a[0] * o.a[1] * o.a[2]; break;
     case OP_QKV: flops = 2.0 * o.a[0] * o.a[1] * 3.0 * o.a[2] * o.a[2]; break;
     case OP_ATTN: flops = 4.0 * o.a[0] * o.a[1] * double(o.a[2]) * o.a[2] * o.a[3] * (o.a[4] ? 0.5 : 1.0); break;
+    case OP_CONV: {  // 2 (B oH oW) oC (k k iC)
+      const double oH = double((o.a[2] + 2 * o.a[7] - o.a[5]) / o.a[6] + 1),
+                   oW = double((o.a[3] + 2 * o.a[7] - o.a[5]) / o.a[6] + 1);
+      flops = 2.0 * o.a[0] * oH * oW * o.a[4] * double(o.a[5]) * o.a[5] * o.a[1];
+      break;
+    }
+    case OP_CONVT: flops = 2.0 * o.a[0] * o.a[2] * o.a[3] * double(o.a[5]) * o.a[5] * o.a[4] * o.a[1]; break;
     case OP_LN: bytes = (2.0 * o.a[0] * o.a[1] + 2.0 * o.a[1]) * es; break;
     case OP_EMBED: case OP_EMBED_POS: bytes = 3.0 * o.a[0] * o.a[2] * es + 4.0 * o.a[0]; break;
     default: break;
@@ -1489,5 +1497,6 @@ int mh_engine_op_times(mh_engine *e, int reps, const char *only, char *buf, size
 int mh_engine_forward_op_times(mh_engine *e, int reps, char *buf, size_t len) {
   ENG_TRY(put_str(e->impl.forward_op_times_json(reps), buf, len))
 }
+
 
 }  // extern "C"

@@ -399,6 +399,42 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
     }
   }
 
+  // Non-temporal output (an output no kernel reads, such as the logits) in
+  // whole lines: each wave rounds its tile into LDS as rows of WTN values and
+  // writes the rows back with 16-byte non-temporal stores, LPR lanes per row,
+  // so every store instruction covers whole 128-byte lines.  Per-fragment
+  // 8-byte non-temporal stores write 32-byte pieces of lines that bypass the
+  // cache's write combining: measured on the vocabulary head, the memory side
+  // then wrote 2.25 times the output's bytes.  Interior tiles of an aligned
+  // row-major output only (the caller checks).
+  static constexpr int NT_LPR = WTN * 2 / 16;  // lanes per staged row
+  static constexpr bool NT_ROWS = WTN % 8 == 0 && NT_LPR <= 64 && 64 % NT_LPR == 0 &&
+                                  WTM * (WTN * 2 + 16) * G::NW <= 2 * (BM + BN) * 128;
+  __device__ __forceinline__ void store_nt_rows(const EpiArgs &ep, f32x4 (&acc)[FM][FN], long off, u32x4 *lds,
+                                                int wave, int lane) {
+    constexpr int RB = WTN * 2 + 16;  // bytes per staged row (16-byte pad against bank conflicts)
+    constexpr int RPI = 64 / NT_LPR;  // rows per store instruction
+    char *stage = reinterpret_cast<char *>(lds) + wave * WTM * RB;
+    __syncthreads();  // every wave has read its last fragments from the K loop's LDS
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+        const uint2 pk = epi_fast_bf16_fixed<KT_::BIAS, ACT_NONE, false>(v, bq[j], make_uint2(0, 0), ep.gelu_c);
+        *reinterpret_cast<uint2 *>(stage + (i * 16 + g.li) * RB + (j * 16 + g.lg * 4) * 2) = pk;
+      }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
+    __builtin_amdgcn_wave_barrier();
+    const int rr = lane / NT_LPR, cc = lane % NT_LPR;
+    uint16_t *base = static_cast<uint16_t *>(ep.out) + off + long(m0 + g.wm * WTM) * ep.ldc + n0 + g.wn * WTN + cc * 8;
+#pragma unroll
+    for (int r = rr; r < WTM; r += RPI) {
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(stage + r * RB + cc * 16);
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(base + long(r) * ep.ldc));
+    }
+  }
+
   // lds: the kernel's LDS (idle by now), at least 2 * (BM + BN) * 128 bytes;
   // lnrow, lncs, lnbw: the folded LayerNorm's row and column terms
   // (ln_finish)
@@ -452,6 +488,13 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
     }
     // Interior tiles (the common case) store every fragment unconditionally.
     const bool interior = m0 + BM <= M && n0 + BN <= N;
+    if constexpr (KT_::NT && NT_ROWS) {
+      if (interior && ep.mode == EPI_ROWMAJOR && (ep.ldc & 7) == 0 && (off & 7) == 0 &&
+          ((uintptr_t)ep.out & 15) == 0) {
+        store_nt_rows(ep, acc, off, lds, wave, lane);
+        return;
+      }
+    }
 #define RQ(I, J) (!has_resid(ep) ? make_uint2(0, 0) : PRE_R ? rq[(I) % RQM][(J) % RQN] : rload(ep, I, J))
     if constexpr (KT_::FIXED) {
       // folded LayerNorm: per-column terms (column sums of gamma (.) W,

@@ -136,6 +136,7 @@ hipError_t argmax_rows(int dt, const void *x, int32_t *out, int rows, int cols, 
 // Measured matrix-core peak (peak.hip): FLOP/s of a full grid of independent
 // 16x16x32 MFMAs (bf16 or fp16), `iters` loop trips per wave.
 hipError_t mfma_peak(int dt, int iters, double *flops_per_s, hipStream_t st);
+hipError_t hbm_read_rate(const void *buf, size_t bytes, int reps, double *bytes_per_s, hipStream_t st);
 
 hipError_t layernorm(int dt, const void *x, const void *w, const void *b, void *y, int rows, int cols, float eps,
                      hipStream_t st);

@@ -160,3 +160,17 @@ def test_measured_mfma_peak():
         assert 1.25e15 < f < 3.0e15, f
     with pytest.raises(_lib.HipError, match="dtype"):
         hip.measure_mfma_peak(0, 10)
+
+
+def test_measured_hbm_read():
+    """mh_measure_hbm_read: a read-only stream over 1 GiB lands between a
+    quarter and 1.1x the datasheet 8 TB/s and rejects a buffer under 1 MiB."""
+    import torch
+    from munet_amd import _lib
+    from munet_amd.backend import HipBackend
+    hip = HipBackend(0)
+    buf = torch.ones(1 << 29, device="cuda", dtype=torch.float16)
+    r = hip.measure_hbm_read(buf, 3)
+    assert 2.0e12 < r < 8.8e12, r
+    with pytest.raises(_lib.HipError, match="at least 1 MiB"):
+        hip.measure_hbm_read(buf[:1024], 1)
