@@ -12,16 +12,18 @@ torch.cuda.synchronize() on both sides.
 Roofline: every op's cost inside the forward is measured with HIP events on
 the engine stream as differences of prefix-graph times (for each prefix
 ops[0..i] of the forward, 20 back-to-back replays between two events; op i's
-time is T(i) - T(i-1): its duration where the forward runs it, with the
-forward's caches, mh_engine_forward_op_times; the kernel trace of the same
-command shows the same per-dispatch durations).  The kernel with the largest
-cost per forward is the dominant one, and its algorithmic work per launch
-(GEMM 2*M*N*K FLOPs, causal attention 4*B*H*T^2*hd/2, LayerNorm unique bytes)
-over its mean in-forward launch time is `achieved`, against the datasheet
-peak and against the measured ones (the register-only MFMA loop of
+cost is T(i) - T(i-1), which also holds what it costs the ops after it,
+mh_engine_forward_op_times).  The kernel category with the largest cost per
+forward is the dominant one.  Its launch duration is timed with HIP events
+over 20 back-to-back launches of the forward's own op (the same arena
+buffers, the folded-LayerNorm and statistics programs) replayed from one
+graph on the engine stream (mh_engine_op_times; these are dispatches a
+kernel trace of the same command shows), and its algorithmic work per
+launch (GEMM 2*M*N*K FLOPs, causal attention 4*B*H*T^2*hd/2, LayerNorm
+unique bytes) over that duration is `achieved`, against the datasheet peak
+and against the measured ones (the register-only MFMA loop of
 mh_measure_mfma_peak; a read-only stream over 2 GiB, mh_measure_hbm_read; a
-1 GiB device copy).  Every op is also timed alone from its own graph (warm
-caches, "kernels_isolated").
+1 GiB device copy).
 
 CPU baseline: the C++ restatement of MuNet's CPU backend (oracle/, "port")
 in its reference-threading mode (MuNet's own split: CPUBackend::parallel_for
@@ -366,11 +368,16 @@ def main():
     del src, dst, buf
 
     # per-op cost inside the forward (prefix-graph differences) picks the
-    # dominant kernel and gives its mean launch time
+    # dominant kernel; its launch duration is the mean over 20 back-to-back
+    # launches of the forward's own op replayed from one graph between HIP
+    # events on the engine stream (the dispatches a kernel trace of this
+    # command shows)
     fwd_rows = categorise(eng.forward_op_times(20))
     for r in fwd_rows.values():
         r["per_fwd"] = r["t"] * r["count"]
-    dom = max(fwd_rows.values(), key=lambda r: r["per_fwd"])
+    iso = categorise(eng.op_times(20))
+    dom_f = max(fwd_rows.values(), key=lambda r: r["per_fwd"])
+    dom = iso[dom_f["name"]]
     t_dom = dom["t"]
     if dom["flops"]:
         ach = dom["flops"] / t_dom
@@ -381,10 +388,11 @@ def main():
         roof = dict(bound="hbm", achieved=ach / 1e9, peak=PEAK_HBM / 1e9, unit="GB/s", frac=ach / PEAK_HBM,
                     peak_measured=peak_read / 1e9, frac_of_measured=ach / peak_read)
     roof.update(kernel=dom["name"], avg_us=t_dom * 1e6, launches_per_forward=dom["count"],
-                work_per_launch=dom["flops"] or dom["bytes"], timing="in-forward: differences of prefix-graph times, HIP events on the engine stream",
-                share_of_forward=dom["per_fwd"] / s, traffic=measured_traffic(dom["name"]))
+                work_per_launch=dom["flops"] or dom["bytes"],
+                timing="20 back-to-back launches of the forward's own op from one graph between HIP events",
+                in_forward_us_per_forward=dom_f["per_fwd"] * 1e6, share_of_forward=dom_f["per_fwd"] / s,
+                traffic=measured_traffic(dom["name"]))
 
-    iso = categorise(eng.op_times(20))
     kernels = {n: dict(avg_us=round(r["t"] * 1e6, 2), per_forward=r["count"],
                        tflops=round(r["flops"] / r["t"] / 1e12, 1) if r["flops"] else None,
                        gbs=round(r["bytes"] / r["t"] / 1e9, 1) if r["bytes"] else None) for n, r in iso.items()}

@@ -77,15 +77,19 @@ template <int DT>
 hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch, long sa,
                      long sb, long sc, const EpiArgs &ep, int tile, int kind, hipStream_t st) {
   const bool dma = gemm_pipe_dma_ok(A, Bt, M, N, K, lda, ldb);
-  // a folded LayerNorm exists only in the fixed programs: a forced tile
-  // without them takes the automatic choice
-  if (tile < 0 || (kind >= PK_LN_BIAS && !fixed_tile(tile))) tile = auto_tile(dma, M, N, K, batch);
+  // a folded LayerNorm exists only in the fixed programs, and the 256x256
+  // tile only has the plain, bias and non-temporal bias ones: a forced tile
+  // without the program takes the automatic choice
+  const bool head_prog = kind == PK_PLAIN || kind == PK_BIAS || kind == PK_BIAS_NT;
+  if (tile == 18 && !(DT == BF16 && dma && head_prog)) tile = -1;
+  if (tile < 0 || (kind >= PK_LN_BIAS && !fixed_tile(tile) && tile != 18)) tile = auto_tile(dma, M, N, K, batch);
   if (tile >= 7 && !dma) tile = 0;
   // LayerNorm partials of stats_cols columns need wave tiles that cover whole
   // groups: move to the nearest tile whose wave-tile width is a multiple
   if (ep.stats_out && pipe_wave_cols(tile) % ep.stats_cols)
     tile = ep.stats_cols == 48 ? (dma ? 8 : 3) : ep.stats_cols == 64 ? (dma ? 9 : 0) : 2;
   if (tile == 16 || tile == 17) return gemm_pipe_wide(DT, kind, tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
+  if (tile == 18) return gemm_pipe_head(kind, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
   if (kind > PK_GENERAL && fixed_tile(tile))
     return tile <= 3 ? gemm_pipe_fixed_staged(kind, tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st)
                      : gemm_pipe_fixed_dma(kind, tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);

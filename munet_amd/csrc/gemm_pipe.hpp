@@ -408,30 +408,42 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
   // then wrote 2.25 times the output's bytes.  Interior tiles of an aligned
   // row-major output only (the caller checks).
   static constexpr int NT_LPR = WTN * 2 / 16;  // lanes per staged row
-  static constexpr bool NT_ROWS = WTN % 8 == 0 && NT_LPR <= 64 && 64 % NT_LPR == 0 &&
-                                  WTM * (WTN * 2 + 16) * G::NW <= 2 * (BM + BN) * 128;
+  static constexpr int NT_RB = WTN * 2 + 16;   // bytes per staged row (16-byte pad against bank conflicts)
+  // rows of its tile a wave stages at a time: all, or a half / quarter when
+  // the waves' tiles do not fit the K loop's LDS (2 stages at least)
+  static constexpr int NT_PASSES = WTM * NT_RB * G::NW <= 2 * (BM + BN) * 128       ? 1
+                                   : (WTM / 2) * NT_RB * G::NW <= 2 * (BM + BN) * 128 ? 2
+                                                                                     : 4;
+  static constexpr bool NT_ROWS = WTN % 8 == 0 && NT_LPR <= 64 && 64 % NT_LPR == 0 && FM % NT_PASSES == 0 &&
+                                  (WTM / NT_PASSES) * NT_RB * G::NW <= 2 * (BM + BN) * 128;
   __device__ __forceinline__ void store_nt_rows(const EpiArgs &ep, f32x4 (&acc)[FM][FN], long off, u32x4 *lds,
                                                 int wave, int lane) {
-    constexpr int RB = WTN * 2 + 16;  // bytes per staged row (16-byte pad against bank conflicts)
     constexpr int RPI = 64 / NT_LPR;  // rows per store instruction
-    char *stage = reinterpret_cast<char *>(lds) + wave * WTM * RB;
+    constexpr int FMP = FM / NT_PASSES, RP = WTM / NT_PASSES;
+    char *stage = reinterpret_cast<char *>(lds) + wave * RP * NT_RB;
     __syncthreads();  // every wave has read its last fragments from the K loop's LDS
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-        const uint2 pk = epi_fast_bf16_fixed<KT_::BIAS, ACT_NONE, false>(v, bq[j], make_uint2(0, 0), ep.gelu_c);
-        *reinterpret_cast<uint2 *>(stage + (i * 16 + g.li) * RB + (j * 16 + g.lg * 4) * 2) = pk;
-      }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
-    __builtin_amdgcn_wave_barrier();
     const int rr = lane / NT_LPR, cc = lane % NT_LPR;
     uint16_t *base = static_cast<uint16_t *>(ep.out) + off + long(m0 + g.wm * WTM) * ep.ldc + n0 + g.wn * WTN + cc * 8;
 #pragma unroll
-    for (int r = rr; r < WTM; r += RPI) {
-      const u32x4 v = *reinterpret_cast<const u32x4 *>(stage + r * RB + cc * 16);
-      __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(base + long(r) * ep.ldc));
+    for (int p = 0; p < NT_PASSES; ++p) {
+#pragma unroll
+      for (int i = 0; i < FMP; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          float v[4] = {acc[p * FMP + i][j][0], acc[p * FMP + i][j][1], acc[p * FMP + i][j][2],
+                        acc[p * FMP + i][j][3]};
+          const uint2 pk = epi_fast_bf16_fixed<KT_::BIAS, ACT_NONE, false>(v, bq[j], make_uint2(0, 0), ep.gelu_c);
+          *reinterpret_cast<uint2 *>(stage + (i * 16 + g.li) * NT_RB + (j * 16 + g.lg * 4) * 2) = pk;
+        }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int r = rr; r < RP; r += RPI) {
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(stage + r * NT_RB + cc * 16);
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(base + long(p * RP + r) * ep.ldc));
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // the rows are read back before the next pass rewrites them
+      __builtin_amdgcn_wave_barrier();
     }
   }
 
@@ -908,5 +920,9 @@ hipError_t gemm_pipe_wide(int dt, int kind, int tile, const void *A, const void 
                           int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st);
 hipError_t gemm_pipe_fixed_dma(int kind, int tile, const void *A, const void *Bt, int M, int N, int K, long lda,
                                long ldb, int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st);
+// Direct-to-LDS 256x256, two stages, AGPR accumulators (gemm_pipe_head.hip,
+// tile 18): the plain, bias and non-temporal bias programs.
+hipError_t gemm_pipe_head(int kind, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch,
+                          long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st);
 
 }  // namespace mh
