@@ -45,6 +45,37 @@ const char *mh_version(void);
 int mh_device_count(int *count);
 /* Select `device` for the calling thread and create its state. */
 int mh_init(int device);
+/* Backend::query_support (src/core/backend.hpp:411-425): whether this backend
+ * runs `feature` on storages of `dtype`, the fallback policy when it does
+ * not, and the accumulation dtype it prefers.  Feature codes 0-12 are the
+ * reference's BackendFeature values in its order (src/core/backend.hpp:
+ * 16-30); codes from 100 are the path's functions that have no reference
+ * capability.  Policy codes follow BackendFallbackPolicy (:32-36): nothing
+ * falls back to the CPU here, so the policy is always ExplicitUnsupported.
+ * An unknown feature is unavailable (the reference's default); an unknown
+ * dtype code is an error.  Needs no device. */
+#define MH_FEATURE_ELEMENTWISE_BINARY 0
+#define MH_FEATURE_BROADCAST_ROW 1
+#define MH_FEATURE_MATMUL 2
+#define MH_FEATURE_UNARY_ACTIVATION 3
+#define MH_FEATURE_SOFTMAX 4
+#define MH_FEATURE_CONCAT 5
+#define MH_FEATURE_LOSS 6
+#define MH_FEATURE_CONVOLUTION 7
+#define MH_FEATURE_POOLING 8
+#define MH_FEATURE_BATCH_NORM 9
+#define MH_FEATURE_OPTIMIZER_STEP 10
+#define MH_FEATURE_RANDOM_FILL 11
+#define MH_FEATURE_REDUCTION 12
+#define MH_FEATURE_TO_CONTIGUOUS 100
+#define MH_FEATURE_LAYER_NORM 101
+#define MH_FEATURE_ATTENTION 102
+#define MH_FEATURE_EMBEDDING 103
+#define MH_FEATURE_MASKED_FILL 104
+#define MH_POLICY_EXPLICIT_UNSUPPORTED 0
+#define MH_POLICY_CPU_FALLBACK 1
+#define MH_POLICY_CONVERSION_FALLBACK 2
+int mh_query_support(int feature, int dtype, int *available, int *fallback_policy, int *accumulation_dtype);
 /* Poll and clear device-side error flags (embedding ids out of range);
  * synchronises the device.  Returns non-zero with a message if any was set. */
 int mh_check_device_errors(void);

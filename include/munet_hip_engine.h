@@ -49,6 +49,19 @@ int mh_engine_create_from_artifact(mh_engine **engine, const char *path, int dev
 int mh_engine_set_param(mh_engine *engine, const char *name, const void *host_data, size_t bytes, int dtype);
 /* Compile for one input shape (exact shape contract). */
 int mh_engine_compile(mh_engine *engine, const int *input_shape, int ndim);
+/* Engine::load (src/inference.hpp:393-444): the parameters set so far are the
+ * module; emits LoadStarted / LoadCompleted to the observer (the completion
+ * message names the parameter count and bytes unless in lean mode).  Compile
+ * loads first when the caller has not. */
+int mh_engine_load(mh_engine *engine);
+/* EngineConfig (src/inference.hpp:32-41; setters :311-335): warmup_runs >= 0
+ * (compile runs warmup_runs - 1 graph forwards after its own first one,
+ * reported as compile_warmup_ms); strict_shape_check = 0 lets a run with any
+ * input shape compile its own instance instead of failing the contract;
+ * lean_mode = 1 leaves memory figures and the parameter scan out of events.
+ * Compile and run events carry a fresh trace id while an observer is
+ * attached (EngineStats last_compile_trace_id / last_run_trace_id). */
+int mh_engine_set_config(mh_engine *engine, int warmup_runs, int strict_shape_check, int lean_mode);
 /* Device address of the input / output buffers inside the arena. */
 int mh_engine_input_ptr(mh_engine *engine, void **ptr);
 int mh_engine_output_ptr(mh_engine *engine, void **ptr);

@@ -55,6 +55,7 @@ _SIGS = {
     "mh_argmax": [_i, _vp, _vp, _i, _i, _vp],
     "mh_measure_mfma_peak": [_i, _i, ctypes.POINTER(ctypes.c_double), _vp],
     "mh_measure_hbm_read": [_vp, _sz, _i, ctypes.POINTER(ctypes.c_double), _vp],
+    "mh_query_support": [_i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i)],
     "mh_matmul": [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "mh_matmul_noalloc": [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "mh_batched_matmul": [_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i64, _i64, _i64, _vp],
@@ -80,6 +81,8 @@ _SIGS = {
     "mh_engine_destroy": [_vp],
     "mh_engine_create_from_artifact": [ctypes.POINTER(_vp), ctypes.c_char_p, _i],
     "mh_engine_set_param": [_vp, ctypes.c_char_p, _vp, _sz, _i],
+    "mh_engine_load": [_vp],
+    "mh_engine_set_config": [_vp, _i, _i, _i],
     "mh_engine_compile": [_vp, _ip, _i],
     "mh_engine_input_ptr": [_vp, ctypes.POINTER(_vp)],
     "mh_engine_output_ptr": [_vp, ctypes.POINTER(_vp)],

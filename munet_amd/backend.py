@@ -116,8 +116,23 @@ class BackendSupport:
     preferred_accumulation_dtype: int
 
 
-FEATURES = ("elementwise", "unary", "softmax", "matmul", "batched_matmul", "concat", "convolution",
-            "pooling", "upsample", "to_contiguous", "layer_norm", "attention", "embedding", "masked_fill")
+# BackendFeature (reference src/core/backend.hpp:16-30, in its order) and the
+# path's functions that have no reference capability: the mh_query_support codes
+FEATURES = {"elementwise_binary": 0, "broadcast_row": 1, "matmul": 2, "unary_activation": 3, "softmax": 4,
+            "concat": 5, "loss": 6, "convolution": 7, "pooling": 8, "batch_norm": 9, "optimizer_step": 10,
+            "random_fill": 11, "reduction": 12, "to_contiguous": 100, "layer_norm": 101, "attention": 102,
+            "embedding": 103, "masked_fill": 104}
+POLICIES = ("ExplicitUnsupported", "CPUFallback", "ConversionFallback")
+
+
+def query_support(feature: str, dtype: int) -> BackendSupport:
+    """Backend::query_support (src/core/backend.hpp:411-425) of the HIP
+    backend, from mh_query_support (no device needed). Unknown features are
+    unavailable."""
+    av, pol, acc = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    call("mh_query_support", FEATURES.get(feature, -1), dtype, ctypes.byref(av), ctypes.byref(pol),
+         ctypes.byref(acc))
+    return BackendSupport(bool(av.value), POLICIES[pol.value], acc.value)
 
 
 class HipBackend:
@@ -131,8 +146,7 @@ class HipBackend:
         return "hip"
 
     def query_support(self, feature: str, dtype: int, shape=None) -> BackendSupport:
-        ok = feature in FEATURES and dtype in (F32, F16, BF16)
-        return BackendSupport(ok, "ExplicitUnsupported", F32)
+        return query_support(feature, dtype)
 
     # ---- allocation / transfer (backend.hpp:190-205) ----------------------
     def allocate(self, nbytes: int) -> int:

@@ -226,6 +226,46 @@ extern "C" {
 const char *mh_last_error(void) { return mh::g_last_error.c_str(); }
 const char *mh_version(void) { return "munet-hip 0.1 (gfx950)"; }
 
+int mh_query_support(int feature, int dtype, int *available, int *fallback_policy, int *accumulation_dtype) {
+  MH_TRY({
+    check_dt(dtype, true);
+    if (!available || !fallback_policy || !accumulation_dtype) throw Error("query_support: null output");
+    const bool fp = dtype != MH_I32;
+    bool ok = false;
+    switch (feature) {
+    // the float products, elementwise, activation, normalisation and spatial
+    // kernels: fp32, fp16 and bf16 storages
+    case MH_FEATURE_ELEMENTWISE_BINARY:
+    case MH_FEATURE_MATMUL:
+    case MH_FEATURE_UNARY_ACTIVATION:
+    case MH_FEATURE_SOFTMAX:
+    case MH_FEATURE_CONVOLUTION:
+    case MH_FEATURE_POOLING:
+    case MH_FEATURE_LAYER_NORM:
+    case MH_FEATURE_ATTENTION:
+    case MH_FEATURE_EMBEDDING:
+    case MH_FEATURE_MASKED_FILL:
+      ok = fp;
+      break;
+    // data movement: any storage, int32 included (broadcast_row runs as a
+    // strided gather with a zero row stride)
+    case MH_FEATURE_BROADCAST_ROW:
+    case MH_FEATURE_CONCAT:
+    case MH_FEATURE_TO_CONTIGUOUS:
+      ok = true;
+      break;
+    // training-only capabilities and the reductions are not part of the
+    // inference path: unavailable, never silently sent to the CPU
+    default:
+      ok = false;
+      break;
+    }
+    *available = ok ? 1 : 0;
+    *fallback_policy = MH_POLICY_EXPLICIT_UNSUPPORTED;
+    *accumulation_dtype = MH_F32;
+  })
+}
+
 int mh_device_count(int *count) {
   MH_TRY({
     int n = 0;

@@ -1127,7 +1127,49 @@ struct mh_engine {
   size_t runs = 0;
   double last_run_ms = 0, last_prepare_ms = 0, last_forward_ms = 0, last_validate_ms = 0;
 
+  // EngineConfig (reference src/inference.hpp:32-41, setters :311-335)
+  int warmup_runs = 0;              // compile runs warmup_runs - 1 forwards after the first
+  bool strict_shape_check = true;   // false: any input shape gets its own instance
+  bool lean_mode = false;           // no memory figures or parameter scan in events
+  bool loaded = false;
+  double compile_warmup_ms = 0;
+  // trace ids (reference next_trace_id / should_enable_trace_contexts,
+  // src/inference.hpp:720-722): a fresh id per compile and per run while an
+  // observer is attached, 0 otherwise; events carry the current one
+  uint64_t next_trace = 0, current_trace = 0, last_compile_trace = 0, last_run_trace = 0;
+  uint64_t new_trace() { return observer ? ++next_trace : 0; }
+
   ~mh_engine() { clear_cache(); }
+
+  // Engine::load (reference src/inference.hpp:393-444): the parameters given
+  // so far are the module; LoadStarted / LoadCompleted, with the parameter
+  // count unless in lean mode.  compile() loads first when the caller did
+  // not.
+  void load() {
+    if (loaded) return;
+    current_trace = 0;
+    emit("LoadStarted", 0.0, {}, {}, "Loading module into inference engine");
+    std::ostringstream m;
+    m << "Module loaded on hip:" << impl.device;
+    if (!lean_mode) {
+      size_t bytes = 0;
+      for (const auto &kv : impl.params) bytes += kv.second.host.size();
+      m << " (" << impl.params.size() << " parameter tensors, " << bytes << " bytes)";
+    }
+    loaded = true;
+    emit("LoadCompleted", 0.0, {}, {}, m.str());
+  }
+
+  // Engine::compile's warm-up: warmup_runs - 1 forwards after the compile's
+  // own first one (reference src/inference.hpp:507-515).
+  void warmup() {
+    compile_warmup_ms = 0;
+    if (impl.plan_only) return;
+    for (int i = 1; i < warmup_runs; ++i) {
+      impl.run_device();
+      compile_warmup_ms += impl.last_gpu_ms;
+    }
+  }
 
   void clear_cache() {
     for (auto &c : cache)
@@ -1149,7 +1191,7 @@ struct mh_engine {
     if (!impl.compiled) throw mh::Error("engine is not compiled");
     if (std::vector<int>(impl.in_shape.begin(), impl.in_shape.end()) == shape) return impl;
     const std::string why = mismatch(shape);
-    if (!why.empty()) throw mh::Error("Engine: input shape mismatch with compiled shape: " + why);
+    if (!why.empty() && strict_shape_check) throw mh::Error("Engine: input shape mismatch with compiled shape: " + why);
     auto it = shapes.find(shape);
     if (it != shapes.end()) return *it->second;
     auto inst = std::make_unique<mh::EngineImpl>();
@@ -1191,10 +1233,11 @@ struct mh_engine {
             const std::string &msg) const {
     if (!observer) return;
     std::ostringstream s;
-    s << "{\"type\":\"" << type << "\",\"device\":" << impl.device << ",\"run_index\":" << runs
-      << ",\"duration_ms\":" << ms << ",\"input_shape\":" << json_shape(in) << ",\"output_shape\":" << json_shape(out)
-      << ",\"current_memory_bytes\":" << memory_bytes() << ",\"peak_memory_bytes\":" << memory_bytes()
-      << ",\"message\":" << json_str(msg) << "}";
+    const size_t mem = lean_mode ? 0 : memory_bytes();
+    s << "{\"type\":\"" << type << "\",\"device\":" << impl.device << ",\"trace_id\":" << current_trace
+      << ",\"run_index\":" << runs << ",\"duration_ms\":" << ms << ",\"input_shape\":" << json_shape(in)
+      << ",\"output_shape\":" << json_shape(out) << ",\"current_memory_bytes\":" << mem
+      << ",\"peak_memory_bytes\":" << mem << ",\"message\":" << json_str(msg) << "}";
     observer(s.str().c_str(), observer_user);
   }
 
@@ -1202,6 +1245,7 @@ struct mh_engine {
   // `dev_in` holds a prepared device copy), `hout` host output.
   void run_one(const std::vector<int> &shape, const void *hin, const void *dev_in, void *hout) {
     const auto t0 = std::chrono::steady_clock::now();
+    current_trace = last_run_trace = new_trace();
     mh::EngineImpl &e = instance(shape);
     e.require_device();
     const std::vector<int> os(e.vals[e.output].shape.begin(), e.vals[e.output].shape.end());
@@ -1280,7 +1324,10 @@ struct mh_engine {
       << ",\"prepared_input_cache_bytes\":" << cache_bytes << ",\"prepared_input_cache_hits\":" << cache_hits
       << ",\"prepared_input_cache_misses\":" << cache_misses
       << ",\"prepared_input_cache_evictions\":" << cache_evictions << ",\"engine_memory_bytes\":" << memory_bytes()
-      << "}";
+      << ",\"last_compile_trace_id\":" << last_compile_trace << ",\"last_run_trace_id\":" << last_run_trace
+      << ",\"compile_warmup_ms\":" << compile_warmup_ms << ",\"warmup_runs\":" << warmup_runs
+      << ",\"strict_shape_check\":" << (strict_shape_check ? "true" : "false")
+      << ",\"lean_mode\":" << (lean_mode ? "true" : "false") << "}";
     // the primary instance's object minus its closing brace, then the engine's fields
     return s.substr(0, s.size() - 1) + x.str();
   }
@@ -1364,7 +1411,9 @@ int mh_engine_set_param(mh_engine *e, const char *name, const void *data, size_t
 int mh_engine_compile(mh_engine *e, const int *shape, int ndim) {
   ENG_TRY({
     if (!e || !shape || ndim <= 0) throw Error("bad input shape");
-    e->impl.compile(mh::Shape(shape, shape + ndim));
+    std::vector<int> ex(shape, shape + ndim);
+    if (mh_engine_compile_expected(e, shape, ndim, ex.data()) != 0) throw Error(mh_last_error());
+    e->expected.clear();  // exact contract
   })
 }
 
@@ -1404,10 +1453,13 @@ int mh_engine_compile_expected(mh_engine *e, const int *shape, int ndim, const i
     for (int i = 0; i < ndim; ++i)
       if (expected[i] != -1 && expected[i] != shape[i])
         throw Error("Engine: compile expected_input_shape mismatch: dim mismatch at index " + std::to_string(i));
+    e->load();
     const auto t0 = std::chrono::steady_clock::now();
-    e->emit("CompileStarted", 0.0, std::vector<int>(shape, shape + ndim), {}, "Starting compile");
+    e->current_trace = e->last_compile_trace = e->new_trace();
+    e->emit("CompileStarted", 0.0, std::vector<int>(shape, shape + ndim), {}, "Compiling inference shape contract");
     try {
       e->impl.compile(mh::Shape(shape, shape + ndim));
+      e->warmup();
     } catch (const std::exception &ex) {
       e->emit("Error", 0.0, std::vector<int>(shape, shape + ndim), {}, std::string("compile failed: ") + ex.what());
       throw;
@@ -1451,6 +1503,17 @@ int mh_engine_run_batch(mh_engine *e, int n, const void *const *inputs, void *co
     if (!e->impl.compiled) throw Error("engine is not compiled");
     const std::vector<int> shape(e->impl.in_shape.begin(), e->impl.in_shape.end());
     for (int i = 0; i < n; ++i) e->run_one(shape, inputs[i], nullptr, outputs[i]);
+  })
+}
+
+int mh_engine_load(mh_engine *e) { ENG_TRY(e->load()) }
+
+int mh_engine_set_config(mh_engine *e, int warmup_runs, int strict_shape_check, int lean_mode) {
+  ENG_TRY({
+    if (warmup_runs < 0) throw Error("Engine warmup_runs must be >= 0");
+    e->warmup_runs = warmup_runs;
+    e->strict_shape_check = strict_shape_check != 0;
+    e->lean_mode = lean_mode != 0;
   })
 }
 

@@ -64,6 +64,18 @@ class Engine:
         del lib
         return self
 
+    def finish_load(self):
+        """Engine::load's completion: emits LoadStarted / LoadCompleted to the
+        observer (compile does it otherwise)."""
+        _lib.call("mh_engine_load", self._h)
+        return self
+
+    def set_config(self, warmup_runs: int = 0, strict_shape_check: bool = True, lean_mode: bool = False):
+        """EngineConfig (reference src/inference.hpp:32-41)."""
+        _lib.call("mh_engine_set_config", self._h, int(warmup_runs), int(bool(strict_shape_check)), int(bool(lean_mode)))
+        self.strict = bool(strict_shape_check)
+        return self
+
     def load_artifact(self, path: str):
         h = _vp()
         _lib.call("mh_engine_create_from_artifact", ctypes.byref(h), str(path).encode(), self.device)
@@ -110,7 +122,7 @@ class Engine:
             out = np.empty(self.out_shape, dtype=self._out_dtype())
             _lib.call("mh_engine_run", self._h, x.ctypes.data_as(_vp), out.ctypes.data_as(_vp))
             return out
-        if getattr(self, "expected", None) is None:
+        if getattr(self, "expected", None) is None and getattr(self, "strict", True):
             raise ValueError(f"input shape {tuple(x.shape)} does not match the compiled contract {self.in_shape}")
         out = np.empty(self.output_shape_for(x.shape), dtype=self._out_dtype())
         _lib.call("mh_engine_run_shaped", self._h, x.ctypes.data_as(_vp), _lib.ints(x.shape), x.ndim,

@@ -260,6 +260,24 @@ class CpuOracle:
         self._call("upsample2d", _i(dt), _ptr(x), _ptr(out), _i(B), _i(C), _i(iH), _i(iW), _i(scale))
         return out
 
+    # -- MuNet's deploy-artifact loader (reference only) ---------------------
+    def load_check(self, path):
+        """None if MuNet's loader accepts the artifact at `path`, else its message."""
+        rc = self.lib.ref_load_check(str(path).encode())
+        return None if rc == 0 else self.lib.ref_last_error().decode()
+
+    def load_forward(self, path, x, dt):
+        """MuNet's loader on `path`, then the loaded module's forward on x."""
+        x = self._c(x, dt)
+        out = np.empty(64 << 20, dtype=np.uint8)
+        shp = (ctypes.c_int * 8)()
+        nd = ctypes.c_int()
+        self._call("load_forward", ctypes.c_char_p(str(path).encode()), _i(dt), _ptr(x), _ints(x.shape), _i(x.ndim),
+                   _ptr(out), _sz(out.nbytes), shp, ctypes.byref(nd))
+        shape = tuple(shp[i] for i in range(nd.value))
+        n = int(np.prod(shape)) * np.dtype(storage_np(dt)).itemsize
+        return out[:n].view(storage_np(dt)).reshape(shape).copy()
+
     def concat(self, xs, dim, dt):
         xs = [self._c(x, dt) for x in xs]
         nd = xs[0].ndim

@@ -18,7 +18,10 @@
 //   ref_upsample2d   -> nn::Upsample            (src/nn/pooling.hpp:37-42)
 //   ref_concat       -> Tensor::cat             (src/core/ops/shape.cpp:8-48)
 //   ref_masked_fill  -> Tensor::masked_fill     (src/core/ops/elementwise.cpp:8-53)
+//   ref_load_check   -> inference::load_serialized (src/inference_serialization.cpp:902-1080)
+//   ref_load_forward -> load_serialized, then Module::forward (src/core/module.hpp:71-83)
 #include "core/grad_mode.hpp"
+#include "inference.hpp"
 #include "nn/activations.hpp"
 #include "nn/attention.hpp"
 #include "nn/linear.hpp"
@@ -241,6 +244,28 @@ int ref_masked_fill(int dt, const void *x, const int32_t *mask, void *out,
     v.dtype = DataType::Float32;
     v.value = value;
     to_host(tx.masked_fill(tm, v), out);
+  })
+}
+
+// MuNet's own deploy-artifact loader on `path`: 0 if it accepts the file,
+// 1 with the loader's message (ref_last_error) if it refuses it.
+int ref_load_check(const char *path) {
+  REF_GUARD((void)inference::load_serialized(path, Device{DeviceType::CPU, 0}))
+}
+
+// Loads `path` with MuNet's loader and runs the module's forward on the host
+// input x (dtype dt, shape xs[xn]); the output's bytes go to out (at most
+// out_bytes), its shape to out_shape / *out_ndim (at most 8 dims).
+int ref_load_forward(const char *path, int dt, const void *x, const int *xs, int xn, void *out, size_t out_bytes,
+                     int *out_shape, int *out_ndim) {
+  REF_GUARD({
+    auto m = inference::load_serialized(path, Device{DeviceType::CPU, 0});
+    Tensor y = m->forward(from_host(x, mk_shape(xs, xn), to_dt(dt))).contiguous();
+    if (y.bytes() > out_bytes) throw std::runtime_error("ref_load_forward: output buffer too small");
+    if (y.shape().size() > 8) throw std::runtime_error("ref_load_forward: output rank above 8");
+    *out_ndim = int(y.shape().size());
+    for (size_t i = 0; i < y.shape().size(); ++i) out_shape[i] = int(y.shape()[i]);
+    to_host(y, out);
   })
 }
 

@@ -11,6 +11,7 @@ import pytest
 from munet_amd import _lib, models, synth
 from munet_amd.artifact import save_deploy_artifact
 from munet_amd.engine import Engine
+from oracle import CpuOracle, available
 
 
 def _params(cfg, scheme):
@@ -91,6 +92,8 @@ def _good_state(cfg, params):
     (lambda s: s.update({"0.weight": np.zeros((784, 256), np.float64)}), "unsupported dtype"),
 ])
 def test_artifact_validation(tmp_path, change, msg):
+    """Each malformed artifact is refused by this loader and, where the
+    reference sources were built, by MuNet's own loader too."""
     cfg = models.mlp_config()
     state = _good_state(cfg, _params(cfg, "mlp"))
     change(state)
@@ -98,6 +101,8 @@ def test_artifact_validation(tmp_path, change, msg):
     _write(path, state)
     with pytest.raises(_lib.HipError, match=msg):
         Engine(device=-1).load_artifact(str(path))
+    if available("reference"):
+        assert CpuOracle("reference").load_check(path) is not None, "MuNet's loader accepted it"
 
 
 def test_compressed_members_are_rejected(tmp_path):
@@ -178,3 +183,39 @@ def test_malformed_npy_headers_are_rejected(tmp_path, member, descr, shape, payl
                 z.writestr(k + ".npy", buf.getvalue())
     with pytest.raises(_lib.HipError, match=msg):
         Engine(device=-1).load_artifact(str(path)).compile((4, 784))
+
+
+needs_ref = pytest.mark.skipif(not available("reference"), reason="oracle/_ref not built (needs /root/reference)")
+
+
+@needs_ref
+@pytest.mark.parametrize("which", ["mlp_f32", "mlp_f16", "cnn_f32"])
+def test_munet_loader_reads_our_artifacts(tmp_path, which):
+    """MuNet's own deploy loader (src/inference_serialization.cpp, compiled
+    into oracle/_ref) accepts the artifacts save_deploy_artifact writes, and
+    the module it builds computes what the restatement computes from the
+    parameter dict, bit for bit."""
+    from oracle import models as om
+    cfg, scheme, shape = {"mlp_f32": (models.mlp_config(), "mlp", (8, 784)),
+                          "mlp_f16": (models.mlp_config(dtype="float16"), "mlp", (8, 784)),
+                          "cnn_f32": (models.cnn_config(), "he", (2, 3, 32, 32))}[which]
+    params = _params(cfg, scheme)
+    x = models.make_input(cfg, shape, scheme, scope="art_x")
+    path = tmp_path / f"{which}.npz"
+    save_deploy_artifact(str(path), cfg, params)
+    ref = CpuOracle("reference")
+    assert ref.load_check(path) is None
+    dt = synth.DTYPE_CODES[cfg["dtype"]]
+    y = ref.load_forward(path, x, dt)
+    assert np.array_equal(y, om.forward(CpuOracle("restatement"), cfg, params, x))
+
+
+@needs_ref
+def test_munet_loader_refuses_bf16_members(tmp_path):
+    """MuNet's loader has no bf16 (src/inference_serialization.cpp:459-471);
+    this loader takes bf16 members as <u2 bit patterns."""
+    cfg = models.mlp_config(dtype="bfloat16")
+    path = tmp_path / "bf16.npz"
+    save_deploy_artifact(str(path), cfg, _params(cfg, "mlp"))
+    assert CpuOracle("reference").load_check(path) is not None
+    Engine(device=-1).load_artifact(str(path)).compile((4, 784))

@@ -49,11 +49,6 @@ def test_plugin_probe_abi():
     assert r is None or isinstance(r, bytes)
 
 
-def test_cpp_backend_mirror_selftest():
-    lib = ctypes.CDLL(_lib.LIB_PATH)
-    assert lib.mh_backend_selftest() == 0
-
-
 def test_error_reporting_without_gpu():
     """Invalid arguments fail with a message instead of touching the device."""
     with pytest.raises(_lib.HipError, match="unsupported dtype"):

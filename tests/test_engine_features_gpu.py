@@ -1,15 +1,25 @@
 """Engine caller features on the GPU: per-shape instances under a wildcard
-contract, the prepared-input cache, run_batch, the observer's run events and
-the pinned-host staging path, each checked bit-exactly against plain runs of
-an engine compiled for that exact shape (reference src/inference.hpp:31-289,
-538-627)."""
+contract, the prepared-input cache, run_batch, the observer's run events, the
+pinned-host staging path and engines built from deploy artifacts (reference
+src/inference.hpp:31-289, 538-627), each checked against the CPU oracle (the
+restatement of MuNet's CPU backend, or MuNet's own compiled loader and
+forward for the artifacts) and bit-exactly against plain runs of an engine
+compiled for that exact shape."""
 import numpy as np
 import pytest
 
-from munet_amd import models
+from munet_amd import models, synth
 from munet_amd.engine import Engine
+from oracle import CpuOracle, available
+from oracle import models as omodels
+from util import assert_close
 
 pytestmark = pytest.mark.gpu
+
+
+def _vs_oracle(orc, cfg, p, x, y, what):
+    dt = synth.DTYPE_CODES[cfg.get("dtype", "float32")]
+    assert_close(y, omodels.forward(orc, cfg, p, x), dt, what=what)
 
 
 def _mlp():
@@ -21,30 +31,36 @@ def _x(cfg, b, scope):
     return models.make_input(cfg, (b, 784), "mlp", scope=scope)
 
 
-def test_wildcard_batch_matches_exact_engines():
+def test_wildcard_batch_matches_exact_engines(orc):
     cfg, p = _mlp()
     e = Engine(0).load(cfg, p).compile((8, 784), expected_input_shape=(-1, 784))
     for b in (8, 16, 3, 16):
         x = _x(cfg, b, f"w{b}")
         ref = Engine(0).load(cfg, p).compile((b, 784)).run(x)
-        assert np.array_equal(e.run(x), ref)
+        y = e.run(x)
+        assert np.array_equal(y, ref)
+        _vs_oracle(orc, cfg, p, x, y, f"wildcard batch {b}")
     assert e.stats()["compiled_instances"] == 3
 
 
-def test_decoder_wildcard_batch():
+def test_decoder_wildcard_batch(orc):
     cfg = models.decoder_config(vocab=500, ctx=64, d_model=64, num_heads=2, num_layers=2, ffn=128, dtype="bfloat16")
     p = models.init_params(cfg, "gpt", scope="featd")
     e = Engine(0).load(cfg, p).compile((2, 64), expected_input_shape=(-1, 64))
     for b in (1, 3):
         ids = models.make_input(cfg, (b, 64), "gpt", scope=f"featd{b}")
-        assert np.array_equal(e.run(ids), Engine(0).load(cfg, p).compile((b, 64)).run(ids))
+        y = e.run(ids)
+        assert np.array_equal(y, Engine(0).load(cfg, p).compile((b, 64)).run(ids))
+        _vs_oracle(orc, cfg, p, ids, y, f"decoder wildcard batch {b}")
 
 
-def test_prepared_input_cache():
+def test_prepared_input_cache(orc):
     cfg, p = _mlp()
     e = Engine(0).load(cfg, p).compile((8, 784))
     x, x2 = _x(cfg, 8, "c1"), _x(cfg, 8, "c2")
     ref, ref2 = e.run(x), e.run(x2)
+    _vs_oracle(orc, cfg, p, x, ref, "cached input")
+    _vs_oracle(orc, cfg, p, x2, ref2, "cached input, new version")
     assert np.array_equal(e.run_prepared(x, key=1, version=0), ref)
     assert np.array_equal(e.run_prepared(x, key=1, version=0), ref)  # hit: no transfer
     st = e.stats()
@@ -65,7 +81,7 @@ def test_prepared_input_cache():
     assert e.stats()["prepared_input_cache_entries"] == 0
 
 
-def test_run_batch_and_observer():
+def test_run_batch_and_observer(orc):
     cfg, p = _mlp()
     e = Engine(0).load(cfg, p).compile((8, 784))
     xs = [_x(cfg, 8, f"b{i}") for i in range(3)]
@@ -73,6 +89,7 @@ def test_run_batch_and_observer():
     e.set_observer(events.append)
     outs = e.run_batch(xs)
     for x, o in zip(xs, outs):
+        _vs_oracle(orc, cfg, p, x, o, "run_batch")
         assert np.array_equal(o, e.run(x))
     kinds = [ev["type"] for ev in events[:6]]
     assert kinds == ["RunStarted", "RunCompleted"] * 3
@@ -80,7 +97,7 @@ def test_run_batch_and_observer():
     assert e.stats()["host_runs"] == 6
 
 
-def test_pinned_io():
+def test_pinned_io(orc):
     cfg = models.decoder_config(vocab=500, ctx=64, d_model=64, num_heads=2, num_layers=1, ffn=128, dtype="bfloat16")
     p = models.init_params(cfg, "gpt", scope="pin")
     ids = models.make_input(cfg, (2, 64), "gpt", scope="pin_in")
@@ -90,6 +107,26 @@ def test_pinned_io():
     pin_in[...] = ids
     e.run_pinned()
     assert np.array_equal(pin_out, ref)
+    _vs_oracle(orc, cfg, p, ids, pin_out.copy(), "pinned-host forward")
+
+
+@pytest.mark.skipif(not available("reference"), reason="oracle/_ref not built (needs /root/reference)")
+@pytest.mark.parametrize("which", ["mlp_f32", "mlp_f16", "cnn_f32"])
+def test_artifact_engine_vs_munet_loader(tmp_path, which):
+    """An engine built from a deploy artifact against MuNet's own loader and
+    forward on the same file (src/inference_serialization.cpp and the
+    reference's CPU ops, compiled into oracle/_ref)."""
+    from munet_amd.artifact import save_deploy_artifact
+    cfg, scheme, shape = {"mlp_f32": (models.mlp_config(), "mlp", (64, 784)),
+                          "mlp_f16": (models.mlp_config(dtype="float16"), "mlp", (64, 784)),
+                          "cnn_f32": (models.cnn_config(), "he", (8, 3, 32, 32))}[which]
+    p = models.init_params(cfg, scheme, scope="art_gpu")
+    x = models.make_input(cfg, shape, scheme, scope="art_gpu_x")
+    path = tmp_path / f"{which}.npz"
+    save_deploy_artifact(str(path), cfg, p)
+    y = Engine(0).load_artifact(str(path)).compile(shape).run(x)
+    dt = synth.DTYPE_CODES[cfg["dtype"]]
+    assert_close(y, CpuOracle("reference").load_forward(path, x, dt), dt, what=f"artifact {which} vs MuNet's loader")
 
 
 def test_per_op_timings():
@@ -174,3 +211,23 @@ def test_measured_hbm_read():
     assert 2.0e12 < r < 8.8e12, r
     with pytest.raises(_lib.HipError, match="at least 1 MiB"):
         hip.measure_hbm_read(buf[:1024], 1)
+
+
+def test_engine_config_on_device(orc):
+    """warmup_runs runs extra forwards at compile (compile_warmup_ms), a
+    non-strict engine serves another batch size from its own instance, and
+    every run event carries its own trace id."""
+    cfg, p = _mlp()
+    e = Engine(0).load(cfg, p).set_config(warmup_runs=3, strict_shape_check=False)
+    events = []
+    e.set_observer(events.append)
+    e.compile((8, 784))
+    assert e.stats()["compile_warmup_ms"] > 0
+    x = _x(cfg, 8, "cfg8")
+    y = e.run(x)
+    _vs_oracle(orc, cfg, p, x, y, "warmed engine")
+    x5 = _x(cfg, 5, "cfg5")
+    _vs_oracle(orc, cfg, p, x5, e.run(x5), "non-strict engine, batch 5")
+    runs = [ev for ev in events if ev["type"] == "RunStarted"]
+    assert len(runs) == 2 and 0 < runs[0]["trace_id"] < runs[1]["trace_id"]
+    assert e.stats()["last_run_trace_id"] == runs[1]["trace_id"]
