@@ -18,6 +18,7 @@ int pipe_wave_cols(int tile) {
   case 0: case 6: case 7: case 9: case 15: return 64;
   case 3: case 8: case 10: case 11: case 17: return 48;
   case 5: case 14: case 16: return 96;
+  case 19: return 144;
   default: return 32;  // 1 (128x64), 2 (64x64), 12 (128x64)
   }
 }
@@ -27,6 +28,10 @@ int pipe_wave_cols(int tile) {
 //  * M tiling evenly by 256 and N by 192 into 232..256 tiles (FFN up: 256):
 //    direct-to-LDS 256x192 with eight waves, one workgroup per CU (FFN up
 //    33.1 -> 31.1 us; QKV, 192 tiles, 28.3 -> 29.5 us, so it stays below);
+//  * M tiling by 128 and N by 288 into 232..256 tiles (QKV, 4096 x 2304):
+//    direct-to-LDS 128x288, eight waves of 32x144, one workgroup per CU
+//    (forward 1.620 -> 1.609 ms against the register-staged 128x96, whose
+//    768 tiles take three rounds of two workgroups per CU);
 //  * N tiling evenly by 96 with at most one tile per CU (N = 768: FFN down,
 //    attention out-projection): direct-to-LDS 128x96, 4 stages, eight waves
 //    (one workgroup per CU, so deep stages and two waves per SIMD hide the
@@ -42,6 +47,8 @@ int auto_tile(bool dma, int M, int N, int K, int batch) {
   const long t64 = long((M + 127) / 128) * ((N + 63) / 64) * batch;
   const long t192w = long(M / 256) * (N / 192) * batch;
   if (dma && M % 256 == 0 && N % 192 == 0 && t192w >= 232 && t192w <= 256) return 16;
+  const long t288 = long(M / 128) * (N / 288) * batch;
+  if (dma && M % 128 == 0 && N % 288 == 0 && t288 >= 232 && t288 <= 256) return 19;
   if (dma && N % 96 == 0 && t96 <= 256) return 17;
   if (N % 128 == 0 && t128 >= 640) return 0;
   if (N % 96 == 0) return 3;
@@ -49,7 +56,9 @@ int auto_tile(bool dma, int M, int N, int K, int batch) {
 }
 
 // The tiles with fixed epilogue programs (gemm_pipe_fixed_*.hip).
-bool fixed_tile(int tile) { return (tile >= 0 && tile <= 3) || tile == 8 || tile == 9 || tile == 16 || tile == 17; }
+bool fixed_tile(int tile) {
+  return (tile >= 0 && tile <= 3) || tile == 8 || tile == 9 || tile == 16 || tile == 17 || tile == 19;
+}
 
 // The epilogue program for these arguments: a fixed program for the
 // combinations the engine emits (bf16, 8-byte aligned destination, bias
@@ -84,11 +93,13 @@ hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long ld
   if (tile == 18 && !(DT == BF16 && dma && head_prog)) tile = -1;
   if (tile < 0 || (kind >= PK_LN_BIAS && !fixed_tile(tile) && tile != 18)) tile = auto_tile(dma, M, N, K, batch);
   if (tile >= 7 && !dma) tile = 0;
+  if (tile == 19 && (M % 128 || N % 288)) tile = auto_tile(dma, M, N, K, batch);
   // LayerNorm partials of stats_cols columns need wave tiles that cover whole
   // groups: move to the nearest tile whose wave-tile width is a multiple
   if (ep.stats_out && pipe_wave_cols(tile) % ep.stats_cols)
     tile = ep.stats_cols == 48 ? (dma ? 8 : 3) : ep.stats_cols == 64 ? (dma ? 9 : 0) : 2;
-  if (tile == 16 || tile == 17) return gemm_pipe_wide(DT, kind, tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
+  if (tile == 16 || tile == 17 || tile == 19)
+    return gemm_pipe_wide(DT, kind, tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
   if (tile == 18) return gemm_pipe_head(kind, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
   if (kind > PK_GENERAL && fixed_tile(tile))
     return tile <= 3 ? gemm_pipe_fixed_staged(kind, tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st)

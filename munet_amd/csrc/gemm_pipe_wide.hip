@@ -2,7 +2,9 @@
 // a 4x2 grid (64x96 wave tiles, two waves per SIMD), two stages: tile 16.
 // Eight waves per CU keep the matrix cores fed where the four-wave 128-row
 // tiles leave them idle, and 256x192 covers a 4096x3072 product in exactly
-// 256 tiles, one per CU.  Every epilogue program (fixed bf16 ones and the
+// 256 tiles, one per CU.  Tile 19, 128x288 (32x144 wave tiles, two stages),
+// does the same for the 4096x2304 q/k/v product; tile 17, 128x96 with four
+// stages, for the N = 768 products.  Every epilogue program (fixed bf16 ones and the
 // general one); accumulators in VGPRs (see build.py).
 #include "gemm_pipe.hpp"
 
@@ -16,6 +18,7 @@ hipError_t run(int tile, const void *A, const void *Bt, int M, int N, int K, lon
   switch (tile) {
   case 16: launch_dma<DT, 256, 192, 4, 2, 2, EK>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;
   case 17: launch_dma<DT, 128, 96, 4, 2, 4, EK>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;
+  case 19: launch_dma<DT, 128, 288, 4, 2, 2, EK>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;
   default: return hipErrorNotSupported;
   }
   return hipGetLastError();

@@ -86,7 +86,7 @@ def test_encoder_block_folded_layer_norm_vs_oracle(orc):
     assert_close(y, ref, synth.BF16, what="encoder block (ln2 folded)")
 
 
-@pytest.mark.parametrize("tile", ["216", "217", "208", "200", "202"])
+@pytest.mark.parametrize("tile", ["216", "217", "208", "200", "202", "219"])
 def test_folded_decoder_bit_identical_across_tiles(monkeypatch, tile):
     """Every pipelined tile accumulates in the same K order and combines a
     row's LayerNorm partials in the same order (four chunks, then pairwise,
