@@ -193,6 +193,13 @@ int mh_qkv_projection(int dt, const void *x, const void *wqkv_t, const void *bqk
  * as [B, T, H*hd].  Scale = 1/sqrt(hd) rounded to dt. */
 int mh_attention(int dt, const void *q, const void *k, const void *v, void *ctx, int B, int H, int T, int hd,
                  int causal, void *stream);
+/* No counterpart in the reference (its attention has no per-position keys,
+ * so it cannot be decoded incrementally): the same rounding steps with key j
+ * of head (b, h) read as row (b*H + h)*T + j of k, like v.  The attention of
+ * the KV-cache decode (mh_decoder_*) and of DecoderLM configs with
+ * "attention": "textbook". */
+int mh_attention_textbook(int dt, const void *q, const void *k, const void *v, void *ctx, int B, int H, int T,
+                          int hd, int causal, void *stream);
 
 /* ---- BackendShapeCapability (src/core/backend.hpp:263-271) --------------- */
 /* :266-267 concat(inputs, out, dim, shapes): `count` contiguous inputs of rank

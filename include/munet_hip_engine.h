@@ -126,6 +126,36 @@ int mh_engine_op_times(mh_engine *engine, int reps, const char *only, char *buf,
  * Profiler (src/core/module.hpp:71-83). */
 int mh_engine_forward_op_times(mh_engine *engine, int reps, char *buf, size_t len);
 
+/* ---- KV-cache decode --------------------------------------------------------
+ * No counterpart in the reference: its roadmap lists a KV cache
+ * (documentation/architecture/gpt3_local_roadmap.md:67) that the code does
+ * not have, and its attention reads the keys through a reinterpretation of
+ * k's buffer (src/nn/attention.hpp:64-67), so a position's key is not its
+ * own and cannot be cached.  A decoder therefore runs DecoderLM configs with
+ * "attention": "textbook" (key j of a head is position j's key; every
+ * rounding step of the reference's chain kept), whose engine forward is the
+ * prefill.  Greedy decoding: each step feeds one token per sequence. */
+typedef struct mh_decoder mh_decoder;
+/* A decoder over a compiled engine (weights shared with it), `batch`
+ * sequences (1..16), positions 0..max_len-1 (max_len <= ctx). */
+int mh_decoder_create(mh_decoder **decoder, mh_engine *engine, int batch, int max_len);
+int mh_decoder_destroy(mh_decoder *decoder);
+/* Prompt ids [batch, T0] (int32) through the engine's forward, filling the
+ * caches for positions 0..T0-1; logits_out [batch, T0, vocab] (storage
+ * dtype) optional.  The next step's input becomes each sequence's greedy
+ * choice at position T0-1. */
+int mh_decoder_prefill(mh_decoder *decoder, const int32_t *ids, int T0, void *logits_out);
+/* One step at the next position: ids [batch] (NULL: the previous greedy
+ * choices); logits_out [batch, vocab] and next_ids [batch] optional. */
+int mh_decoder_step(mh_decoder *decoder, const int32_t *ids, void *logits_out, int32_t *next_ids);
+/* n greedy steps back to back (one graph launch each): tokens_out [n, batch];
+ * gpu_ms (optional): device time of the n steps. */
+int mh_decoder_generate(mh_decoder *decoder, int n, int32_t *tokens_out, float *gpu_ms);
+/* The position the next step feeds (-1 before the first prefill). */
+int mh_decoder_position(mh_decoder *decoder, int *pos);
+/* Sizes, step count and last timings as JSON. */
+int mh_decoder_stats(mh_decoder *decoder, char *buf, size_t len);
+
 #ifdef __cplusplus
 }
 #endif

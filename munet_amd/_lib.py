@@ -63,6 +63,7 @@ _SIGS = {
     "mh_pack_linear_weight": [_i, _vp, _vp, _i, _i, _vp],
     "mh_qkv_projection": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
     "mh_attention": [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
+    "mh_attention_textbook": [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp],
     "mh_concat": [_i, ctypes.POINTER(_vp), _i, _vp, _i, _i, _ip, _vp],
     "mh_transpose2d": [_i, _vp, _vp, _i, _i, _i, _vp],
     "mh_conv2d": [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp],
@@ -94,6 +95,13 @@ _SIGS = {
     "mh_engine_plan": [_vp, ctypes.c_char_p, _sz],
     "mh_engine_op_times": [_vp, ctypes.c_int, ctypes.c_char_p, ctypes.c_char_p, _sz],
     "mh_engine_forward_op_times": [_vp, ctypes.c_int, ctypes.c_char_p, _sz],
+    "mh_decoder_create": [ctypes.POINTER(_vp), _vp, _i, _i],
+    "mh_decoder_destroy": [_vp],
+    "mh_decoder_prefill": [_vp, _vp, _i, _vp],
+    "mh_decoder_step": [_vp, _vp, _vp, _vp],
+    "mh_decoder_generate": [_vp, _i, _vp, ctypes.POINTER(ctypes.c_float)],
+    "mh_decoder_position": [_vp, ctypes.POINTER(_i)],
+    "mh_decoder_stats": [_vp, ctypes.c_char_p, _sz],
     "mh_engine_stream": [_vp, ctypes.POINTER(_vp)],
     "mh_engine_compile_expected": [_vp, _ip, _i, _ip],
     "mh_engine_output_shape_for": [_vp, _ip, _i, _ip, _ip],

@@ -285,6 +285,11 @@ class HipBackend:
     def attention(self, q, k, v, ctx, B, H, T, hd, causal):
         call("mh_attention", _dt(q), _p(q), _p(k), _p(v), _p(ctx), B, H, T, hd, int(causal), _stream())
 
+    def attention_textbook(self, q, k, v, ctx, B, H, T, hd, causal):
+        """Textbook keys (key j of a head is row j of its k): the decode
+        attention; no MuNet counterpart."""
+        call("mh_attention_textbook", _dt(q), _p(q), _p(k), _p(v), _p(ctx), B, H, T, hd, int(causal), _stream())
+
     # ---- shape (backend.hpp:263-271) ---------------------------------------
     def concat(self, inputs, out, dim, shapes):
         ptrs = (_vp * len(inputs))(*[x.data_ptr() for x in inputs])

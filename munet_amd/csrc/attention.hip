@@ -330,7 +330,10 @@ template <int DT> __device__ __forceinline__ void round_scores(float v[4]) {
   }
 }
 
-template <int DT, int RW>
+// TXT (textbook keys): K is head-split like V, key j of block bh at row
+// bh*T + j; its tile is staged in natural [j][d] layout (the swz pattern) and
+// the MFMA's K operand is read straight, without the transposing read.
+template <int DT, int RW, bool TXT>
 __global__ void __launch_bounds__(256)
 flash_attn_tr_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
                      uint16_t *__restrict__ O, int B, int H, int T, int causal, float c2) {
@@ -344,7 +347,8 @@ flash_attn_tr_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict_
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const long N = long(BH) * T;
-  const uint16_t *Kb = K + long(bh) * T;  // column offset into the [64, N] slab
+  // column offset into the [64, N] slab, or the block's first key row (TXT)
+  const uint16_t *Kb = TXT ? K + long(bh) * T * HD : K + long(bh) * T;
   const uint16_t *Vb = V + long(bh) * T * HD;
   const int wrow0 = q0 + wave * 16 * RW;
 
@@ -373,7 +377,7 @@ flash_attn_tr_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict_
 
   // staging: rows r0 and r0 + 32 of each tile, chunk c0
   const int r0 = tid >> 3, c0 = tid & 7;
-  const int st_k0 = tswz<3>(r0, c0) * 16, st_k1 = tswz<3>(r0 + 32, c0) * 16;
+  const int st_k0 = (TXT ? swz(r0, c0) : tswz<3>(r0, c0)) * 16, st_k1 = (TXT ? swz(r0 + 32, c0) : tswz<3>(r0 + 32, c0)) * 16;
   const int st_v0 = tswz<2>(r0, c0) * 16, st_v1 = tswz<2>(r0 + 32, c0) * 16;
   // transposed reads: this lane addresses row base + (s >> 2), 8 bytes at
   // column 4(s & 3) of a 16-column block; the row swizzle term is lane-fixed
@@ -385,7 +389,8 @@ flash_attn_tr_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict_
   const int ntiles = (kv_end + KB - 1) / KB;
   // loop-carried load pointers (advanced one tile per gload) keep the address
   // registers live, so they are never recycled while a prefetch is in flight
-  const uint16_t *kp0 = Kb + long(r0) * N + c0 * 8, *kp1 = Kb + long(r0 + 32) * N + c0 * 8;
+  const long kld = TXT ? HD : N;  // elements between the rows of a K tile
+  const uint16_t *kp0 = Kb + long(r0) * kld + c0 * 8, *kp1 = Kb + long(r0 + 32) * kld + c0 * 8;
   const uint16_t *vp0 = Vb + long(r0) * HD + c0 * 8, *vp1 = Vb + long(r0 + 32) * HD + c0 * 8;
   uint4 kr[2], vr[2];
   auto gload = [&](int j0) {
@@ -394,6 +399,11 @@ flash_attn_tr_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict_
       kr[1] = *reinterpret_cast<const uint4 *>(kp1);
       vr[0] = *reinterpret_cast<const uint4 *>(vp0);
       vr[1] = *reinterpret_cast<const uint4 *>(vp1);
+    } else if (TXT) {  // ragged last tile: zero the rows past T
+      kr[0] = (j0 + r0 < T) ? *reinterpret_cast<const uint4 *>(kp0) : make_uint4(0, 0, 0, 0);
+      kr[1] = (j0 + r0 + 32 < T) ? *reinterpret_cast<const uint4 *>(kp1) : make_uint4(0, 0, 0, 0);
+      vr[0] = (j0 + r0 < T) ? *reinterpret_cast<const uint4 *>(vp0) : make_uint4(0, 0, 0, 0);
+      vr[1] = (j0 + r0 + 32 < T) ? *reinterpret_cast<const uint4 *>(vp1) : make_uint4(0, 0, 0, 0);
     } else {  // ragged last tile: zero what lies past T
       const bool kin = j0 + c0 * 8 < T;
       kr[0] = kin ? *reinterpret_cast<const uint4 *>(kp0) : make_uint4(0, 0, 0, 0);
@@ -401,8 +411,8 @@ flash_attn_tr_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict_
       vr[0] = (j0 + r0 < T) ? *reinterpret_cast<const uint4 *>(vp0) : make_uint4(0, 0, 0, 0);
       vr[1] = (j0 + r0 + 32 < T) ? *reinterpret_cast<const uint4 *>(vp1) : make_uint4(0, 0, 0, 0);
     }
-    kp0 += KB;
-    kp1 += KB;
+    kp0 += TXT ? KB * HD : KB;
+    kp1 += TXT ? KB * HD : KB;
     vp0 += KB * HD;
     vp1 += KB * HD;
   };
@@ -442,9 +452,13 @@ flash_attn_tr_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict_
       for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
-          const uint8_t *p = kt + rd_k + ((2 * jt) ^ sx) * 16 + ks * 32 * 128;
-          const uint2 lo = lds_tr(p), hi = lds_tr(p + 4 * 128);
-          kf[ks][jt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+          if constexpr (TXT) {
+            kf[ks][jt] = *reinterpret_cast<const uint4 *>(kt + swz(jt * 16 + li, ks * 4 + lg) * 16);
+          } else {
+            const uint8_t *p = kt + rd_k + ((2 * jt) ^ sx) * 16 + ks * 32 * 128;
+            const uint2 lo = lds_tr(p), hi = lds_tr(p + 4 * 128);
+            kf[ks][jt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+          }
         }
       f32x4 s[RW][4];
 #pragma unroll
@@ -554,7 +568,7 @@ flash_attn_tr_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict_
 template <int DT>
 __global__ void __launch_bounds__(64)
 attn_generic_kernel(const void *__restrict__ Qv, const void *__restrict__ Kv, const void *__restrict__ Vv,
-                    void *__restrict__ Ov, int B, int H, int T, int hd, int causal, float scale) {
+                    void *__restrict__ Ov, int B, int H, int T, int hd, int causal, float scale, int textbook) {
   typedef Store<DT> S;
   typedef typename S::T T_;
   extern __shared__ float srow[];  // [T]
@@ -569,7 +583,8 @@ attn_generic_kernel(const void *__restrict__ Qv, const void *__restrict__ Kv, co
   float mx = -INFINITY;
   for (int j = lane; j < jend; j += 64) {
     float acc = 0.f;
-    for (int d = 0; d < hd; ++d) acc += S::dec(Q[qrow + d]) * S::dec(K[long(d) * N + long(bh) * T + j]);
+    const long kj = textbook ? (long(bh) * T + j) * hd : long(bh) * T + j, kd = textbook ? 1 : N;
+    for (int d = 0; d < hd; ++d) acc += S::dec(Q[qrow + d]) * S::dec(K[kj + long(d) * kd]);
     const float v = S::round(S::round(acc) * scale);
     srow[j] = v;
     mx = fmaxf(mx, v);
@@ -606,11 +621,22 @@ int tr_rows_env() {
 }  // namespace
 
 hipError_t attention(int dt, const void *q, const void *k, const void *v, void *ctx, int B, int H, int T, int hd,
-                     int causal, float scale, int force_generic, hipStream_t st) {
+                     int causal, float scale, int force_generic, hipStream_t st, int textbook) {
   if (B <= 0 || H <= 0 || T <= 0) return hipSuccess;
   const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)k % 16 == 0) && ((uintptr_t)v % 16 == 0) &&
                        ((uintptr_t)ctx % 8 == 0);
-  if (!force_generic && hd == HD && (dt == BF16 || dt == F16) && aligned && T % 8 == 0 && pow2(scale)) {
+  if (textbook && !force_generic && hd == HD && (dt == BF16 || dt == F16) && aligned && pow2(scale)) {
+    // textbook keys: rows of K like V, so any T (ragged tiles are row-masked)
+    const int bh = B * H;
+    const dim3 grid(unsigned(long((T + 63) / 64) * bh));
+    const float c2 = scale * 1.4426950408889634f;
+    const uint16_t *Q = (const uint16_t *)q, *K = (const uint16_t *)k, *V = (const uint16_t *)v;
+    uint16_t *O = (uint16_t *)ctx;
+    if (dt == BF16) hipLaunchKernelGGL((flash_attn_tr_kernel<BF16, 1, true>), grid, dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2);
+    else hipLaunchKernelGGL((flash_attn_tr_kernel<F16, 1, true>), grid, dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2);
+    return hipGetLastError();
+  }
+  if (!textbook && !force_generic && hd == HD && (dt == BF16 || dt == F16) && aligned && T % 8 == 0 && pow2(scale)) {
     const int bh = B * H;
     static const int forced = tr_rows_env();
     // 16 query rows per wave: more resident waves hide the softmax latency
@@ -622,15 +648,15 @@ hipError_t attention(int dt, const void *q, const void *k, const void *v, void *
     const uint16_t *Q = (const uint16_t *)q, *K = (const uint16_t *)k, *V = (const uint16_t *)v;
     uint16_t *O = (uint16_t *)ctx;
     if (dt == BF16) {
-      if (rw == 2) hipLaunchKernelGGL((flash_attn_tr_kernel<BF16, 2>), grid, dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2);
-      else hipLaunchKernelGGL((flash_attn_tr_kernel<BF16, 1>), grid, dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2);
+      if (rw == 2) hipLaunchKernelGGL((flash_attn_tr_kernel<BF16, 2, false>), grid, dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2);
+      else hipLaunchKernelGGL((flash_attn_tr_kernel<BF16, 1, false>), grid, dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2);
     } else {
-      if (rw == 2) hipLaunchKernelGGL((flash_attn_tr_kernel<F16, 2>), grid, dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2);
-      else hipLaunchKernelGGL((flash_attn_tr_kernel<F16, 1>), grid, dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2);
+      if (rw == 2) hipLaunchKernelGGL((flash_attn_tr_kernel<F16, 2, false>), grid, dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2);
+      else hipLaunchKernelGGL((flash_attn_tr_kernel<F16, 1, false>), grid, dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2);
     }
     return hipGetLastError();
   }
-  if (!force_generic && hd == HD && (dt == BF16 || dt == F16) && aligned) {
+  if (!textbook && !force_generic && hd == HD && (dt == BF16 || dt == F16) && aligned) {
     const int bh = B * H;
     // 128-row blocks when that still fills the chip, else 64-row blocks
     const int rw = (long((T + 127) / 128) * bh >= 512) ? 2 : 1;
@@ -651,9 +677,9 @@ hipError_t attention(int dt, const void *q, const void *k, const void *v, void *
   dim3 grid(T, B * H);
   const size_t lds = size_t(T) * 4;
   switch (dt) {
-  case F32: hipLaunchKernelGGL(attn_generic_kernel<F32>, grid, dim3(64), lds, st, q, k, v, ctx, B, H, T, hd, causal, scale); break;
-  case F16: hipLaunchKernelGGL(attn_generic_kernel<F16>, grid, dim3(64), lds, st, q, k, v, ctx, B, H, T, hd, causal, scale); break;
-  case BF16: hipLaunchKernelGGL(attn_generic_kernel<BF16>, grid, dim3(64), lds, st, q, k, v, ctx, B, H, T, hd, causal, scale); break;
+  case F32: hipLaunchKernelGGL(attn_generic_kernel<F32>, grid, dim3(64), lds, st, q, k, v, ctx, B, H, T, hd, causal, scale, textbook); break;
+  case F16: hipLaunchKernelGGL(attn_generic_kernel<F16>, grid, dim3(64), lds, st, q, k, v, ctx, B, H, T, hd, causal, scale, textbook); break;
+  case BF16: hipLaunchKernelGGL(attn_generic_kernel<BF16>, grid, dim3(64), lds, st, q, k, v, ctx, B, H, T, hd, causal, scale, textbook); break;
   default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

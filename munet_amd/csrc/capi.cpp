@@ -521,6 +521,18 @@ int mh_attention(int dt, const void *q, const void *k, const void *v, void *ctx,
   })
 }
 
+int mh_attention_textbook(int dt, const void *q, const void *k, const void *v, void *ctx, int B, int H, int T, int hd,
+                          int causal, void *stream) {
+  MH_TRY({
+    check_dt(dt);
+    if (hd <= 0) throw Error("attention: head_dim must be positive");
+    if (size_t(T) * 4 > 64 * 1024 && !(hd == 64 && dt != MH_F32))
+      throw Error("attention: sequence too long for the generic kernel");
+    const float scale = host_round(dt, 1.0f / std::sqrt(float(hd)));
+    hip_check(attention(dt, q, k, v, ctx, B, H, T, hd, causal, scale, 0, S_(stream), 1), "attention_textbook");
+  })
+}
+
 // ---- shape -------------------------------------------------------------------
 int mh_concat(int dt, const void *const *inputs, int count, void *out, int dim, int ndim, const int *shapes,
               void *stream) {

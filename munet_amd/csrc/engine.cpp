@@ -133,6 +133,14 @@ struct EngineImpl {
   size_t shared_wbytes = 0;
   // pinned host staging for the PCIe path (allocated on first use)
   void *pin_in = nullptr, *pin_out = nullptr;
+  // attention with textbook keys (DecoderLM "attention": "textbook")
+  bool textbook_attn = false;
+  // KV-cache prefill: every attention op also copies its k and v into the
+  // caches of a decoder (attention layer i at kv_k / kv_v + i * kv_layer_bytes,
+  // [B, H, kv_Lmax, hd] each); set before compile
+  char *kv_k = nullptr, *kv_v = nullptr;
+  size_t kv_layer_bytes = 0;
+  int kv_Lmax = 0, attn_layers = 0;
 
   std::vector<Val> vals;
   std::vector<Op> ops;
@@ -481,6 +489,8 @@ struct EngineImpl {
     const int ctx = new_val({B, T, E}, dt);
     Op &a = emit(OP_ATTN, pfx + "attention", {q, k, v}, {ctx});
     a.a[0] = B; a.a[1] = H; a.a[2] = T; a.a[3] = hd; a.a[4] = causal ? 1 : 0;
+    a.a[5] = textbook_attn ? 1 : 0;
+    a.a[6] = attn_layers++;
     a.f = host_round(dt, 1.0f / std::sqrt(float(hd)));
     return linear(ctx, pfx + "out_proj.", E, E, true, ACT_NONE, resid);
   }
@@ -561,6 +571,9 @@ struct EngineImpl {
     if (t == "DecoderLM") {
       const Shape xs = vals[x].shape;
       const int V = m.at("vocab").as_int(), C = m.at("ctx").as_int(), d = m.at("d_model").as_int();
+      const std::string attn = m.get_str("attention", "munet");
+      if (attn != "munet" && attn != "textbook") throw Error("DecoderLM: attention must be \"munet\" or \"textbook\"");
+      textbook_attn = attn == "textbook";
       if (vals[x].dt != I32 || xs.size() != 2) throw Error("DecoderLM: expects int32 [B,T] ids");
       if (xs[1] > C) throw Error("DecoderLM: sequence longer than the position table");
       // token + position gathers and their add, one rounding
@@ -727,8 +740,12 @@ struct EngineImpl {
     }
     case OP_ATTN:
       hip_check(attention(dt, dptr(o.in[0]), dptr(o.in[1]), dptr(o.in[2]), dptr(o.out[0]), int(o.a[0]), int(o.a[1]),
-                          int(o.a[2]), int(o.a[3]), int(o.a[4]), o.f, 0, st),
+                          int(o.a[2]), int(o.a[3]), int(o.a[4]), o.f, 0, st, int(o.a[5])),
                 o.name.c_str());
+      if (kv_k)
+        hip_check(kv_store(dt, dptr(o.in[1]), dptr(o.in[2]), kv_k + o.a[6] * kv_layer_bytes,
+                           kv_v + o.a[6] * kv_layer_bytes, int(o.a[0] * o.a[1]), int(o.a[2]), int(o.a[3]), kv_Lmax, st),
+                  (o.name + ".kv_store").c_str());
       break;
     case OP_LN:
       hip_check(layernorm(dt, dptr(o.in[0]), wptr(o.w), wptr(o.b), dptr(o.out[0]), int(o.a[0]), int(o.a[1]), o.f, st),
@@ -810,6 +827,7 @@ struct EngineImpl {
     in_shape = ishape;
     vals.clear();
     ops.clear();
+    attn_layers = 0;
     wbytes = 0;
     wpending.clear();
     const std::string t = cfg.at("type").as_str();
@@ -1333,6 +1351,303 @@ struct mh_engine {
   }
 };
 
+// Greedy autoregressive decode with a KV cache over a compiled DecoderLM
+// whose attention uses textbook keys (no counterpart in the reference; its
+// attention's keys are not per position, see decode.hip).  The prefill is the
+// engine's own forward for [B, T0] (one compiled instance per T0) with each
+// attention op also storing its k and v into the caches; each decode step is
+// one captured graph of weight-streaming kernels (decode.hip) that feeds B
+// tokens at the device-resident position and writes the B greedy choices
+// back as the next step's input.
+struct mh_decoder {
+  mh_engine *eng = nullptr;
+  int dt = mh::BF16, B = 0, Lmax = 0, L = 0, d = 0, H = 0, hd = 0, ffn = 0, V = 0, C = 0, nsplit = 0;
+  float eps = 1e-5f;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  char *wbuf = nullptr, *buf = nullptr, *cache = nullptr;
+  size_t wbytes = 0, bufbytes = 0, cache_bytes = 0, layer_bytes = 0;
+  struct LayerW {
+    const void *ln1w, *ln1b, *wqkv, *bqkv, *wo, *bo, *ln2w, *ln2b, *w1, *b1, *w2, *b2;
+  };
+  std::vector<LayerW> lw;
+  const void *tok = nullptr, *pos_tab = nullptr, *lnfw = nullptr, *lnfb = nullptr, *whead = nullptr, *bhead = nullptr;
+  void *x = nullptr, *x1 = nullptr, *q = nullptr, *ctx = nullptr, *h = nullptr, *logits = nullptr;
+  int32_t *ids = nullptr, *tokens = nullptr;
+  int *state = nullptr, *counters = nullptr;
+  float *scores = nullptr, *opart = nullptr;
+  float2 *stats = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  std::map<int, std::unique_ptr<mh::EngineImpl>> prefills;  // by prompt length
+  int pos = -1;  // host copy of state[0]; -1 before the first prefill
+  double last_step_ms = 0, last_generate_ms = 0, last_prefill_ms = 0;
+  size_t steps = 0;
+
+  ~mh_decoder() {
+    prefills.clear();
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    if (wbuf) (void)hipFree(wbuf);
+    if (buf) (void)hipFree(buf);
+    if (cache) (void)hipFree(cache);
+    if (ev0) (void)hipEventDestroy(ev0);
+    if (ev1) (void)hipEventDestroy(ev1);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+
+  void create(mh_engine *e, int batch, int max_len) {
+    using mh::Error;
+    using mh::hip_check;
+    eng = e;
+    mh::EngineImpl &pi = e->impl;
+    if (!pi.compiled || pi.plan_only) throw Error("decoder: the engine must be compiled on a device first");
+    const mh::json::Value &m = pi.cfg;
+    if (m.at("type").as_str() != "DecoderLM") throw Error("decoder: the model must be a DecoderLM");
+    if (m.get_str("attention", "munet") != "textbook")
+      throw Error("decoder: the DecoderLM must use \"attention\": \"textbook\" (MuNet's attention has no per-position keys to cache)");
+    dt = pi.dt;
+    const size_t es = mh::dt_size(dt), ce = 16 / es;
+    V = m.at("vocab").as_int(); C = m.at("ctx").as_int(); d = m.at("d_model").as_int();
+    L = m.at("num_layers").as_int(); H = m.at("num_heads").as_int(); ffn = m.at("ffn").as_int();
+    eps = float(m.get_num("eps", 1e-5));
+    hd = d / H;
+    if (batch < 1 || batch > 16) throw Error("decoder: batch must be in 1..16");
+    if (max_len < 1 || max_len > C) throw Error("decoder: max_len must be in 1..ctx");
+    if (d % H || hd > 64 || hd % 4 || hd % int(ce) || d % int(ce) || ffn % int(ce))
+      throw Error("decoder: d_model, ffn and head_dim must be multiples of 16 bytes, head_dim <= 64");
+    if (size_t(batch) * std::max(d, ffn) * es > 65536) throw Error("decoder: batch x width exceeds the 64 KiB row stage");
+    B = batch;
+    Lmax = max_len;
+    nsplit = (Lmax + 255) / 256;
+
+    // weights, packed as the decode kernels read them ([out, in] rows)
+    mh::EngineImpl pk;
+    pk.plan_only = true;
+    pk.pp = &pi.params;
+    pk.dt = dt;
+    std::vector<std::pair<std::vector<uint8_t>, const void **>> up;
+    auto add = [&](std::vector<uint8_t> b, const void **dst) { up.emplace_back(std::move(b), dst); };
+    auto vec = [&](const std::string &n, size_t cnt) { return pk.param(n, cnt).host; };
+    auto bias = [&](const std::string &n, size_t cnt) {
+      return pi.params.count(n) ? vec(n, cnt) : std::vector<uint8_t>(cnt * es, 0);
+    };
+    lw.resize(L);
+    for (int i = 0; i < L; ++i) {
+      const std::string p = "blocks." + std::to_string(i) + ".";
+      LayerW &w = lw[i];
+      add(vec(p + "ln1.weight", d), &w.ln1w);
+      add(vec(p + "ln1.bias", d), &w.ln1b);
+      std::vector<uint8_t> wq, bq;
+      for (const char *n : {"q_proj.", "k_proj.", "v_proj."}) {
+        auto t = pk.pack_linear(pk.param(p + "attn." + n + "weight"), d, d);
+        wq.insert(wq.end(), t.begin(), t.end());
+        auto b = vec(p + "attn." + n + "bias", d);
+        bq.insert(bq.end(), b.begin(), b.end());
+      }
+      add(std::move(wq), &w.wqkv);
+      add(std::move(bq), &w.bqkv);
+      add(pk.pack_linear(pk.param(p + "attn.out_proj.weight"), d, d), &w.wo);
+      add(vec(p + "attn.out_proj.bias", d), &w.bo);
+      add(vec(p + "ln2.weight", d), &w.ln2w);
+      add(vec(p + "ln2.bias", d), &w.ln2b);
+      add(pk.pack_linear(pk.param(p + "ff.0.weight"), d, ffn), &w.w1);
+      add(bias(p + "ff.0.bias", ffn), &w.b1);
+      add(pk.pack_linear(pk.param(p + "ff.2.weight"), ffn, d), &w.w2);
+      add(bias(p + "ff.2.bias", d), &w.b2);
+    }
+    add(vec("token_embed.weight", size_t(V) * d), &tok);
+    add(vec("pos_embed.weight", size_t(C) * d), &pos_tab);
+    add(vec("ln_f.weight", d), &lnfw);
+    add(vec("ln_f.bias", d), &lnfb);
+    add(pk.pack_linear(pk.param("head.weight"), d, V), &whead);
+    add(bias("head.bias", V), &bhead);
+    std::vector<size_t> offs;
+    for (auto &u : up) {
+      offs.push_back(wbytes);
+      wbytes += (u.first.size() + 255) & ~size_t(255);
+    }
+    hip_check(hipSetDevice(pi.device), "hipSetDevice");
+    hip_check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
+    hip_check(hipEventCreate(&ev0), "hipEventCreate");
+    hip_check(hipEventCreate(&ev1), "hipEventCreate");
+    hip_check(hipMalloc(&wbuf, wbytes), "hipMalloc(decoder weights)");
+    for (size_t i = 0; i < up.size(); ++i) {
+      hip_check(hipMemcpy(wbuf + offs[i], up[i].first.data(), up[i].first.size(), hipMemcpyHostToDevice),
+                "upload decoder weights");
+      *up[i].second = wbuf + offs[i];
+    }
+
+    // activations, scratch and the caches ([layer][b][h][Lmax][hd], K then V)
+    size_t off = 0;
+    auto carve = [&](size_t bytes) { const size_t o = off; off += (bytes + 255) & ~size_t(255); return o; };
+    const size_t o_x = carve(size_t(B) * d * es), o_x1 = carve(size_t(B) * d * es), o_q = carve(size_t(B) * d * es),
+                 o_ctx = carve(size_t(B) * d * es), o_h = carve(size_t(B) * ffn * es),
+                 o_lg = carve(size_t(B) * V * es), o_ids = carve(size_t(B) * 4), o_tok = carve(size_t(Lmax) * B * 4),
+                 o_st = carve(16), o_cnt = carve(size_t(B) * H * 4), o_sc = carve(size_t(B) * H * Lmax * 4),
+                 o_stats = carve(size_t(B) * H * nsplit * 8), o_op = carve(size_t(B) * H * nsplit * hd * 4);
+    bufbytes = off;
+    hip_check(hipMalloc(&buf, bufbytes), "hipMalloc(decoder buffers)");
+    hip_check(hipMemset(buf, 0, bufbytes), "hipMemset(decoder buffers)");
+    x = buf + o_x; x1 = buf + o_x1; q = buf + o_q; ctx = buf + o_ctx; h = buf + o_h; logits = buf + o_lg;
+    ids = reinterpret_cast<int32_t *>(buf + o_ids);
+    tokens = reinterpret_cast<int32_t *>(buf + o_tok);
+    state = reinterpret_cast<int *>(buf + o_st);
+    counters = reinterpret_cast<int *>(buf + o_cnt);
+    scores = reinterpret_cast<float *>(buf + o_sc);
+    stats = reinterpret_cast<float2 *>(buf + o_stats);
+    opart = reinterpret_cast<float *>(buf + o_op);
+    layer_bytes = size_t(B) * H * Lmax * hd * es;
+    cache_bytes = 2 * size_t(L) * layer_bytes;
+    hip_check(hipMalloc(&cache, cache_bytes), "hipMalloc(KV cache)");
+    hip_check(hipMemset(cache, 0, cache_bytes), "hipMemset(KV cache)");
+
+    // the step graph
+    hip_check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    try {
+      enqueue_step();
+    } catch (...) {
+      hipGraph_t g = nullptr;
+      (void)hipStreamEndCapture(stream, &g);
+      if (g) (void)hipGraphDestroy(g);
+      throw;
+    }
+    hip_check(hipStreamEndCapture(stream, &graph), "hipStreamEndCapture");
+    hip_check(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+  }
+
+  char *kcache(int l) const { return cache + size_t(l) * layer_bytes; }
+  char *vcache(int l) const { return cache + (size_t(L) + l) * layer_bytes; }
+
+  void enqueue_step() {
+    using mh::hip_check;
+    const float gelu_c = mh::host_round(dt, 1.702f), scale = mh::host_round(dt, 1.0f / std::sqrt(float(hd)));
+    hip_check(mh::dec_embed(dt, ids, tok, pos_tab, state, x, B, V, d, mh::device_error_flag(), stream), "decode embed");
+    for (int l = 0; l < L; ++l) {
+      const LayerW &w = lw[l];
+      hip_check(mh::dec_linear(dt, 0, x, w.wqkv, w.bqkv, w.ln1w, w.ln1b, eps, nullptr, q, kcache(l), vcache(l), state,
+                               B, 3 * d, d, d, H, hd, Lmax, gelu_c, stream),
+                "decode ln1 + qkv");
+      hip_check(mh::dec_attention(dt, q, kcache(l), vcache(l), state, scores, stats, opart, counters, ctx, B, H, hd,
+                                  Lmax, scale, stream),
+                "decode attention");
+      hip_check(mh::dec_linear(dt, 1, ctx, w.wo, w.bo, nullptr, nullptr, eps, x, x1, nullptr, nullptr, state, B, d, d,
+                               d, H, hd, Lmax, gelu_c, stream),
+                "decode out_proj");
+      hip_check(mh::dec_linear(dt, 2, x1, w.w1, w.b1, w.ln2w, w.ln2b, eps, nullptr, h, nullptr, nullptr, state, B, ffn,
+                               d, d, H, hd, Lmax, gelu_c, stream),
+                "decode ln2 + ff.0 + gelu");
+      hip_check(mh::dec_linear(dt, 1, h, w.w2, w.b2, nullptr, nullptr, eps, x1, x, nullptr, nullptr, state, B, d, ffn,
+                               d, H, hd, Lmax, gelu_c, stream),
+                "decode ff.2");
+    }
+    hip_check(mh::dec_linear(dt, 3, x, whead, bhead, lnfw, lnfb, eps, nullptr, logits, nullptr, nullptr, state, B, V,
+                             d, d, H, hd, Lmax, gelu_c, stream),
+              "decode ln_f + head");
+    hip_check(mh::dec_argmax(dt, logits, ids, tokens, state, B, V, Lmax, stream), "decode argmax");
+  }
+
+  // Prompt ids [B, T0] through the engine's forward (textbook attention), the
+  // caches filled for positions 0..T0-1; logits_out [B, T0, V] optional.
+  void prefill(const int32_t *hids, int T0, void *logits_out) {
+    using mh::Error;
+    using mh::hip_check;
+    if (T0 < 1 || T0 > Lmax) throw Error("decoder: prompt length must be in 1..max_len");
+    auto it = prefills.find(T0);
+    if (it == prefills.end()) {
+      auto inst = std::make_unique<mh::EngineImpl>();
+      const mh::EngineImpl &pi = eng->impl;
+      inst->cfg = pi.cfg;
+      inst->dt = pi.dt;
+      inst->device = pi.device;
+      inst->pp = &pi.params;
+      inst->shared_wbuf = pi.wbuf;
+      inst->shared_wbytes = pi.wbytes;
+      inst->kv_k = cache;
+      inst->kv_v = cache + size_t(L) * layer_bytes;
+      inst->kv_layer_bytes = layer_bytes;
+      inst->kv_Lmax = Lmax;
+      inst->compile(mh::Shape{B, T0});
+      it = prefills.emplace(T0, std::move(inst)).first;
+    }
+    mh::EngineImpl &e = *it->second;
+    const auto t0 = std::chrono::steady_clock::now();
+    e.stage_input(hids);
+    e.run_device();
+    const size_t es = mh::dt_size(dt);
+    const char *out = static_cast<const char *>(e.dptr(e.output));
+    if (logits_out)
+      hip_check(hipMemcpyAsync(logits_out, out, size_t(B) * T0 * V * es, hipMemcpyDeviceToHost, e.stream), "logits D2H");
+    // the next input: each sequence's greedy choice at its last position
+    for (int b = 0; b < B; ++b)
+      hip_check(mh::argmax_rows(dt, out + (size_t(b) * T0 + T0 - 1) * V * es, ids + b, 1, V, e.stream), "prefill argmax");
+    const int st[2] = {T0, 0};
+    hip_check(hipMemcpyAsync(state, st, sizeof(st), hipMemcpyHostToDevice, e.stream), "decoder state");
+    hip_check(hipStreamSynchronize(e.stream), "prefill");
+    e.check_error_flag();
+    pos = T0;
+    last_prefill_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  }
+
+  void require_room(int n) const {
+    if (pos < 0) throw mh::Error("decoder: prefill first");
+    if (pos + n > Lmax) throw mh::Error("decoder: position past max_len");
+  }
+
+  // One step at position pos: hids [B] (nullptr: the previous greedy
+  // choice); logits_out [B, V] and next_ids [B] optional.
+  void step(const int32_t *hids, void *logits_out, int32_t *next_ids) {
+    using mh::hip_check;
+    require_room(1);
+    if (hids) hip_check(hipMemcpyAsync(ids, hids, size_t(B) * 4, hipMemcpyHostToDevice, stream), "decoder ids H2D");
+    hip_check(hipEventRecord(ev0, stream), "hipEventRecord");
+    hip_check(hipGraphLaunch(exec, stream), "hipGraphLaunch");
+    hip_check(hipEventRecord(ev1, stream), "hipEventRecord");
+    if (logits_out)
+      hip_check(hipMemcpyAsync(logits_out, logits, size_t(B) * V * mh::dt_size(dt), hipMemcpyDeviceToHost, stream),
+                "logits D2H");
+    if (next_ids) hip_check(hipMemcpyAsync(next_ids, ids, size_t(B) * 4, hipMemcpyDeviceToHost, stream), "ids D2H");
+    hip_check(hipStreamSynchronize(stream), "decode step");
+    float ms = 0.f;
+    hip_check(hipEventElapsedTime(&ms, ev0, ev1), "hipEventElapsedTime");
+    last_step_ms = ms;
+    ++pos;
+    ++steps;
+    eng->impl.check_error_flag();
+  }
+
+  // n greedy steps back to back; tokens_out [n, B].
+  void generate(int n, int32_t *tokens_out) {
+    using mh::hip_check;
+    if (n < 1) throw mh::Error("decoder: n must be positive");
+    require_room(n);
+    const int zero = 0;
+    hip_check(hipMemcpyAsync(state + 1, &zero, sizeof(int), hipMemcpyHostToDevice, stream), "decoder state");
+    hip_check(hipEventRecord(ev0, stream), "hipEventRecord");
+    for (int i = 0; i < n; ++i) hip_check(hipGraphLaunch(exec, stream), "hipGraphLaunch");
+    hip_check(hipEventRecord(ev1, stream), "hipEventRecord");
+    if (tokens_out)
+      hip_check(hipMemcpyAsync(tokens_out, tokens, size_t(n) * B * 4, hipMemcpyDeviceToHost, stream), "tokens D2H");
+    hip_check(hipStreamSynchronize(stream), "generate");
+    float ms = 0.f;
+    hip_check(hipEventElapsedTime(&ms, ev0, ev1), "hipEventElapsedTime");
+    last_generate_ms = ms;
+    pos += n;
+    steps += size_t(n);
+    eng->impl.check_error_flag();
+  }
+
+  std::string stats_json() const {
+    std::ostringstream s;
+    s << "{\"batch\":" << B << ",\"max_len\":" << Lmax << ",\"position\":" << pos << ",\"steps\":" << steps
+      << ",\"weight_bytes\":" << wbytes << ",\"cache_bytes\":" << cache_bytes << ",\"buffer_bytes\":" << bufbytes
+      << ",\"kernels_per_step\":" << (3 + 6 * L) << ",\"last_step_ms\":" << last_step_ms
+      << ",\"last_generate_ms\":" << last_generate_ms << ",\"last_prefill_ms\":" << last_prefill_ms
+      << ",\"prefill_instances\":" << prefills.size() << "}";
+    return s.str();
+  }
+};
+
 using mh::Error;
 
 #define ENG_TRY(...)                   \
@@ -1559,6 +1874,31 @@ int mh_engine_op_times(mh_engine *e, int reps, const char *only, char *buf, size
 
 int mh_engine_forward_op_times(mh_engine *e, int reps, char *buf, size_t len) {
   ENG_TRY(put_str(e->impl.forward_op_times_json(reps), buf, len))
+}
+
+// ---- KV-cache decode -----------------------------------------------------------
+int mh_decoder_create(mh_decoder **d, mh_engine *e, int batch, int max_len) {
+  if (!d || !e) {
+    mh::set_last_error("null handle");
+    return 1;
+  }
+  *d = nullptr;
+  auto dec = std::make_unique<mh_decoder>();
+  ENG_TRY(dec->create(e, batch, max_len); *d = dec.release())
+}
+int mh_decoder_destroy(mh_decoder *d) { ENG_TRY(delete d) }
+int mh_decoder_prefill(mh_decoder *d, const int32_t *ids, int T0, void *logits_out) {
+  ENG_TRY(if (!d || !ids) throw Error("null argument"); d->prefill(ids, T0, logits_out))
+}
+int mh_decoder_step(mh_decoder *d, const int32_t *ids, void *logits_out, int32_t *next_ids) {
+  ENG_TRY(if (!d) throw Error("null handle"); d->step(ids, logits_out, next_ids))
+}
+int mh_decoder_generate(mh_decoder *d, int n, int32_t *tokens_out, float *gpu_ms) {
+  ENG_TRY(if (!d) throw Error("null handle"); d->generate(n, tokens_out); if (gpu_ms) *gpu_ms = float(d->last_generate_ms))
+}
+int mh_decoder_position(mh_decoder *d, int *pos) { ENG_TRY(if (!d || !pos) throw Error("null argument"); *pos = d->pos) }
+int mh_decoder_stats(mh_decoder *d, char *buf, size_t len) {
+  ENG_TRY(if (!d) throw Error("null handle"); put_str(d->stats_json(), buf, len))
 }
 
 

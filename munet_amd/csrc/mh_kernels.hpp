@@ -120,8 +120,28 @@ hipError_t conv_nhwc(int dt, const void *x, const void *w_ohwi, const ConvArgs &
                      int tile_hint, hipStream_t st);
 
 // Fused attention core (q, k, v in the head-split [B*H, T, hd] layout).
+// textbook = 0: MuNet's scores, k's buffer read as a [hd, B*H*T] matrix;
+// textbook = 1: key j of a head is row j of its k (the decode attention).
 hipError_t attention(int dt, const void *q, const void *k, const void *v, void *ctx, int B, int H, int T, int hd,
-                     int causal, float scale, int force_generic, hipStream_t st);
+                     int causal, float scale, int force_generic, hipStream_t st, int textbook = 0);
+
+// KV-cache decode (decode.hip).  state: device ints {pos, step}.
+hipError_t dec_embed(int dt, const int32_t *ids, const void *tok, const void *pos_tab, const int *state, void *out,
+                     int B, int V, int D, int *err, hipStream_t st);
+// kind 0: LayerNorm + q/k/v (k, v into the caches at pos); 1: + residual;
+// 2: LayerNorm + GELU; 3: LayerNorm (the head).  M <= 16 rows.
+hipError_t dec_linear(int dt, int kind, const void *x, const void *w, const void *bias, const void *ln_w,
+                      const void *ln_b, float eps, const void *resid, void *out, void *kc, void *vc, const int *state,
+                      int M, int N, int K, int E, int H, int hd, int Lmax, float gelu_c, hipStream_t st);
+// scratch: scores [B*H, Lmax], stats / opart per (head, 256-key block),
+// counters [B*H] (zero before the first call; every call leaves them zero)
+hipError_t dec_attention(int dt, const void *q, const void *kc, const void *vc, const int *state, float *scores,
+                         float2 *stats, float *opart, int *counters, void *ctx, int B, int H, int hd, int Lmax,
+                         float scale, hipStream_t st);
+hipError_t dec_argmax(int dt, const void *logits, int32_t *ids, int32_t *tokens, int *state, int B, int V, int cap,
+                      hipStream_t st);
+hipError_t kv_store(int dt, const void *k, const void *v, void *kc, void *vc, int BH, int T, int hd, int Lmax,
+                    hipStream_t st);
 
 hipError_t binary(int dt, int op, const void *a, const void *b, void *out, const BcastArgs &g, hipStream_t st);
 hipError_t unary(int dt, int op, const void *in, void *out, size_t n, float c, hipStream_t st);

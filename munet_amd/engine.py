@@ -245,3 +245,73 @@ class Engine:
             self.close()
         except Exception:
             pass
+
+
+class Decoder:
+    """Greedy autoregressive decode with a KV cache over a compiled DecoderLM
+    engine whose config has ``"attention": "textbook"`` (mh_decoder_*; no
+    counterpart in the reference, whose attention has no per-position keys).
+
+    ``prefill(ids [B, T0])`` runs the engine's forward and fills the caches;
+    ``step(ids [B] or None)`` feeds one token per sequence; ``generate(n)``
+    runs n greedy steps back to back on the device."""
+
+    def __init__(self, engine: Engine, batch: int, max_len: int):
+        self.engine = engine
+        self.batch = int(batch)
+        self.max_len = int(max_len)
+        self.vocab = int(engine.config["vocab"])
+        h = _vp()
+        _lib.call("mh_decoder_create", ctypes.byref(h), engine._h, self.batch, self.max_len)
+        self._h = h
+
+    def _dt(self):
+        return synth.storage_dtype(synth.DTYPE_CODES[self.engine.config.get("dtype", "float32")])
+
+    def prefill(self, ids: np.ndarray, logits: bool = True):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        if ids.ndim != 2 or ids.shape[0] != self.batch:
+            raise ValueError(f"prompt must be [batch={self.batch}, T0] int32")
+        out = np.empty((self.batch, ids.shape[1], self.vocab), dtype=self._dt()) if logits else None
+        _lib.call("mh_decoder_prefill", self._h, ids.ctypes.data_as(_vp), ids.shape[1],
+                  out.ctypes.data_as(_vp) if out is not None else None)
+        return out
+
+    def step(self, ids=None):
+        """-> (logits [B, V], next greedy ids [B])."""
+        src = None
+        if ids is not None:
+            ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(self.batch)
+            src = ids.ctypes.data_as(_vp)
+        logits = np.empty((self.batch, self.vocab), dtype=self._dt())
+        nxt = np.empty(self.batch, dtype=np.int32)
+        _lib.call("mh_decoder_step", self._h, src, logits.ctypes.data_as(_vp), nxt.ctypes.data_as(_vp))
+        return logits, nxt
+
+    def generate(self, n: int):
+        """-> (tokens [n, B], device ms of the n steps)."""
+        toks = np.empty((int(n), self.batch), dtype=np.int32)
+        ms = ctypes.c_float()
+        _lib.call("mh_decoder_generate", self._h, int(n), toks.ctypes.data_as(_vp), ctypes.byref(ms))
+        return toks, float(ms.value)
+
+    def position(self) -> int:
+        p = ctypes.c_int()
+        _lib.call("mh_decoder_position", self._h, ctypes.byref(p))
+        return p.value
+
+    def stats(self) -> dict:
+        buf = ctypes.create_string_buffer(1 << 12)
+        _lib.call("mh_decoder_stats", self._h, buf, len(buf))
+        return json.loads(buf.value.decode())
+
+    def close(self):
+        if self._h is not None:
+            _lib.call("mh_decoder_destroy", self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -63,10 +63,15 @@ def block_config(d_model=512, num_heads=8, ffn=2048, causal=False, dtype="bfloat
 
 
 def decoder_config(vocab=32000, ctx=1024, d_model=768, num_heads=12, num_layers=12,
-                   ffn=3072, dtype="bfloat16", eps=1e-5):
-    return {"type": "DecoderLM", "dtype": dtype, "vocab": vocab, "ctx": ctx,
-            "d_model": d_model, "num_heads": num_heads, "num_layers": num_layers,
-            "ffn": ffn, "eps": eps}
+                   ffn=3072, dtype="bfloat16", eps=1e-5, attention="munet"):
+    """attention: "munet" (the reference's key reading) or "textbook"
+    (per-position keys: the attention the KV-cache decoder runs)."""
+    cfg = {"type": "DecoderLM", "dtype": dtype, "vocab": vocab, "ctx": ctx,
+           "d_model": d_model, "num_heads": num_heads, "num_layers": num_layers,
+           "ffn": ffn, "eps": eps}
+    if attention != "munet":
+        cfg["attention"] = attention
+    return cfg
 
 
 def unet_config(dtype="float16", in_channels=3, channels=(64, 128, 256, 512), out_channels=2):

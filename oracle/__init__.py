@@ -189,13 +189,16 @@ class CpuOracle:
         y = self.matmul(x, w, dt)
         return y if b is None else self.add(y, b, dt)
 
-    def mha(self, x, p, heads, causal, dt, prefix=""):
+    def mha(self, x, p, heads, causal, dt, prefix="", textbook=False):
         """nn::MultiHeadAttention forward on x [B,T,E]; p holds
-        ``<prefix>{q,k,v,out}_proj.{weight,bias}``."""
+        ``<prefix>{q,k,v,out}_proj.{weight,bias}``.  textbook: the attention
+        core reads key j as position j's own key (mha_core)."""
         x = self._c(x, dt)
         B, T, E = x.shape
         g = lambda n: self._c(p[prefix + n], dt)
         if self.which == "reference":
+            if textbook:
+                raise ValueError("MuNet has no textbook-key attention")
             out = np.empty_like(x)
             self._call("mha", _i(dt), _ptr(x), _i(B), _i(T), _i(E), _i(heads), _i(int(causal)),
                        _ptr(g("q_proj.weight")), _ptr(g("q_proj.bias")),
@@ -207,15 +210,19 @@ class CpuOracle:
         q = self.linear(x2, g("q_proj.weight"), g("q_proj.bias"), dt)
         k = self.linear(x2, g("k_proj.weight"), g("k_proj.bias"), dt)
         v = self.linear(x2, g("v_proj.weight"), g("v_proj.bias"), dt)
-        ctx = self.mha_core(q, k, v, B, T, heads, causal, dt)
+        ctx = self.mha_core(q, k, v, B, T, heads, causal, dt, textbook=textbook)
         return self.linear(ctx, g("out_proj.weight"), g("out_proj.bias"), dt).reshape(B, T, E)
 
-    def mha_core(self, q2d, k2d, v2d, B, T, heads, causal, dt):
-        """Restatement only: projected q/k/v [B*T,E] -> merged context [B*T,E]."""
+    def mha_core(self, q2d, k2d, v2d, B, T, heads, causal, dt, textbook=False):
+        """Restatement only: projected q/k/v [B*T,E] -> merged context [B*T,E].
+        textbook=False: MuNet's reading of k's buffer as [hd, B*H*T]
+        (src/nn/attention.hpp:64-67, src/core/ops/matmul.cpp:331-392);
+        textbook=True: key j of a head is position j's key, with the same
+        rounding steps (the build's decode attention; no MuNet counterpart)."""
         q2d, k2d, v2d = self._c(q2d, dt), self._c(k2d, dt), self._c(v2d, dt)
         out = np.empty_like(q2d)
         E = q2d.shape[-1]
-        self._call("mha_core", _i(dt), _ptr(q2d), _ptr(k2d), _ptr(v2d), _ptr(out),
+        self._call("mha_core_textbook" if textbook else "mha_core", _i(dt), _ptr(q2d), _ptr(k2d), _ptr(v2d), _ptr(out),
                    _i(B), _i(T), _i(heads), _i(E // heads), _i(int(causal)))
         return out
 

@@ -48,7 +48,8 @@ def block_forward(o: CpuOracle, cfg, p, x, prefix, causal):
     dt = _dt(cfg)
     eps = cfg.get("eps", 1e-5)
     h = o.layer_norm(x, p[prefix + "ln1.weight"], p[prefix + "ln1.bias"], dt, eps)
-    a = o.mha(h, p, cfg["num_heads"], causal, dt, prefix=prefix + "attn.")
+    a = o.mha(h, p, cfg["num_heads"], causal, dt, prefix=prefix + "attn.",
+              textbook=cfg.get("attention", "munet") == "textbook")
     x = o.add(x, a, dt)
     h2 = o.layer_norm(x, p[prefix + "ln2.weight"], p[prefix + "ln2.bias"], dt, eps)
     f = o.linear(h2, p[prefix + "ff.0.weight"], p[prefix + "ff.0.bias"], dt)

@@ -460,8 +460,13 @@ void layer_norm(int dt, const void *x, const void *w, const void *b, void *out,
 // mask is block diagonal; masked entries contribute exact zeros to every sum,
 // so each (b,h) block is computed on its own with the reference's own
 // operation order (documented in the function body).
+// textbook: key j of block bh is row bh*T + j of the head-split k (the usual
+// attention), instead of the reference's reading of k's buffer as a
+// [hd, B*H*T] matrix; every rounding step stays the reference's.  This is the
+// attention of the build's autoregressive decode (a KV cache needs each key
+// to be its own position's), which MuNet itself does not have.
 void mha_core(int dt, const void *q2d, const void *k2d, const void *v2d,
-              void *ctx2d, int B, int T, int H, int hd, bool causal) {
+              void *ctx2d, int B, int T, int H, int hd, bool causal, bool textbook) {
   const int E = H * hd, BH = B * H;
   const size_t N = size_t(BH) * T, es = dsize(dt);
   // permute [B,T,H,hd] -> [B,H,T,hd] contiguous (bit copies).
@@ -499,12 +504,14 @@ void mha_core(int dt, const void *q2d, const void *k2d, const void *v2d,
       const size_t bh = gi / T, i = gi % T;
       const size_t col0 = bh * T;
       // scores[gi][col0+j] = sum_k Q[gi][k] * Kflat[k*N + col0 + j]
+      // (textbook: K[col0+j][k])
       for (int j = 0; j < T; ++j) {
         double sc;
+        auto kidx = [&](int kk) { return textbook ? (col0 + j) * hd + kk : size_t(kk) * N + col0 + j; };
         if (dt == F32 || dt == F16) {
           float sum = 0.0f;
           for (int kk = 0; kk < hd; ++kk)
-            sum += qf[gi * hd + kk] * kf[size_t(kk) * N + col0 + j];
+            sum += qf[gi * hd + kk] * kf[kidx(kk)];
           // matmul output rounded to dtype, then scaled by the [1] tensor
           if (dt == F32) {
             sc = double(sum * scale_f);
@@ -516,7 +523,7 @@ void mha_core(int dt, const void *q2d, const void *k2d, const void *v2d,
         } else {
           double sum = 0.0;
           for (int kk = 0; kk < hd; ++kk)
-            sum += rd(q.data(), dt, gi * hd + kk) * rd(k.data(), dt, size_t(kk) * N + col0 + j);
+            sum += rd(q.data(), dt, gi * hd + kk) * rd(k.data(), dt, kidx(kk));
           double sv = double(dec_bf16(enc_bf16(float(sum))));
           sc = double(dec_bf16(enc_bf16(float(sv * scale_d))));
         }
@@ -679,7 +686,12 @@ int orc_layer_norm(int dt, const void *x, const void *w, const void *b, void *ou
 }
 int orc_mha_core(int dt, const void *q2d, const void *k2d, const void *v2d,
                  void *ctx, int B, int T, int H, int hd, int causal) {
-  ORC_GUARD(mha_core(dt, q2d, k2d, v2d, ctx, B, T, H, hd, causal != 0))
+  ORC_GUARD(mha_core(dt, q2d, k2d, v2d, ctx, B, T, H, hd, causal != 0, false))
+}
+
+int orc_mha_core_textbook(int dt, const void *q2d, const void *k2d, const void *v2d,
+                          void *ctx, int B, int T, int H, int hd, int causal) {
+  ORC_GUARD(mha_core(dt, q2d, k2d, v2d, ctx, B, T, H, hd, causal != 0, true))
 }
 
 // Embedding gather (linear.hpp:92-128): ids int32 [n], weight [V, D].

@@ -380,3 +380,57 @@ def test_reference_threading_mode_gives_the_same_bits():
         assert np.array_equal(outs[0], outs[2]) and np.array_equal(outs[1], outs[3])
     finally:
         o.set_threading("parity")
+
+
+# ---- textbook-key attention (the KV-cache decode's attention) ---------------
+# No MuNet counterpart exists (its attention reads keys through the buffer
+# reinterpretation), so the textbook mode is pinned against torch's
+# scaled_dot_product_attention in float64 and by the causal prefix property.
+
+def _sdpa(q2d, k2d, v2d, B, T, H, causal, dt):
+    import torch
+    E = q2d.shape[-1]
+    hd = E // H
+    f = lambda a: torch.from_numpy(synth.decode(a, dt).astype(np.float64)).view(B, T, H, hd).permute(0, 2, 1, 3)
+    o = torch.nn.functional.scaled_dot_product_attention(f(q2d), f(k2d), f(v2d), is_causal=causal)
+    return o.permute(0, 2, 1, 3).reshape(B * T, E).numpy()
+
+
+@pytest.mark.parametrize("dt,tol", [(synth.F32, 1e-5), (synth.BF16, 2e-2), (synth.F16, 4e-3)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_textbook_attention_matches_sdpa(orc, dt, tol, causal):
+    rng = np.random.default_rng(7)
+    B, T, H, hd = 2, 13, 3, 16
+    q, k, v = (synth.encode(rng.standard_normal((B * T, H * hd)), dt) for _ in range(3))
+    out = synth.decode(orc.mha_core(q, k, v, B, T, H, causal, dt, textbook=True), dt)
+    ref = _sdpa(q, k, v, B, T, H, causal, dt)
+    assert np.max(np.abs(out - ref)) <= tol * np.max(np.abs(ref))
+
+
+def test_textbook_attention_planted_mistakes_are_rejected(orc):
+    """MuNet's key reading, and keys shifted by one position, both miss."""
+    rng = np.random.default_rng(8)
+    B, T, H, hd = 2, 11, 2, 8
+    q, k, v = (rng.standard_normal((B * T, H * hd)).astype(np.float32) for _ in range(3))
+    ref = _sdpa(q, k, v, B, T, H, True, synth.F32)
+    munet = orc.mha_core(q, k, v, B, T, H, True, synth.F32)
+    assert np.max(np.abs(munet - ref)) > 0.1
+    ks = np.roll(k.reshape(B, T, -1), 1, axis=1).reshape(B * T, -1)
+    shifted = orc.mha_core(q, ks, v, B, T, H, True, synth.F32, textbook=True)
+    assert np.max(np.abs(shifted - ref)) > 0.1
+
+
+def test_textbook_decoder_is_causal_bit_for_bit(orc):
+    """Textbook attention: position t's logits depend on tokens <= t only, so a
+    prefix's forward equals the full forward's first rows bit for bit (MuNet's
+    key reading mixes positions: it fails the same check)."""
+    from munet_amd import models
+    from oracle import models as omodels
+    for attn, equal in (("textbook", True), ("munet", False)):
+        cfg = models.decoder_config(vocab=97, ctx=32, d_model=32, num_heads=2, num_layers=2, ffn=64,
+                                    attention=attn)
+        p = models.init_params(cfg, "gpt", scope="tbc")
+        ids = models.make_input(cfg, (2, 12), "gpt", scope="tbc_in")
+        full = omodels.forward(orc, cfg, p, ids)
+        pre = omodels.forward(orc, cfg, p, ids[:, :7])
+        assert np.array_equal(full[:, :7], pre) == equal, attn
