@@ -34,7 +34,9 @@ same bf16 Linear is timed in it and in the port ("reference_check").
 
 "configs": BASELINE configs[0..3] (MLP, CNN, encoder block bf16 / fp16,
 UNet) at their full sizes: forward time, samples/s, MFMA / HBM fractions of
-their products and norms, and the CPU baseline per config.
+their products and norms, and the CPU baseline per config; "decode": greedy
+KV-cache decode on the headline architecture with textbook-key attention
+(ms per step, tokens/s, HBM bytes per step against the 8 TB/s peak).
 """
 from __future__ import annotations
 
@@ -300,6 +302,45 @@ def config_line(torch, key, idx, cpu_batch, steps, warmup, with_cpu):
     return row
 
 
+def decode_line(steps=256, prompt=512, max_len=1024):
+    """Greedy KV-cache decode (mh_decoder_*) on the headline architecture with
+    textbook-key attention (the decode has no MuNet counterpart): prefill a
+    [4, prompt] batch, then `steps` one-token steps back to back on the
+    device (positions prompt .. prompt + steps - 1).  HBM roofline: per step
+    every Linear weight row is streamed once (the embedding tables are only
+    gathered) and every head reads its cached keys and values."""
+    from munet_amd import models, synth
+    from munet_amd.engine import Decoder, Engine
+    cfg = models.decoder_config(**CFG, attention="textbook")
+    params = models.init_params(cfg, "gpt", scope="bench_decode")
+    ids = models.make_input(cfg, (B, prompt), "gpt", scope="bench_decode_in")
+    eng = Engine(0).load(cfg, params).compile((B, prompt))
+    del params
+    dcd = Decoder(eng, B, max_len)
+    dcd.prefill(ids, logits=False)
+    dcd.generate(8)  # warm-up
+    dcd.prefill(ids, logits=False)
+    toks, ms = dcd.generate(steps)
+    st = dcd.stats()
+    d, L, H, V, C = cfg["d_model"], cfg["num_layers"], cfg["num_heads"], cfg["vocab"], cfg["ctx"]
+    es = 2
+    streamed = st["weight_bytes"] - (V + C) * d * es  # every weight row but the gathered tables
+    avg_len = prompt + (steps + 1) / 2.0
+    kv = 2.0 * L * B * d * es * avg_len  # K and V of every cached position, every layer
+    per_step = streamed + kv
+    t = ms * 1e-3 / steps
+    row = dict(workload="gpt_decoder_decode (BASELINE configs[4] architecture, textbook-key attention)",
+               batch=B, prompt=prompt, steps=steps, positions=[prompt, prompt + steps - 1], dtype="bf16",
+               ms_per_step=t * 1e3, tokens_per_s=B / t, prefill_ms=st["last_prefill_ms"],
+               kernels_per_step=st["kernels_per_step"],
+               roofline=dict(bound="hbm", bytes_per_step=per_step, achieved=per_step / t / 1e9, peak=PEAK_HBM / 1e9,
+                             unit="GB/s", frac=per_step / t / PEAK_HBM),
+               tokens_sample=toks[:4, 0].tolist())
+    dcd.close()
+    eng.close()
+    return row
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -417,6 +458,8 @@ def main():
         for key, idx, cpu_batch in CONFIG_ROWS:
             log(f"bench: config {key}")
             configs[key] = config_line(torch, key, idx, cpu_batch, args.steps, args.warmup, not args.no_cpu_baseline)
+        log("bench: KV-cache decode")
+        configs["decode"] = decode_line()
     line = {
         "metric": "decoder inference tokens/s at 1 GPU",
         "value": tokens_s,

@@ -13,6 +13,8 @@
 //   state[1] = step index into the generated-token buffer
 // Cache layout: [layer][b][h][Lmax][hd] for K and for V, 16-byte rows of
 // the head dimension contiguous.
+#include <type_traits>
+
 #include "mh_common.hpp"
 #include "mh_kernels.hpp"
 
@@ -34,6 +36,17 @@ template <int DT> struct Chunk {
         v[2 * i] = Store<DT>::dec(uint16_t(w[i] & 0xffffu));
         v[2 * i + 1] = Store<DT>::dec(uint16_t(w[i] >> 16));
       }
+    }
+  }
+  static __device__ __forceinline__ uint4 enc(const float v[E]) {
+    if constexpr (DT == F32) {
+      return make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
+    } else {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = uint32_t(Store<DT>::enc(v[2 * i])) | (uint32_t(Store<DT>::enc(v[2 * i + 1])) << 16);
+      return make_uint4(w[0], w[1], w[2], w[3]);
     }
   }
 };
@@ -70,128 +83,367 @@ __device__ __forceinline__ float linear_chain(float acc, float bias, float gelu_
   return v;
 }
 
-// y[m][n] = chain(sum_k xin[m][k] W[n][k]) for m < M, one wave per column n.
-// LN: xin = LayerNorm(x) (the LayerNorm kernel's arithmetic, rounded to the
-// dtype), computed by every block into LDS; otherwise xin = x copied there.
-// QKV: columns [0,E) go to q [M, E], [E,2E) and [2E,3E) to the K and V
-// caches at position state[0] (head h = e / hd, element e % hd).
+// Float -> unsigned key with the same order (NaN excluded by the caller);
+// the argmax key is (key << 32) | ~index: the largest value, then the first
+// index.
+__device__ __forceinline__ uint32_t order_key(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Sum over the 16 lanes of a DPP row (every lane of the row gets it):
+// rotate by 8 and 4 within the row, then the two quad swaps.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false));  // row_ror:8
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xf, 0xf, false));  // row_ror:4
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false));   // quad [2,3,0,1]
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xb1, 0xf, 0xf, false));   // quad [1,0,3,2]
+  return v;
+}
+
+enum DecIn : int { IN_ROW = 0, IN_LN = 1, IN_ATTN = 2 };
+enum DecOut : int { OUT_ROW = 0, OUT_QKV = 1, OUT_ARGMAX = 2 };
+
+// y[m][n] = chain(sum_k xin[m][k] W[n][k]) for M <= MB rows: each wave
+// takes 4 output columns, one per 16-lane DPP row, and a column's
+// K-contiguous weight row is split over its 16 lanes in 16-byte chunks
+// (chunk c on lane c % 16, up to KCH per lane), so the dot products reduce
+// with four DPP adds and no branch.  Each launch is a few
+// microseconds of memory latency, so every global load a block needs is
+// issued before the first wait: the input stage's loads first (its waits
+// then cover only them), the weights next, the epilogue's bias and residual
+// last.  Input stages:
+//   IN_ROW : xin = x, copied to LDS;
+//   IN_LN  : xin = LayerNorm(x) (fp32 mean and variance of the row, the
+//            result rounded to the dtype, as the LayerNorm kernel), one row
+//            per wave from registers;
+//   IN_ATTN: xin = the attention context from dec_attn_kernel's per-block
+//            shares: ctx = round(sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M)),
+//            M the largest block max, in block order.
+// Outputs: OUT_ROW y [M, N]; OUT_QKV columns [0,E) to q [M, E], [E,2E) and
+// [2E,3E) to the K / V caches at position state[0]; OUT_ARGMAX y [M, N] and
+// each row's greedy choice folded into best[m] by a 64-bit atomic max.
 struct DecLinArgs {
   const void *x, *w, *bias, *ln_w, *ln_b, *resid;
+  const float *part_o;
+  const float2 *part_ml;
   void *out, *kc, *vc;
+  unsigned long long *best;
   const int *state;
-  int M, N, K, E, H, hd, Lmax;
+  int M, N, K, E, H, hd, Lmax, nsplit;
   float eps, gelu_c;
 };
 
-template <int DT, bool LN, int ACT, bool RESID, bool QKV>
+constexpr int kMaxSplit = 16;  // key blocks per head (max_len <= 4096)
+
+template <int DT, int KCH, int MB, int CPL, int WS, int IN, int OUT, int ACT, bool RESID>
 __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
   typedef Store<DT> S;
   typedef typename S::T T;
   typedef Chunk<DT> C;
-  extern __shared__ uint4 xs[];  // [M][K / C::E] chunks
+  static_assert(WS == 1 || WS == 4, "waves per column group");
+  extern __shared__ uint4 xs[];  // [M][K / C::E] chunks of the staged input
+  __shared__ unsigned long long bk[16 * CPL][16];
+  __shared__ float wred[WS == 4 ? 4 : 1][4 * CPL][MB];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int K = a.K, KC = K / C::E, M = a.M;
-  const T *x = static_cast<const T *>(a.x);
-  T *xl = reinterpret_cast<T *>(xs);
-  if constexpr (LN) {
-    const T *g = static_cast<const T *>(a.ln_w), *bb = static_cast<const T *>(a.ln_b);
+  const int K = a.K, KC = K / C::E, M = a.M, N = a.N;
+  constexpr int LCH = (KCH * WS + 3) / 4;  // LayerNorm: row chunks per lane (64 lanes)
+  // column group of this wave (WS = 4: the four waves split one group's K)
+  const int grp = WS == 1 ? wave : 0, q = WS == 1 ? 0 : wave;
+  const int rl = lane & 15, row = lane >> 4;  // lane within its DPP row, row of the wave
+  const int nbase = (blockIdx.x * (4 / WS) + grp) * 4 * CPL + row * CPL;  // this row's CPL columns
+  const uint4 zero4 = make_uint4(0, 0, 0, 0);
+
+  // ---- 1. the input stage's loads
+  constexpr int XR = 8;  // IN_ROW chunks per thread held in registers
+  uint4 xq[IN == IN_ROW ? XR : 1];
+  uint4 xr0[IN == IN_LN ? LCH : 1], gq[IN == IN_LN ? LCH : 1], bq[IN == IN_LN ? LCH : 1];
+  if constexpr (IN == IN_ROW) {
+    const uint4 *xc = static_cast<const uint4 *>(a.x);
+#pragma unroll
+    for (int r = 0; r < XR; ++r) {
+      const int i = tid + 256 * r;
+      xq[r] = i < M * KC ? xc[i] : zero4;
+    }
+  } else if constexpr (IN == IN_LN) {
+    const uint4 *g = static_cast<const uint4 *>(a.ln_w), *bb = static_cast<const uint4 *>(a.ln_b);
+    const uint4 *xr = static_cast<const uint4 *>(a.x) + long(min(wave, M - 1)) * KC;
+#pragma unroll
+    for (int i = 0; i < LCH; ++i) {
+      const int c = lane + 64 * i;
+      xr0[i] = c < KC ? xr[c] : zero4;
+      gq[i] = c < KC ? g[c] : zero4;
+      bq[i] = c < KC ? bb[c] : zero4;
+    }
+  }
+
+  // ---- 2. weights: chunks rl + 16 (q + WS i) of each of the row's columns
+  uint4 wv[CPL][KCH];
+#pragma unroll
+  for (int cc = 0; cc < CPL; ++cc) {
+    const uint4 *wr = static_cast<const uint4 *>(a.w) + long(min(nbase + cc, N - 1)) * KC;
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int c = rl + 16 * (q + WS * i);
+      wv[cc][i] = c < KC ? wr[c] : zero4;
+    }
+  }
+
+  // ---- 3. the epilogue's operands (lane rl finishes row rl of its columns)
+  float bia[CPL], res[CPL];
+#pragma unroll
+  for (int cc = 0; cc < CPL; ++cc) {
+    const int nn = min(nbase + cc, N - 1), mm = min(rl, M - 1);
+    bia[cc] = a.bias ? S::dec(static_cast<const T *>(a.bias)[nn]) : 0.f;
+    res[cc] = RESID ? S::dec(static_cast<const T *>(a.resid)[long(mm) * N + nn]) : 0.f;
+  }
+
+  // ---- 4. stage the input in LDS
+  if constexpr (IN == IN_ROW) {
+    const uint4 *xc = static_cast<const uint4 *>(a.x);
+#pragma unroll
+    for (int r = 0; r < XR; ++r) {
+      const int i = tid + 256 * r;
+      if (i < M * KC) xs[i] = xq[r];
+    }
+    for (int i = tid + 256 * XR; i < M * KC; i += 256) xs[i] = xc[i];
+  } else if constexpr (IN == IN_LN) {
     for (int m = wave; m < M; m += 4) {
-      const T *xr = x + long(m) * K;
+      float v[LCH][C::E];
       float sum = 0.f;
-      for (int c = lane; c < K; c += 64) sum += S::dec(xr[c]);
+#pragma unroll
+      for (int i = 0; i < LCH; ++i) {
+        const int c = lane + 64 * i;
+        C::dec(m == wave ? xr0[i] : (c < KC ? static_cast<const uint4 *>(a.x)[long(m) * KC + c] : zero4), v[i]);
+#pragma unroll
+        for (int e = 0; e < C::E; ++e) sum += v[i][e];
+      }
       const float mean = wave_sum(sum) / float(K);
       float var = 0.f;
-      for (int c = lane; c < K; c += 64) {
-        const float d = S::dec(xr[c]) - mean;
-        var += d * d;
-      }
+#pragma unroll
+      for (int i = 0; i < LCH; ++i)
+        if (lane + 64 * i < KC)
+#pragma unroll
+          for (int e = 0; e < C::E; ++e) {
+            const float d = v[i][e] - mean;
+            var += d * d;
+          }
       var = wave_sum(var) / float(K);
       const float inv = 1.0f / sqrtf(var + a.eps);
-      for (int c = lane; c < K; c += 64) xl[long(m) * K + c] = S::enc((S::dec(xr[c]) - mean) * inv * S::dec(g[c]) + S::dec(bb[c]));
+#pragma unroll
+      for (int i = 0; i < LCH; ++i) {
+        const int c = lane + 64 * i;
+        if (c < KC) {
+          float gv[C::E], bv[C::E], o[C::E];
+          C::dec(gq[i], gv);
+          C::dec(bq[i], bv);
+#pragma unroll
+          for (int e = 0; e < C::E; ++e) o[e] = (v[i][e] - mean) * inv * gv[e] + bv[e];
+          xs[m * KC + c] = C::enc(o);
+        }
+      }
     }
   } else {
-    const uint4 *xc = static_cast<const uint4 *>(a.x);
-    for (int i = tid; i < M * KC; i += 256) xs[i] = xc[i];
+    // groups of 4 consecutive context values of one head, two groups per
+    // trip with every share load of both issued together
+    T *xl = reinterpret_cast<T *>(xs);
+    const int H = a.H, hd = a.hd, ns = a.nsplit, G4 = M * K / 4;
+    for (int g0 = tid; g0 < G4; g0 += 512) {
+      float4 o[2][kMaxSplit];
+      float2 ml[2][kMaxSplit];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int g = min(g0 + 256 * u, G4 - 1), e4 = g * 4, m = e4 / K, e = e4 - m * K, h = e / hd, d = e - h * hd;
+        const long bh = long(m) * H + h;
+#pragma unroll
+        for (int sp = 0; sp < kMaxSplit; ++sp)
+          if (sp < ns) {
+            o[u][sp] = *reinterpret_cast<const float4 *>(a.part_o + (bh * ns + sp) * hd + d);
+            ml[u][sp] = a.part_ml[bh * ns + sp];
+          }
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int g = g0 + 256 * u;
+        if (g < G4) {
+          float mx = ml[u][0].x;
+#pragma unroll
+          for (int sp = 1; sp < kMaxSplit; ++sp)
+            if (sp < ns) mx = fmaxf(mx, ml[u][sp].x);
+          float den = 0.f, num[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int sp = 0; sp < kMaxSplit; ++sp)
+            if (sp < ns && ml[u][sp].y > 0.f) {
+              const float f = __expf(ml[u][sp].x - mx);
+              den += ml[u][sp].y * f;
+              num[0] += o[u][sp].x * f;
+              num[1] += o[u][sp].y * f;
+              num[2] += o[u][sp].z * f;
+              num[3] += o[u][sp].w * f;
+            }
+          const float r = 1.0f / den;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xl[g * 4 + e] = S::enc(num[e] * r);
+        }
+      }
+    }
   }
   __syncthreads();
 
-  const int n = blockIdx.x * 4 + wave;
-  if (n >= a.N) return;
-  const uint4 *wr = static_cast<const uint4 *>(a.w) + long(n) * KC;
-  float acc[16];
+  // ---- 5. products, reductions, epilogue
+  float acc[CPL][MB];
 #pragma unroll
-  for (int m = 0; m < 16; ++m) acc[m] = 0.f;
-  for (int c = lane; c < KC; c += 64) {
-    float wv[C::E];
-    C::dec(wr[c], wv);
+  for (int cc = 0; cc < CPL; ++cc)
 #pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      if (m < M) {
-        float xv[C::E];
-        C::dec(xs[m * KC + c], xv);
+    for (int m = 0; m < MB; ++m) acc[cc][m] = 0.f;
 #pragma unroll
-        for (int e = 0; e < C::E; ++e) acc[m] = fmaf(wv[e], xv[e], acc[m]);
+  for (int i = 0; i < KCH; ++i) {
+    const int c = rl + 16 * (q + WS * i);
+    if (c < KC) {
+      float w[CPL][C::E];
+#pragma unroll
+      for (int cc = 0; cc < CPL; ++cc) C::dec(wv[cc][i], w[cc]);
+#pragma unroll
+      for (int m = 0; m < MB; ++m) {
+        if (m < M) {
+          float xv[C::E];
+          C::dec(xs[m * KC + c], xv);
+#pragma unroll
+          for (int cc = 0; cc < CPL; ++cc)
+#pragma unroll
+            for (int e = 0; e < C::E; ++e) acc[cc][m] = fmaf(w[cc][e], xv[e], acc[cc][m]);
+        }
       }
     }
   }
 #pragma unroll
-  for (int m = 0; m < 16; ++m)
-    if (m < M) acc[m] = wave_sum(acc[m]);
-  // lane m finishes row m
-  float mine = 0.f;
+  for (int cc = 0; cc < CPL; ++cc)
 #pragma unroll
-  for (int m = 0; m < 16; ++m)
-    if (lane == m) mine = acc[m];
-  if (lane >= M) return;
-  const int m = lane;
-  const float bias = a.bias ? S::dec(static_cast<const T *>(a.bias)[n]) : 0.f;
-  const float res = RESID ? S::dec(static_cast<const T *>(a.resid)[long(m) * a.N + n]) : 0.f;
-  const T y = S::enc(linear_chain<DT, ACT, RESID>(mine, bias, a.gelu_c, res));
-  if constexpr (QKV) {
-    const int which = n / a.E, e = n - which * a.E, h = e / a.hd, dd = e - h * a.hd;
-    if (which == 0) {
-      static_cast<T *>(a.out)[long(m) * a.E + e] = y;
-    } else {
-      T *cache = static_cast<T *>(which == 1 ? a.kc : a.vc);
-      cache[((long(m) * a.H + h) * a.Lmax + a.state[0]) * a.hd + dd] = y;
+    for (int m = 0; m < MB; ++m) acc[cc][m] = row16_sum(acc[cc][m]);
+  if constexpr (WS == 4) {
+    // the four waves' shares of K, added in wave order by wave 0
+    if (rl == 0) {
+#pragma unroll
+      for (int cc = 0; cc < CPL; ++cc)
+#pragma unroll
+        for (int m = 0; m < MB; ++m) wred[q][row * CPL + cc][m] = acc[cc][m];
     }
-  } else {
-    static_cast<T *>(a.out)[long(m) * a.N + n] = y;
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int cc = 0; cc < CPL; ++cc)
+#pragma unroll
+      for (int m = 0; m < MB; ++m)
+        acc[cc][m] = ((wred[0][row * CPL + cc][m] + wred[1][row * CPL + cc][m]) + wred[2][row * CPL + cc][m]) +
+                     wred[3][row * CPL + cc][m];
+  }
+
+  unsigned long long key = 0;
+#pragma unroll
+  for (int cc = 0; cc < CPL; ++cc) {
+    const int n = nbase + cc;
+    float mine = acc[cc][0];
+#pragma unroll
+    for (int m = 1; m < MB; ++m)
+      if (rl == m) mine = acc[cc][m];
+    if (rl < M && n < N) {
+      const int m = rl;
+      const T y = S::enc(linear_chain<DT, ACT, RESID>(mine, bia[cc], a.gelu_c, res[cc]));
+      if constexpr (OUT == OUT_QKV) {
+        const int which = n / a.E, e = n - which * a.E, h = e / a.hd, dd = e - h * a.hd;
+        if (which == 0) {
+          static_cast<T *>(a.out)[long(m) * a.E + e] = y;
+        } else {
+          T *cache = static_cast<T *>(which == 1 ? a.kc : a.vc);
+          cache[((long(m) * a.H + h) * a.Lmax + a.state[0]) * a.hd + dd] = y;
+        }
+      } else {
+        static_cast<T *>(a.out)[long(m) * N + n] = y;
+      }
+      if constexpr (OUT == OUT_ARGMAX) {
+        const float yv = S::dec(y);
+        if (yv == yv) {  // NaN never wins
+          const unsigned long long k = (static_cast<unsigned long long>(order_key(yv)) << 32) | (0xffffffffu - uint32_t(n));
+          key = k > key ? k : key;
+        }
+      }
+    }
+  }
+  if constexpr (OUT == OUT_ARGMAX) {
+    // row rl's best over the block's columns, then one atomic per row
+    constexpr int SLOTS = (4 / WS) * 4;
+    bk[grp * 4 + row][rl] = key;
+    if constexpr (WS == 1) __syncthreads();
+    else __builtin_amdgcn_s_waitcnt(0xc07f);  // wave 0 alone: its LDS writes done
+    if (tid < M) {
+      unsigned long long k = bk[0][tid];
+#pragma unroll
+      for (int c = 1; c < SLOTS; ++c) k = bk[c][tid] > k ? bk[c][tid] : k;
+      if (k) atomicMax(&a.best[tid], k);
+    }
   }
 }
 
-// Attention of the fed tokens over the cached keys 0..pos (all of them: the
-// newest key is the query's own position).  Pass 1, one block per kSplit keys
-// of head (b, h): score s_j = round(round(q.k_j) * scale) (the reference's
-// matmul and scale roundings), kept in `scores`; the block's max and
-// sum of exp(s_j - max) go to `stats`.
+// Attention of the fed tokens over the cached keys 0..pos (the newest key is
+// the query's own position), one block per kSplit keys of head (b, h), the
+// way the prefill's flash kernel runs a key tile: scores
+// s_j = round(round(q.k_j) * scale) (the reference's matmul and scale
+// roundings), the block max m, p_j = round(e^(s_j - m)) (the rounded,
+// unnormalised probabilities the product uses), and the block's shares
+// o = sum_j p_j v_j, l = sum_j p_j into part_o / part_ml for the
+// out-projection's input stage to combine.  Every K and V load of a thread is
+// issued before the first wait.
 template <int DT>
 __global__ void __launch_bounds__(kSplit)
-dec_attn_scores_kernel(const typename Store<DT>::T *__restrict__ q, const typename Store<DT>::T *__restrict__ kc,
-                       const int *__restrict__ state, float *__restrict__ scores, float2 *__restrict__ stats, int H,
-                       int hd, int Lmax, float scale) {
+dec_attn_kernel(const typename Store<DT>::T *__restrict__ q, const typename Store<DT>::T *__restrict__ kc,
+                const typename Store<DT>::T *__restrict__ vc, const int *__restrict__ state,
+                float *__restrict__ part_o, float2 *__restrict__ part_ml, int H, int hd, int Lmax, float scale) {
   typedef Store<DT> S;
   typedef typename S::T T;
   typedef Chunk<DT> C;
-  __shared__ float qs[256];
+  constexpr int KCH = 64 / C::E;  // 16-byte chunks of a key row (hd <= 64)
+  __shared__ float qs[64];
+  __shared__ float ps[kSplit];
   __shared__ float red[kSplit / 64];
+  __shared__ float osh[16][65];
   const int s = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int b = bh / H, h = bh - b * H, L = state[0] + 1, nsplit = gridDim.x;
-  for (int d = tid; d < hd; d += kSplit) qs[d] = S::dec(q[long(b) * H * hd + long(h) * hd + d]);
-  __syncthreads();
-  const int j = s * kSplit + tid;
-  float sc = -INFINITY;
-  if (j < L) {
-    const uint4 *kr = reinterpret_cast<const uint4 *>(kc + (long(bh) * Lmax + j) * hd);
-    float sum = 0.f;
-    for (int c = 0; c < hd / C::E; ++c) {
-      float kv[C::E];
-      C::dec(kr[c], kv);
+  const int b = bh / H, h = bh - b * H, L = state[0] + 1, ns = gridDim.x;
+  const int j0 = s * kSplit, jn = min(kSplit, L - j0);
+  if (jn <= 0) {  // past the position: an empty share
+    if (tid < hd) part_o[(long(bh) * ns + s) * hd + tid] = 0.f;
+    if (tid == 0) part_ml[long(bh) * ns + s] = make_float2(-INFINITY, 0.f);
+    return;
+  }
+  const int kcn = hd / C::E;
+  // K row of this thread's key, V elements dq..dq+3 of keys jg, jg+16, ...
+  const int j = j0 + tid, jg = tid >> 4, dq = (tid & 15) * 4;
+  uint4 kr[KCH];
+  const uint4 *krow = reinterpret_cast<const uint4 *>(kc + (long(bh) * Lmax + min(j, L - 1)) * hd);
 #pragma unroll
-      for (int e = 0; e < C::E; ++e) sum = fmaf(qs[c * C::E + e], kv[e], sum);
-    }
+  for (int c = 0; c < KCH; ++c) kr[c] = c < kcn ? krow[c] : make_uint4(0, 0, 0, 0);
+  typedef typename std::conditional<sizeof(T) == 2, uint2, uint4>::type V4;
+  V4 vr[kSplit / 16];
+  const int dqc = min(dq, hd - 4);
+#pragma unroll
+  for (int t = 0; t < kSplit / 16; ++t) {
+    const int jj = min(jg + 16 * t, jn - 1);
+    vr[t] = *reinterpret_cast<const V4 *>(vc + (long(bh) * Lmax + j0 + jj) * hd + dqc);
+  }
+  if (tid < hd) qs[tid] = S::dec(q[long(b) * H * hd + long(h) * hd + tid]);
+  __syncthreads();
+
+  float sc = -INFINITY;
+  if (tid < jn) {
+    float sum = 0.f;
+#pragma unroll
+    for (int c = 0; c < KCH; ++c)
+      if (c < kcn) {
+        float kv[C::E];
+        C::dec(kr[c], kv);
+#pragma unroll
+        for (int e = 0; e < C::E; ++e) sum = fmaf(qs[c * C::E + e], kv[e], sum);
+      }
     sc = S::round(S::round(sum) * scale);
-    scores[long(bh) * Lmax + j] = sc;
   }
   float mx = wave_max(sc);
   if (lane == 0) red[wave] = mx;
@@ -199,59 +451,28 @@ dec_attn_scores_kernel(const typename Store<DT>::T *__restrict__ q, const typena
   mx = red[0];
 #pragma unroll
   for (int w = 1; w < kSplit / 64; ++w) mx = fmaxf(mx, red[w]);
+  const float p = tid < jn ? S::round(__expf(sc - mx)) : 0.f;
+  ps[tid] = p;
+  const float l = wave_sum(p);
   __syncthreads();
-  float e = j < L ? __expf(sc - mx) : 0.f;
-  e = wave_sum(e);
-  if (lane == 0) red[wave] = e;
-  __syncthreads();
-  if (tid == 0) {
-    float l = 0.f;
-#pragma unroll
-    for (int w = 0; w < kSplit / 64; ++w) l += red[w];
-    stats[long(bh) * nsplit + s] = make_float2(s * kSplit < L ? mx : -INFINITY, l);
-  }
-}
-
-// Pass 2: the row's max M and sum S over every block's statistics (fixed
-// order), probabilities p_j = round(exp(s_j - M) / S) like the reference's
-// softmax output, then this block's share of sum_j p_j v_j (fp32) into
-// `opart`.  The last block of the head to finish (a counter per head, reset
-// by that block) adds the shares in block order and writes the rounded
-// context.
-template <int DT>
-__global__ void __launch_bounds__(kSplit)
-dec_attn_pv_kernel(const float *__restrict__ scores, const float2 *__restrict__ stats,
-                   const typename Store<DT>::T *__restrict__ vc, const int *__restrict__ state,
-                   float *__restrict__ opart, int *__restrict__ counters, typename Store<DT>::T *__restrict__ ctx, int H,
-                   int hd, int Lmax) {
-  typedef Store<DT> S;
-  typedef typename S::T T;
-  __shared__ float ps[kSplit];
-  __shared__ float osh[16][65];
-  __shared__ int last;
-  const int s = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x, nsplit = gridDim.x;
-  const int L = state[0] + 1;
-  float Mx = -INFINITY;
-  for (int i = 0; i < nsplit; ++i) Mx = fmaxf(Mx, stats[long(bh) * nsplit + i].x);
-  float Ssum = 0.f;
-  for (int i = 0; i < nsplit; ++i) {
-    const float2 st = stats[long(bh) * nsplit + i];
-    if (st.y > 0.f) Ssum += st.y * __expf(st.x - Mx);
-  }
-  const int j = s * kSplit + tid;
-  ps[tid] = j < L ? S::round(__expf(scores[long(bh) * Lmax + j] - Mx) / Ssum) : 0.f;
-  __syncthreads();
-  // 16 key groups x 16 lanes of 4 head elements (hd <= 64)
-  const int jg = tid >> 4, dq = (tid & 15) * 4;
+  if (lane == 0) red[wave] = l;
   float o[4] = {0.f, 0.f, 0.f, 0.f};
-  if (dq < hd) {
-    const int jn = min(kSplit, L - s * kSplit);
-    for (int jj = jg; jj < jn; jj += 16) {
-      float v[4];
-      ld4<DT>(vc + (long(bh) * Lmax + s * kSplit + jj) * hd + dq, v);
-      const float p = ps[jj];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = fmaf(p, v[e], o[e]);
+  for (int t = 0; t < kSplit / 16; ++t) {
+    const int jj = jg + 16 * t;
+    if (jj < jn) {
+      float v[4];
+      if constexpr (sizeof(T) == 2) {
+        const uint2 w = vr[t];
+        v[0] = S::dec(uint16_t(w.x)); v[1] = S::dec(uint16_t(w.x >> 16));
+        v[2] = S::dec(uint16_t(w.y)); v[3] = S::dec(uint16_t(w.y >> 16));
+      } else {
+        const uint4 w = vr[t];
+        v[0] = __uint_as_float(w.x); v[1] = __uint_as_float(w.y); v[2] = __uint_as_float(w.z); v[3] = __uint_as_float(w.w);
+      }
+      const float pj = ps[jj];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = fmaf(pj, v[e], o[e]);
     }
   }
 #pragma unroll
@@ -261,70 +482,35 @@ dec_attn_pv_kernel(const float *__restrict__ scores, const float2 *__restrict__ 
     float t = 0.f;
 #pragma unroll
     for (int g = 0; g < 16; ++g) t += osh[g][tid];
-    opart[(long(bh) * nsplit + s) * hd + tid] = t;
+    part_o[(long(bh) * ns + s) * hd + tid] = t;
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) last = atomicAdd(&counters[bh], 1) == nsplit - 1;
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  if (tid < hd) {
-    float t = 0.f;
-    // device-coherent loads: the shares were written by other blocks
-    for (int i = 0; i < nsplit; ++i)
-      t += __int_as_float(__hip_atomic_load(reinterpret_cast<int *>(&opart[(long(bh) * nsplit + i) * hd + tid]),
-                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    const int b = bh / H, h = bh - b * H;
-    ctx[long(b) * H * hd + long(h) * hd + tid] = S::enc(t);
+  if (tid == 0) {
+    float lt = 0.f;
+#pragma unroll
+    for (int w = 0; w < kSplit / 64; ++w) lt += red[w];
+    part_ml[long(bh) * ns + s] = make_float2(mx, lt);
   }
-  if (tid == 0) atomicExch(&counters[bh], 0);
 }
 
-// Greedy choice: first index of each row's maximum (one block, waves split
-// over the rows), written as the next step's input and into the generated
-// tokens; then the position and the step index advance.
-template <int DT>
-__global__ void __launch_bounds__(1024)
-dec_argmax_kernel(const typename Store<DT>::T *__restrict__ logits, int32_t *__restrict__ ids,
-                  int32_t *__restrict__ tokens, int *__restrict__ state, int B, int V, int cap) {
-  typedef Store<DT> S;
-  __shared__ float bv[16];
-  __shared__ int bi[16];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wpr = 16 / B;  // waves per row (B <= 16)
-  const int row = wave / wpr, part = wave - row * wpr;
-  float best = -INFINITY;
-  int idx = 0x7fffffff;
-  if (row < B) {
-    const typename S::T *p = logits + long(row) * V;
-    for (int c = part * 64 + lane; c < V; c += wpr * 64) {
-      const float v = S::dec(p[c]);
-      if (v > best || (idx == 0x7fffffff && v == best)) { best = v; idx = c; }
-    }
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ob = __shfl_xor(best, o, 64);
-    const int oi = __shfl_xor(idx, o, 64);
-    if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
-  }
-  if (lane == 0) { bv[wave] = best; bi[wave] = idx; }
-  __syncthreads();
-  if (tid < B) {
-    float bb = -INFINITY;
-    int ii = 0x7fffffff;
-    for (int w = tid * wpr; w < (tid + 1) * wpr; ++w)
-      if (bv[w] > bb || (bv[w] == bb && bi[w] < ii)) { bb = bv[w]; ii = bi[w]; }
-    const int out = ii == 0x7fffffff ? 0 : ii;
-    ids[tid] = out;
-    const int st = state[1];
-    if (st < cap) tokens[long(st) * B + tid] = out;
+// The greedy choices folded by the head (best[b]) become the next step's
+// input and the generated tokens; best is reset and the position and step
+// index advance.
+__global__ void __launch_bounds__(64)
+dec_finish_kernel(unsigned long long *__restrict__ best, int32_t *__restrict__ ids, int32_t *__restrict__ tokens,
+                  int *__restrict__ state, int B, int cap) {
+  const int b = threadIdx.x;
+  const int st = state[1];
+  if (b < B) {
+    const unsigned long long k = best[b];
+    const int out = k ? int(0xffffffffu - uint32_t(k & 0xffffffffu)) : 0;
+    ids[b] = out;
+    if (st < cap) tokens[long(st) * B + b] = out;
+    best[b] = 0;
   }
   __syncthreads();
-  if (tid == 0) {
+  if (b == 0) {
     state[0] += 1;
-    state[1] += 1;
+    state[1] = st + 1;
   }
 }
 
@@ -355,23 +541,50 @@ hipError_t dec_embed(int dt, const int32_t *ids, const void *tok, const void *po
   return hipGetLastError();
 }
 
-// kind: 0 LayerNorm + QKV, 1 + residual, 2 LayerNorm + GELU, 3 LayerNorm only
-// (the head)
-hipError_t dec_linear(int dt, int kind, const void *x, const void *w, const void *bias, const void *ln_w,
-                      const void *ln_b, float eps, const void *resid, void *out, void *kc, void *vc, const int *state,
-                      int M, int N, int K, int E, int H, int hd, int Lmax, float gelu_c, hipStream_t st) {
+// kind: 0 LayerNorm + q/k/v into q and the caches, 1 + residual, 2 LayerNorm
+// + GELU, 3 LayerNorm + greedy argmax (the head), 4 attention shares +
+// residual (the out-projection)
+hipError_t dec_linear(int dt, int kind, const DecLinear &p, hipStream_t st) {
   const size_t es = dt_size(dt);
-  if (M < 1 || M > 16 || K % int(16 / es) != 0 || size_t(M) * K * es > 65536) return hipErrorInvalidValue;
-  DecLinArgs a{x, w, bias, ln_w, ln_b, resid, out, kc, vc, state, M, N, K, E, H, hd, Lmax, eps, gelu_c};
-  const dim3 grid((N + 3) / 4);
-  const size_t lds = size_t(M) * K * es;
-#define MH_DL(DTV)                                                                                                     \
-  switch (kind) {                                                                                                      \
-  case 0: hipLaunchKernelGGL((dec_linear_kernel<DTV, true, ACT_NONE, false, true>), grid, dim3(256), lds, st, a); break;  \
-  case 1: hipLaunchKernelGGL((dec_linear_kernel<DTV, false, ACT_NONE, true, false>), grid, dim3(256), lds, st, a); break; \
-  case 2: hipLaunchKernelGGL((dec_linear_kernel<DTV, true, ACT_GELU, false, false>), grid, dim3(256), lds, st, a); break; \
-  case 3: hipLaunchKernelGGL((dec_linear_kernel<DTV, true, ACT_NONE, false, false>), grid, dim3(256), lds, st, a); break; \
-  default: return hipErrorInvalidValue;                                                                                \
+  const int ce = int(16 / es);
+  if (p.M < 1 || p.M > 16 || p.K % ce != 0 || size_t(p.M) * p.K * es > 65536) return hipErrorInvalidValue;
+  const int KC = p.K / ce;
+  if (kind == 4 && (p.nsplit < 1 || p.nsplit > kMaxSplit || p.hd % 4 != 0 || p.K % 4 != 0)) return hipErrorInvalidValue;
+  DecLinArgs a{p.x, p.w, p.bias, p.ln_w, p.ln_b, p.resid, p.part_o, p.part_ml, p.out, p.kc, p.vc, p.best, p.state,
+               p.M, p.N, p.K, p.E, p.H, p.hd, p.Lmax, p.nsplit, p.eps, p.gelu_c};
+  // Launch shape: K up to 128 chunks per column on one wave's 16-lane row
+  // (8 chunks per lane), longer K split over the block's four waves (up to
+  // 512 chunks); the vocabulary head (N >= 8192, short K) takes 4 columns per
+  // row so each block amortises its LayerNorm stage over 64 columns.
+  if (KC > 512) return hipErrorInvalidValue;
+  const int ws = KC > 128 ? 4 : 1, cpl = (kind == 3 && ws == 1 && p.N >= 8192) ? 4 : 1;
+  const bool few = p.M <= 4;
+  const int ncols = (4 / ws) * 4 * cpl;  // columns per block
+  const dim3 grid(unsigned((p.N + ncols - 1) / ncols));
+  const size_t lds = size_t(p.M) * p.K * es;
+#define MH_DLK(DTV, MB, CPL, WS)                                                                                           \
+  switch (kind) {                                                                                                          \
+  case 0: hipLaunchKernelGGL((dec_linear_kernel<DTV, 8, MB, CPL, WS, IN_LN, OUT_QKV, ACT_NONE, false>), grid, dim3(256), lds, st, a); break;   \
+  case 1: hipLaunchKernelGGL((dec_linear_kernel<DTV, 8, MB, CPL, WS, IN_ROW, OUT_ROW, ACT_NONE, true>), grid, dim3(256), lds, st, a); break;   \
+  case 2: hipLaunchKernelGGL((dec_linear_kernel<DTV, 8, MB, CPL, WS, IN_LN, OUT_ROW, ACT_GELU, false>), grid, dim3(256), lds, st, a); break;   \
+  case 3: hipLaunchKernelGGL((dec_linear_kernel<DTV, 8, MB, CPL, WS, IN_LN, OUT_ARGMAX, ACT_NONE, false>), grid, dim3(256), lds, st, a); break; \
+  case 4: hipLaunchKernelGGL((dec_linear_kernel<DTV, 8, MB, CPL, WS, IN_ATTN, OUT_ROW, ACT_NONE, true>), grid, dim3(256), lds, st, a); break;  \
+  default: return hipErrorInvalidValue;                                                                                    \
+  }
+#define MH_DLS(DTV, MB)                                                          \
+  if (ws == 4) {                                                                 \
+    MH_DLK(DTV, MB, 1, 4)                                                        \
+  } else if (cpl == 4) {                                                         \
+    if (kind != 3) return hipErrorInvalidValue;                                  \
+    hipLaunchKernelGGL((dec_linear_kernel<DTV, 8, MB, 4, 1, IN_LN, OUT_ARGMAX, ACT_NONE, false>), grid, dim3(256), lds, st, a); \
+  } else {                                                                       \
+    MH_DLK(DTV, MB, 1, 1)                                                        \
+  }
+#define MH_DL(DTV)              \
+  if (few) {                    \
+    MH_DLS(DTV, 4)              \
+  } else {                      \
+    MH_DLS(DTV, 16)             \
   }
   switch (dt) {
   case F32: MH_DL(F32); break;
@@ -380,38 +593,29 @@ hipError_t dec_linear(int dt, int kind, const void *x, const void *w, const void
   default: return hipErrorInvalidValue;
   }
 #undef MH_DL
+#undef MH_DLS
+#undef MH_DLK
   return hipGetLastError();
 }
 
-hipError_t dec_attention(int dt, const void *q, const void *kc, const void *vc, const int *state, float *scores,
-                         float2 *stats, float *opart, int *counters, void *ctx, int B, int H, int hd, int Lmax,
-                         float scale, hipStream_t st) {
-  if (hd > 64 || hd % 4 != 0 || hd % int(16 / dt_size(dt)) != 0) return hipErrorInvalidValue;
-  const dim3 grid((Lmax + kSplit - 1) / kSplit, B * H);
-#define MH_DA(DTV, T)                                                                                               \
-  hipLaunchKernelGGL(dec_attn_scores_kernel<DTV>, grid, dim3(kSplit), 0, st, (const T *)q, (const T *)kc, state,     \
-                     scores, stats, H, hd, Lmax, scale);                                                             \
-  hipLaunchKernelGGL(dec_attn_pv_kernel<DTV>, grid, dim3(kSplit), 0, st, scores, stats, (const T *)vc, state, opart, \
-                     counters, (T *)ctx, H, hd, Lmax)
+hipError_t dec_attention(int dt, const void *q, const void *kc, const void *vc, const int *state, float *part_o,
+                         float2 *part_ml, int B, int H, int hd, int Lmax, float scale, hipStream_t st) {
+  const int ns = (Lmax + kSplit - 1) / kSplit;
+  if (hd > 64 || hd % 4 != 0 || hd % int(16 / dt_size(dt)) != 0 || ns > kMaxSplit) return hipErrorInvalidValue;
+  const dim3 grid(ns, B * H);
   switch (dt) {
-  case F32: MH_DA(F32, float); break;
-  case F16: MH_DA(F16, uint16_t); break;
-  case BF16: MH_DA(BF16, uint16_t); break;
+  case F32: hipLaunchKernelGGL(dec_attn_kernel<F32>, grid, dim3(kSplit), 0, st, (const float *)q, (const float *)kc, (const float *)vc, state, part_o, part_ml, H, hd, Lmax, scale); break;
+  case F16: hipLaunchKernelGGL(dec_attn_kernel<F16>, grid, dim3(kSplit), 0, st, (const uint16_t *)q, (const uint16_t *)kc, (const uint16_t *)vc, state, part_o, part_ml, H, hd, Lmax, scale); break;
+  case BF16: hipLaunchKernelGGL(dec_attn_kernel<BF16>, grid, dim3(kSplit), 0, st, (const uint16_t *)q, (const uint16_t *)kc, (const uint16_t *)vc, state, part_o, part_ml, H, hd, Lmax, scale); break;
   default: return hipErrorInvalidValue;
   }
-#undef MH_DA
   return hipGetLastError();
 }
 
-hipError_t dec_argmax(int dt, const void *logits, int32_t *ids, int32_t *tokens, int *state, int B, int V, int cap,
+hipError_t dec_finish(unsigned long long *best, int32_t *ids, int32_t *tokens, int *state, int B, int cap,
                       hipStream_t st) {
   if (B < 1 || B > 16) return hipErrorInvalidValue;
-  switch (dt) {
-  case F32: hipLaunchKernelGGL(dec_argmax_kernel<F32>, dim3(1), dim3(1024), 0, st, (const float *)logits, ids, tokens, state, B, V, cap); break;
-  case F16: hipLaunchKernelGGL(dec_argmax_kernel<F16>, dim3(1), dim3(1024), 0, st, (const uint16_t *)logits, ids, tokens, state, B, V, cap); break;
-  case BF16: hipLaunchKernelGGL(dec_argmax_kernel<BF16>, dim3(1), dim3(1024), 0, st, (const uint16_t *)logits, ids, tokens, state, B, V, cap); break;
-  default: return hipErrorInvalidValue;
-  }
+  hipLaunchKernelGGL(dec_finish_kernel, dim3(1), dim3(64), 0, st, best, ids, tokens, state, B, cap);
   return hipGetLastError();
 }
 

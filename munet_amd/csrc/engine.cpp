@@ -1372,11 +1372,12 @@ struct mh_decoder {
   };
   std::vector<LayerW> lw;
   const void *tok = nullptr, *pos_tab = nullptr, *lnfw = nullptr, *lnfb = nullptr, *whead = nullptr, *bhead = nullptr;
-  void *x = nullptr, *x1 = nullptr, *q = nullptr, *ctx = nullptr, *h = nullptr, *logits = nullptr;
+  void *x = nullptr, *x1 = nullptr, *q = nullptr, *h = nullptr, *logits = nullptr;
   int32_t *ids = nullptr, *tokens = nullptr;
-  int *state = nullptr, *counters = nullptr;
-  float *scores = nullptr, *opart = nullptr;
-  float2 *stats = nullptr;
+  int *state = nullptr;
+  unsigned long long *best = nullptr;
+  float *part_o = nullptr;
+  float2 *part_ml = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   std::map<int, std::unique_ptr<mh::EngineImpl>> prefills;  // by prompt length
@@ -1414,6 +1415,7 @@ struct mh_decoder {
     hd = d / H;
     if (batch < 1 || batch > 16) throw Error("decoder: batch must be in 1..16");
     if (max_len < 1 || max_len > C) throw Error("decoder: max_len must be in 1..ctx");
+    if (max_len > 4096) throw Error("decoder: max_len above 4096 (16 attention blocks of 256 keys)");
     if (d % H || hd > 64 || hd % 4 || hd % int(ce) || d % int(ce) || ffn % int(ce))
       throw Error("decoder: d_model, ffn and head_dim must be multiples of 16 bytes, head_dim <= 64");
     if (size_t(batch) * std::max(d, ffn) * es > 65536) throw Error("decoder: batch x width exceeds the 64 KiB row stage");
@@ -1482,21 +1484,19 @@ struct mh_decoder {
     size_t off = 0;
     auto carve = [&](size_t bytes) { const size_t o = off; off += (bytes + 255) & ~size_t(255); return o; };
     const size_t o_x = carve(size_t(B) * d * es), o_x1 = carve(size_t(B) * d * es), o_q = carve(size_t(B) * d * es),
-                 o_ctx = carve(size_t(B) * d * es), o_h = carve(size_t(B) * ffn * es),
-                 o_lg = carve(size_t(B) * V * es), o_ids = carve(size_t(B) * 4), o_tok = carve(size_t(Lmax) * B * 4),
-                 o_st = carve(16), o_cnt = carve(size_t(B) * H * 4), o_sc = carve(size_t(B) * H * Lmax * 4),
-                 o_stats = carve(size_t(B) * H * nsplit * 8), o_op = carve(size_t(B) * H * nsplit * hd * 4);
+                 o_h = carve(size_t(B) * ffn * es), o_lg = carve(size_t(B) * V * es), o_ids = carve(size_t(B) * 4),
+                 o_tok = carve(size_t(Lmax) * B * 4), o_st = carve(16), o_best = carve(size_t(B) * 8),
+                 o_ml = carve(size_t(B) * H * nsplit * 8), o_part = carve(size_t(B) * H * nsplit * hd * 4);
     bufbytes = off;
     hip_check(hipMalloc(&buf, bufbytes), "hipMalloc(decoder buffers)");
     hip_check(hipMemset(buf, 0, bufbytes), "hipMemset(decoder buffers)");
-    x = buf + o_x; x1 = buf + o_x1; q = buf + o_q; ctx = buf + o_ctx; h = buf + o_h; logits = buf + o_lg;
+    x = buf + o_x; x1 = buf + o_x1; q = buf + o_q; h = buf + o_h; logits = buf + o_lg;
     ids = reinterpret_cast<int32_t *>(buf + o_ids);
     tokens = reinterpret_cast<int32_t *>(buf + o_tok);
     state = reinterpret_cast<int *>(buf + o_st);
-    counters = reinterpret_cast<int *>(buf + o_cnt);
-    scores = reinterpret_cast<float *>(buf + o_sc);
-    stats = reinterpret_cast<float2 *>(buf + o_stats);
-    opart = reinterpret_cast<float *>(buf + o_op);
+    best = reinterpret_cast<unsigned long long *>(buf + o_best);
+    part_ml = reinterpret_cast<float2 *>(buf + o_ml);
+    part_o = reinterpret_cast<float *>(buf + o_part);
     layer_bytes = size_t(B) * H * Lmax * hd * es;
     cache_bytes = 2 * size_t(L) * layer_bytes;
     hip_check(hipMalloc(&cache, cache_bytes), "hipMalloc(KV cache)");
@@ -1523,28 +1523,32 @@ struct mh_decoder {
     using mh::hip_check;
     const float gelu_c = mh::host_round(dt, 1.702f), scale = mh::host_round(dt, 1.0f / std::sqrt(float(hd)));
     hip_check(mh::dec_embed(dt, ids, tok, pos_tab, state, x, B, V, d, mh::device_error_flag(), stream), "decode embed");
+    mh::DecLinear p;
+    p.state = state; p.M = B; p.E = d; p.H = H; p.hd = hd; p.Lmax = Lmax; p.nsplit = nsplit; p.eps = eps;
+    p.gelu_c = gelu_c;
     for (int l = 0; l < L; ++l) {
       const LayerW &w = lw[l];
-      hip_check(mh::dec_linear(dt, 0, x, w.wqkv, w.bqkv, w.ln1w, w.ln1b, eps, nullptr, q, kcache(l), vcache(l), state,
-                               B, 3 * d, d, d, H, hd, Lmax, gelu_c, stream),
-                "decode ln1 + qkv");
-      hip_check(mh::dec_attention(dt, q, kcache(l), vcache(l), state, scores, stats, opart, counters, ctx, B, H, hd,
-                                  Lmax, scale, stream),
+      mh::DecLinear a = p;  // ln1 + q/k/v: q, and k / v into the caches at pos
+      a.x = x; a.w = w.wqkv; a.bias = w.bqkv; a.ln_w = w.ln1w; a.ln_b = w.ln1b; a.out = q;
+      a.kc = kcache(l); a.vc = vcache(l); a.N = 3 * d; a.K = d;
+      hip_check(mh::dec_linear(dt, 0, a, stream), "decode ln1 + qkv");
+      hip_check(mh::dec_attention(dt, q, kcache(l), vcache(l), state, part_o, part_ml, B, H, hd, Lmax, scale, stream),
                 "decode attention");
-      hip_check(mh::dec_linear(dt, 1, ctx, w.wo, w.bo, nullptr, nullptr, eps, x, x1, nullptr, nullptr, state, B, d, d,
-                               d, H, hd, Lmax, gelu_c, stream),
-                "decode out_proj");
-      hip_check(mh::dec_linear(dt, 2, x1, w.w1, w.b1, w.ln2w, w.ln2b, eps, nullptr, h, nullptr, nullptr, state, B, ffn,
-                               d, d, H, hd, Lmax, gelu_c, stream),
-                "decode ln2 + ff.0 + gelu");
-      hip_check(mh::dec_linear(dt, 1, h, w.w2, w.b2, nullptr, nullptr, eps, x1, x, nullptr, nullptr, state, B, d, ffn,
-                               d, H, hd, Lmax, gelu_c, stream),
-                "decode ff.2");
+      mh::DecLinear o = p;  // attention shares -> out_proj + residual
+      o.part_o = part_o; o.part_ml = part_ml; o.w = w.wo; o.bias = w.bo; o.resid = x; o.out = x1; o.N = d; o.K = d;
+      hip_check(mh::dec_linear(dt, 4, o, stream), "decode out_proj");
+      mh::DecLinear f = p;  // ln2 + ff.0 + GELU
+      f.x = x1; f.w = w.w1; f.bias = w.b1; f.ln_w = w.ln2w; f.ln_b = w.ln2b; f.out = h; f.N = ffn; f.K = d;
+      hip_check(mh::dec_linear(dt, 2, f, stream), "decode ln2 + ff.0 + gelu");
+      mh::DecLinear g = p;  // ff.2 + residual
+      g.x = h; g.w = w.w2; g.bias = w.b2; g.resid = x1; g.out = x; g.N = d; g.K = ffn;
+      hip_check(mh::dec_linear(dt, 1, g, stream), "decode ff.2");
     }
-    hip_check(mh::dec_linear(dt, 3, x, whead, bhead, lnfw, lnfb, eps, nullptr, logits, nullptr, nullptr, state, B, V,
-                             d, d, H, hd, Lmax, gelu_c, stream),
-              "decode ln_f + head");
-    hip_check(mh::dec_argmax(dt, logits, ids, tokens, state, B, V, Lmax, stream), "decode argmax");
+    mh::DecLinear hd_ = p;  // ln_f + head, greedy choice folded into best
+    hd_.x = x; hd_.w = whead; hd_.bias = bhead; hd_.ln_w = lnfw; hd_.ln_b = lnfb; hd_.out = logits; hd_.best = best;
+    hd_.N = V; hd_.K = d;
+    hip_check(mh::dec_linear(dt, 3, hd_, stream), "decode ln_f + head");
+    hip_check(mh::dec_finish(best, ids, tokens, state, B, Lmax, stream), "decode finish");
   }
 
   // Prompt ids [B, T0] through the engine's forward (textbook attention), the
@@ -1641,7 +1645,7 @@ struct mh_decoder {
     std::ostringstream s;
     s << "{\"batch\":" << B << ",\"max_len\":" << Lmax << ",\"position\":" << pos << ",\"steps\":" << steps
       << ",\"weight_bytes\":" << wbytes << ",\"cache_bytes\":" << cache_bytes << ",\"buffer_bytes\":" << bufbytes
-      << ",\"kernels_per_step\":" << (3 + 6 * L) << ",\"last_step_ms\":" << last_step_ms
+      << ",\"kernels_per_step\":" << (3 + 5 * L) << ",\"last_step_ms\":" << last_step_ms
       << ",\"last_generate_ms\":" << last_generate_ms << ",\"last_prefill_ms\":" << last_prefill_ms
       << ",\"prefill_instances\":" << prefills.size() << "}";
     return s.str();

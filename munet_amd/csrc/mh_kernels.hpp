@@ -128,17 +128,28 @@ hipError_t attention(int dt, const void *q, const void *k, const void *v, void *
 // KV-cache decode (decode.hip).  state: device ints {pos, step}.
 hipError_t dec_embed(int dt, const int32_t *ids, const void *tok, const void *pos_tab, const int *state, void *out,
                      int B, int V, int D, int *err, hipStream_t st);
-// kind 0: LayerNorm + q/k/v (k, v into the caches at pos); 1: + residual;
-// 2: LayerNorm + GELU; 3: LayerNorm (the head).  M <= 16 rows.
-hipError_t dec_linear(int dt, int kind, const void *x, const void *w, const void *bias, const void *ln_w,
-                      const void *ln_b, float eps, const void *resid, void *out, void *kc, void *vc, const int *state,
-                      int M, int N, int K, int E, int H, int hd, int Lmax, float gelu_c, hipStream_t st);
-// scratch: scores [B*H, Lmax], stats / opart per (head, 256-key block),
-// counters [B*H] (zero before the first call; every call leaves them zero)
-hipError_t dec_attention(int dt, const void *q, const void *kc, const void *vc, const int *state, float *scores,
-                         float2 *stats, float *opart, int *counters, void *ctx, int B, int H, int hd, int Lmax,
-                         float scale, hipStream_t st);
-hipError_t dec_argmax(int dt, const void *logits, int32_t *ids, int32_t *tokens, int *state, int B, int V, int cap,
+// One weight-streaming Linear over M <= 16 rows (dec_linear kinds: 0
+// LayerNorm + q/k/v, k and v into the caches at pos; 1 + residual; 2
+// LayerNorm + GELU; 3 LayerNorm + greedy argmax folded into best; 4 the
+// attention's per-block shares part_o / part_ml combined into the input,
+// + residual).
+struct DecLinear {
+  const void *x = nullptr, *w = nullptr, *bias = nullptr, *ln_w = nullptr, *ln_b = nullptr, *resid = nullptr;
+  const float *part_o = nullptr;
+  const float2 *part_ml = nullptr;
+  void *out = nullptr, *kc = nullptr, *vc = nullptr;
+  unsigned long long *best = nullptr;
+  const int *state = nullptr;
+  int M = 0, N = 0, K = 0, E = 0, H = 1, hd = 1, Lmax = 1, nsplit = 1;
+  float eps = 1e-5f, gelu_c = 1.702f;
+};
+hipError_t dec_linear(int dt, int kind, const DecLinear &p, hipStream_t st);
+// One block per 256 keys of each head: shares part_o [B*H][blocks][hd],
+// part_ml [B*H][blocks] (blocks = ceil(Lmax / 256) <= 16)
+hipError_t dec_attention(int dt, const void *q, const void *kc, const void *vc, const int *state, float *part_o,
+                         float2 *part_ml, int B, int H, int hd, int Lmax, float scale, hipStream_t st);
+// best [B] -> ids [B] and tokens[step] (best reset), position and step + 1
+hipError_t dec_finish(unsigned long long *best, int32_t *ids, int32_t *tokens, int *state, int B, int cap,
                       hipStream_t st);
 hipError_t kv_store(int dt, const void *k, const void *v, void *kc, void *vc, int BH, int T, int hd, int Lmax,
                     hipStream_t st);
