@@ -35,6 +35,7 @@
 // fp32 CPU kernels do (src/backend/cpu_backend.hpp:334-374, 587-611).
 #include <cmath>
 #include <cstdlib>
+#include <string>
 
 #include "mh_common.hpp"
 #include "mh_kernels.hpp"
@@ -564,6 +565,265 @@ flash_attn_tr_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict_
   }
 }
 
+// ---------------------------------------------------------------------------
+// Software-pipelined main path (bf16/fp16, hd = 64, T % 64 == 0, power-of-two
+// scale, MuNet's K reading): the same tiles, transposing reads, log2-domain
+// softmax and lazy max raise as flash_attn_tr_kernel, with the work of one
+// 64-key tile spread over two loop trips so that a wave always has matrix and
+// vector work in flight together:
+//   trip t:  P(t) = exp2(S(t) c2 - m)          (VALU)
+//            S(t+1) = K(t+1) Q^T               (MFMA, beside the exponentials)
+//            O += V(t) P(t)^T                  (MFMA)
+//            round / mask / lane max of S(t+1) (VALU, beside the PV MFMAs)
+// K/V tiles rotate through three LDS buffers (tile t + 2 is written while
+// tiles t and t + 1 are read), so a trip needs one barrier.  Trips past the
+// last tile read stale buffers and re-load the last tile; their results are
+// never used.  The score rounding takes one instruction per value: packing
+// (0, x) to bf16 leaves round(x) as a float in the high half.
+//
+// Work order: items (query block, bh) heaviest first (causal), and within
+// every odd round of `snake` workgroups (one per CU) the order is reversed in
+// groups of 8, so the workgroups that share a CU pair heavy query blocks with
+// light ones while each XCD keeps the same heads.
+template <int DT> __device__ __forceinline__ float round1(float x);
+template <> __device__ __forceinline__ float round1<BF16>(float x) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  return __uint_as_float(__builtin_bit_cast(uint32_t, __builtin_convertvector(f2{0.f, x}, b2)));
+}
+template <> __device__ __forceinline__ float round1<F16>(float x) { return Store<F16>::round(x); }
+
+template <int DT>
+__global__ void __launch_bounds__(256, 3)
+flash_attn_pipe_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K, const uint16_t *__restrict__ V,
+                       uint16_t *__restrict__ O, int B, int H, int T, int causal, float c2, int snake) {
+  constexpr float kRaise = 8.0f;  // log2 of the largest unnormalised p
+  __shared__ __attribute__((aligned(16))) uint8_t lds[3][2][KB * HD * 2];  // [buf][K|V][tile]
+
+  const int BH = B * H, nq = T / KB, n = nq * BH;
+  int p = blockIdx.x;
+  if (snake > 0) {
+    const int r = p / snake;
+    if (r & 1) {
+      const int base = r * snake, cnt = min(n - base, snake), c = p - base;
+      if ((cnt & 7) == 0) p = base + (cnt / 8 - 1 - c / 8) * 8 + (c & 7);
+    }
+  }
+  const int lvl = p / BH, bh = p - lvl * BH;
+  const int q0 = (causal ? nq - 1 - lvl : lvl) * KB;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const long N = long(BH) * T;
+  const uint16_t *Kb = K + long(bh) * T;  // column offset into the [64, N] slab
+  const uint16_t *Vb = V + long(bh) * T * HD;
+  const int wrow0 = q0 + wave * 16;
+
+  uint4 qf[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+    qf[ks] = *reinterpret_cast<const uint4 *>(Q + (long(bh) * T + wrow0 + li) * HD + ks * 32 + lg * 8);
+  f32x4 o[4], osum = f32x4{0.f, 0.f, 0.f, 0.f};
+  float mrow = -1e30f;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint32_t one2 = DT == BF16 ? 0x3F803F80u : 0x3C003C00u;
+  const uint4 ones = make_uint4(one2, one2, one2, one2);
+
+  // staging: rows r0 and r0 + 32 of each tile, chunk c0
+  const int r0 = tid >> 3, c0 = tid & 7;
+  const int st_k0 = tswz<3>(r0, c0) * 16, st_k1 = tswz<3>(r0 + 32, c0) * 16;
+  const int st_v0 = tswz<2>(r0, c0) * 16, st_v1 = tswz<2>(r0 + 32, c0) * 16;
+  const int s16 = lane & 15, sr = s16 >> 2, sx = ((s16 & 3) >> 1) ^ (2 * (sr ^ (lg & 1))), sh = (s16 & 1) * 8;
+  const int rd_k = (8 * lg + sr) * 128 + sh;
+  const int rd_v = (4 * lg + sr) * 128 + sh;
+
+  const int ntiles = causal ? q0 / KB + 1 : nq;
+  const uint16_t *kp0 = Kb + long(r0) * N + c0 * 8, *kp1 = Kb + long(r0 + 32) * N + c0 * 8;
+  const uint16_t *vp0 = Vb + long(r0) * HD + c0 * 8, *vp1 = Vb + long(r0 + 32) * HD + c0 * 8;
+  // staging registers as native vectors (HIP's uint4 is a struct: arrays of
+  // it were copied through private memory); tile indices past the last tile
+  // re-read the last tile
+  typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(1))) const v4u gv4u;
+  v4u kr0, kr1, vr0, vr1;
+  auto gload = [&](int tile) {
+    const int tt = min(tile, ntiles - 1);
+    kr0 = *(gv4u *)(kp0 + tt * KB);
+    kr1 = *(gv4u *)(kp1 + tt * KB);
+    vr0 = *(gv4u *)(vp0 + tt * (KB * HD));
+    vr1 = *(gv4u *)(vp1 + tt * (KB * HD));
+  };
+  auto sstore = [&](int buf) {
+    *reinterpret_cast<v4u *>(&lds[buf][0][st_k0]) = kr0;
+    *reinterpret_cast<v4u *>(&lds[buf][0][st_k1]) = kr1;
+    *reinterpret_cast<v4u *>(&lds[buf][1][st_v0]) = vr0;
+    *reinterpret_cast<v4u *>(&lds[buf][1][st_v1]) = vr1;
+  };
+  // S^T = K Q^T: lane holds S[i = li][j = jt*16 + 4*lg + e]
+  auto kread = [&](const uint8_t *kt, uint4 (&kf)[2][4]) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        const uint8_t *p8 = kt + rd_k + ((2 * jt) ^ sx) * 16 + ks * 32 * 128;
+        const uint2 lo = lds_tr(p8), hi = lds_tr(p8 + 4 * 128);
+        kf[ks][jt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      }
+  };
+  auto kmma = [&](const uint4 (&kf)[2][4], f32x4 (&s)[4]) {
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      s[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      AttnMfma<DT>::mma(s[jt], kf[0][jt], qf[0]);
+    }
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) AttnMfma<DT>::mma(s[jt], kf[1][jt], qf[1]);
+  };
+  auto lane_max = [&](const float (&v)[16]) -> float {
+    float mx = fmaxf(fmaxf(v[0], v[1]), v[2]);
+#pragma unroll
+    for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, v[e]), v[e + 1]);
+    return fmaxf(mx, v[15]);
+  };
+  // round the scores and take this lane's max
+  auto round_scores16 = [&](const f32x4 (&s)[4], float (&v)[16]) -> float {
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[jt * 4 + e] = round1<DT>(s[jt][e]);
+    return lane_max(v);
+  };
+  // the diagonal tile (j0 = q0): key j0 + 16 jt + 4 lg + e is masked above
+  // row wrow0 + li; the max is taken again
+  auto mask_diag = [&](float (&v)[16]) -> float {
+    const int lim = wave * 16 + li - 4 * lg;
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (jt * 16 + e > lim) v[jt * 4 + e] = -INFINITY;
+    return lane_max(v);
+  };
+
+  gload(0);
+  sstore(0);
+  gload(1);
+  sstore(1);
+  gload(2);  // tile 2 (or the last tile again) in the staging registers
+  __syncthreads();
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+    asm volatile("" : "+v"(qf[ks].x), "+v"(qf[ks].y), "+v"(qf[ks].z), "+v"(qf[ks].w)::"memory");
+  float v[16];
+  float mx;
+  {
+    uint4 kf[2][4];
+    f32x4 s0[4];
+    kread(lds[0][0], kf);
+    kmma(kf, s0);
+    mx = round_scores16(s0, v);
+    if (causal && ntiles == 1) mx = mask_diag(v);
+  }
+
+  // trip t: tile t's scores in v (rounded, masked) with this lane's max mx;
+  // tile t in buffer bc, tile t + 1 in bn, tile t + 2 goes to bf
+  auto trip = [&](int t, auto bcc, auto bnc, auto bfc) {
+    constexpr int bc = decltype(bcc)::value, bn = decltype(bnc)::value, bf = decltype(bfc)::value;
+    // raise the row max only when some lane's own max exceeds it by 2^kRaise
+    if (__any(mx * c2 > mrow + kRaise)) {
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mnew = fmaxf(mrow, mx * c2);
+      const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
+      mrow = mnew;
+      osum *= alpha;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) o[d] *= alpha;
+    }
+    const float nm = -mrow;
+    // one block: fragment reads, the exponentials beside S(t+1), the PV
+    // MFMAs beside the staging and the rounding of S(t+1)
+    uint4 kf[2][4];
+    kread(lds[bn][0], kf);
+    const uint8_t *vt = lds[bc][1];
+    uint4 vf[2][4];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const uint8_t *p8 = vt + rd_v + ((2 * dt) ^ sx) * 16 + kk * 32 * 128;
+        const uint2 lo = lds_tr(p8), hi = lds_tr(p8 + 16 * 128);
+        vf[kk][dt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      }
+    uint32_t pk[8];
+#pragma unroll
+    for (int e = 0; e < 16; e += 2)
+      pk[e >> 1] = AttnMfma<DT>::cvt2(__builtin_amdgcn_exp2f(__builtin_fmaf(v[e], c2, nm)),
+                                      __builtin_amdgcn_exp2f(__builtin_fmaf(v[e + 1], c2, nm)));
+    f32x4 sn[4];
+    kmma(kf, sn);
+    // (keeps the S MFMAs in phase 1: without a use here the instruction
+    // selection may move them after the barrier below)
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) asm volatile("" : "+v"(sn[jt]));
+    // phase 1: the 16 K fragment reads; 8 VALU; 8 x (S MFMA, 4 VALU, 2 V
+    // fragment reads): the V reads spread over the phase instead of queueing
+    // behind the K reads
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+    __builtin_amdgcn_sched_group_barrier(0x402, 8, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x402, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const uint4 pf = make_uint4(pk[4 * kk], pk[4 * kk + 1], pk[4 * kk + 2], pk[4 * kk + 3]);
+      AttnMfma<DT>::mma(osum, ones, pf);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) AttnMfma<DT>::mma(o[dt], vf[kk][dt], pf);
+    }
+    sstore(bf);
+    gload(t + 3);
+    mx = round_scores16(sn, v);
+    // phase 2: 10 x (PV MFMA, 3 VALU, one staging store or load)
+#pragma unroll
+    for (int i = 0; i < 10; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x402, 3, 0);
+      if (i < 4) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+      else if (i < 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+    if (causal && t + 2 == ntiles) mx = mask_diag(v);
+    __syncthreads();
+  };
+  int t = 0;
+  for (; t + 3 <= ntiles; t += 3) {
+    trip(t, BufIdx<0>{}, BufIdx<1>{}, BufIdx<2>{});
+    trip(t + 1, BufIdx<1>{}, BufIdx<2>{}, BufIdx<0>{});
+    trip(t + 2, BufIdx<2>{}, BufIdx<0>{}, BufIdx<1>{});
+  }
+  if (t < ntiles) trip(t, BufIdx<0>{}, BufIdx<1>{}, BufIdx<2>{});
+  if (t + 1 < ntiles) trip(t + 1, BufIdx<1>{}, BufIdx<2>{}, BufIdx<0>{});
+
+  const int b = bh / H, h = bh - b * H;
+  const long E = long(H) * HD;
+  const int i = wrow0 + li;
+  const float inv = 1.0f / osum[0];
+  uint16_t *dst = O + (long(b) * T + i) * E + long(h) * HD;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    u16x4 w;
+    w.x = Store<DT>::enc(o[dt][0] * inv);
+    w.y = Store<DT>::enc(o[dt][1] * inv);
+    w.z = Store<DT>::enc(o[dt][2] * inv);
+    w.w = Store<DT>::enc(o[dt][3] * inv);
+    *reinterpret_cast<u16x4 *>(dst + dt * 16 + lg * 4) = w;
+  }
+}
+
 // Generic attention: one wave per (query row, bh); scores in LDS.
 template <int DT>
 __global__ void __launch_bounds__(64)
@@ -618,6 +878,29 @@ int tr_rows_env() {
   const int v = e ? std::atoi(e) : 0;
   return (v == 1 || v == 2) ? v : 0;
 }
+// tuning overrides, read per call (so tests can compare the kernels in one
+// process): MUNET_HIP_ATTN_KERNEL=tr keeps the single-trip flash kernel;
+// MUNET_HIP_ATTN_ORDER=0 keeps the plain heaviest-first order
+bool pipe_kernel_env() {
+  const char *e = std::getenv("MUNET_HIP_ATTN_KERNEL");
+  return !(e && std::string(e) == "tr");
+}
+bool snake_order_env() {
+  const char *e = std::getenv("MUNET_HIP_ATTN_ORDER");
+  return !(e && std::string(e) == "0");
+}
+// compute units of the current device (one workgroup round of the snake order)
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 0;
+    cached[dev] = cus > 0 ? cus : -1;
+  }
+  return cached[dev] > 0 ? cached[dev] : 0;
+}
 }  // namespace
 
 hipError_t attention(int dt, const void *q, const void *k, const void *v, void *ctx, int B, int H, int T, int hd,
@@ -634,6 +917,23 @@ hipError_t attention(int dt, const void *q, const void *k, const void *v, void *
     uint16_t *O = (uint16_t *)ctx;
     if (dt == BF16) hipLaunchKernelGGL((flash_attn_tr_kernel<BF16, 1, true>), grid, dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2);
     else hipLaunchKernelGGL((flash_attn_tr_kernel<F16, 1, true>), grid, dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2);
+    return hipGetLastError();
+  }
+  const bool use_pipe = pipe_kernel_env();
+  if (use_pipe && !textbook && !force_generic && hd == HD && (dt == BF16 || dt == F16) && aligned && T % KB == 0 &&
+      pow2(scale)) {
+    const long items = long(T / KB) * B * H;
+    if (items > 0x7fffffffL) return hipErrorInvalidValue;
+    const bool snake_ok = snake_order_env();
+    const int cus = cu_count();
+    const int snake = (snake_ok && causal && cus > 0 && items > cus) ? cus : 0;
+    const float c2 = scale * 1.4426950408889634f;
+    const uint16_t *Q = (const uint16_t *)q, *K = (const uint16_t *)k, *V = (const uint16_t *)v;
+    uint16_t *O = (uint16_t *)ctx;
+    if (dt == BF16)
+      hipLaunchKernelGGL((flash_attn_pipe_kernel<BF16>), dim3(unsigned(items)), dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2, snake);
+    else
+      hipLaunchKernelGGL((flash_attn_pipe_kernel<F16>), dim3(unsigned(items)), dim3(256), 0, st, Q, K, V, O, B, H, T, causal, c2, snake);
     return hipGetLastError();
   }
   if (!textbook && !force_generic && hd == HD && (dt == BF16 || dt == F16) && aligned && T % 8 == 0 && pow2(scale)) {

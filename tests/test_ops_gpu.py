@@ -97,7 +97,9 @@ def _mha_params(E, dt, seed):
 
 @pytest.mark.parametrize("dt", [F16, BF16, F32])
 @pytest.mark.parametrize("B,T,H,hd", [(2, 64, 2, 64), (1, 200, 3, 64), (64, 72, 4, 64), (1, 77, 2, 64),
-                                      (2, 40, 2, 32), (1, 3, 2, 4)])
+                                      (2, 40, 2, 32), (1, 3, 2, 4),
+                                      (1, 128, 2, 64), (2, 192, 3, 64), (1, 320, 2, 64), (5, 256, 16, 64),
+                                      (1, 384, 47, 64)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_attention_core(hip, orc, dt, B, T, H, hd, causal):
     """q/k/v projection (fused head split) + fused attention vs the reference
@@ -123,6 +125,32 @@ def test_attention_core(hip, orc, dt, B, T, H, hd, causal):
     ctx = empty((B * T, E), dt)
     hip.attention(q, k, v, ctx, B, H, T, hd, causal)
     assert_close(to_host(ctx, dt), ref, dt, what="attention")
+
+
+@pytest.mark.parametrize("dt", [F16, BF16])
+@pytest.mark.parametrize("B,T,H", [(4, 1024, 12), (1, 128, 2), (2, 192, 3), (5, 256, 16), (1, 384, 47), (8, 256, 8)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_pipelined_kernel_bits(hip, dt, B, T, H, causal, monkeypatch):
+    """The software-pipelined flash kernel (T % 64 == 0) gives the bits of the
+    single-trip kernel it replaces, in both work orders, at the decoder's full
+    size and over the trip remainders (1-6 and 16 key tiles) and partial
+    second rounds of the CU-paired order."""
+    hd = 64
+    q, k, v = (to_device(rand((B * H * T * hd,), dt, 70 + i, 0.5), dt) for i in range(3))
+    outs = {}
+    for name, env in (("pipe", {}), ("pipe_plain_order", {"MUNET_HIP_ATTN_ORDER": "0"}),
+                      ("tr", {"MUNET_HIP_ATTN_KERNEL": "tr"})):
+        monkeypatch.delenv("MUNET_HIP_ATTN_ORDER", raising=False)
+        monkeypatch.delenv("MUNET_HIP_ATTN_KERNEL", raising=False)
+        for key, val in env.items():
+            monkeypatch.setenv(key, val)
+        ctx = empty((B * T, H * hd), dt)
+        hip.attention(q, k, v, ctx, B, H, T, hd, causal)
+        hip.synchronize()
+        outs[name] = to_host(ctx, dt)
+    assert np.all(np.isfinite(dec(outs["pipe"], dt)))
+    for name in ("pipe_plain_order", "tr"):
+        assert np.array_equal(outs["pipe"], outs[name]), f"pipelined kernel differs from {name}"
 
 
 @pytest.mark.parametrize("dt", DTS)
