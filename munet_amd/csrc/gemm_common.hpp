@@ -44,11 +44,17 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 }
 __device__ __forceinline__ float lo_bf16(uint32_t p) { return __uint_as_float(p << 16); }
 __device__ __forceinline__ float hi_bf16(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
-// round 4 floats through bf16 in place; returns the packed bits
-__device__ __forceinline__ uint2 round4_bf16(float v[4]) {
-  const uint32_t p0 = pack_bf16x2(v[0], v[1]), p1 = pack_bf16x2(v[2], v[3]);
-  v[0] = lo_bf16(p0); v[1] = hi_bf16(p0); v[2] = lo_bf16(p1); v[3] = hi_bf16(p1);
-  return make_uint2(p0, p1);
+// round a float through bf16 with one instruction: packing (0, x) leaves
+// bf16(x) in the high half and zero in the low half, i.e. round(x) as a float
+__device__ __forceinline__ float round1_bf16(float x) { return __uint_as_float(pack_bf16x2(0.f, x)); }
+// round 4 floats through bf16 in place
+__device__ __forceinline__ void round4_inplace_bf16(float v[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = round1_bf16(v[i]);
+}
+// 4 floats -> packed bf16 (rounds; exact for values already rounded)
+__device__ __forceinline__ uint2 pack4_bf16(const float v[4]) {
+  return make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
 }
 
 // Destination of output element (m, n) for the epilogue modes.
@@ -89,75 +95,74 @@ template <int DT> __device__ __forceinline__ bool epi_fast(const EpiArgs &ep, in
 
 // The bf16 fast path's arithmetic: the rounded, packed 4 output values, with
 // the bias and the residual already loaded (callers batch those loads).
+// Intermediate results are rounded in place; the last one by the final pack.
 __device__ __forceinline__ uint2 epi_fast_bf16_value(const EpiArgs &ep, float v[4], uint2 bias, uint2 resid) {
-  uint2 pk;
   if (ep.bias && ep.bias_first) {
     v[0] += lo_bf16(bias.x); v[1] += hi_bf16(bias.x); v[2] += lo_bf16(bias.y); v[3] += hi_bf16(bias.y);
-    pk = round4_bf16(v);
+    round4_inplace_bf16(v);
   } else {
-    pk = round4_bf16(v);
+    round4_inplace_bf16(v);
     if (ep.bias) {
       v[0] += lo_bf16(bias.x); v[1] += hi_bf16(bias.x); v[2] += lo_bf16(bias.y); v[3] += hi_bf16(bias.y);
-      pk = round4_bf16(v);
+      round4_inplace_bf16(v);
     }
   }
   if (ep.act == ACT_RELU) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = v[i] > 0.0f ? v[i] : 0.0f;
-    pk = round4_bf16(v);  // exact: re-packs the rounded values
+    for (int i = 0; i < 4; ++i) v[i] = v[i] > 0.0f ? v[i] : 0.0f;  // exact on rounded values
   } else if (ep.act == ACT_GELU) {
     float t[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) t[i] = v[i] * ep.gelu_c;
-    round4_bf16(t);
+    round4_inplace_bf16(t);
 #pragma unroll
     for (int i = 0; i < 4; ++i) t[i] = sigmoidf_ref(t[i]);
-    round4_bf16(t);
+    round4_inplace_bf16(t);
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] *= t[i];
-    pk = round4_bf16(v);
+    round4_inplace_bf16(v);
   }
   if (ep.resid) {
     v[0] = lo_bf16(resid.x) + v[0]; v[1] = hi_bf16(resid.x) + v[1];
     v[2] = lo_bf16(resid.y) + v[2]; v[3] = hi_bf16(resid.y) + v[3];
-    pk = round4_bf16(v);
   }
-  return pk;
+  return pack4_bf16(v);
 }
 
 // The same chain with the epilogue kind fixed at compile time (bias added
 // after the matmul rounding, activation, residual): no runtime branches per
-// fragment, and the last rounding only packs.
+// fragment; every step but the last rounds in place (one instruction per
+// value), the last step's rounding is the final pack.
 template <bool BIAS, int ACT, bool RESID>
 __device__ __forceinline__ uint2 epi_fast_bf16_fixed(float v[4], uint2 bias, uint2 resid, float gelu_c) {
-  constexpr bool more = BIAS || ACT != ACT_NONE || RESID;
-  uint2 pk = more ? round4_bf16(v) : make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+  if constexpr (!BIAS && ACT == ACT_NONE && !RESID) return pack4_bf16(v);
+  round4_inplace_bf16(v);
   if constexpr (BIAS) {
     v[0] += lo_bf16(bias.x); v[1] += hi_bf16(bias.x); v[2] += lo_bf16(bias.y); v[3] += hi_bf16(bias.y);
-    pk = round4_bf16(v);
+    if constexpr (ACT == ACT_NONE && !RESID) return pack4_bf16(v);
+    round4_inplace_bf16(v);
   }
   if constexpr (ACT == ACT_RELU) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = v[i] > 0.0f ? v[i] : 0.0f;
-    pk = round4_bf16(v);
+    for (int i = 0; i < 4; ++i) v[i] = v[i] > 0.0f ? v[i] : 0.0f;  // exact on rounded values
   } else if constexpr (ACT == ACT_GELU) {
     float t[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) t[i] = v[i] * gelu_c;
-    round4_bf16(t);
+    round4_inplace_bf16(t);
 #pragma unroll
     for (int i = 0; i < 4; ++i) t[i] = sigmoidf_ref(t[i]);
-    round4_bf16(t);
+    round4_inplace_bf16(t);
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] *= t[i];
-    pk = round4_bf16(v);
+    if constexpr (!RESID) return pack4_bf16(v);
+    round4_inplace_bf16(v);
   }
   if constexpr (RESID) {
     v[0] = lo_bf16(resid.x) + v[0]; v[1] = hi_bf16(resid.x) + v[1];
     v[2] = lo_bf16(resid.y) + v[2]; v[3] = hi_bf16(resid.y) + v[3];
-    pk = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
   }
-  return pk;
+  return pack4_bf16(v);
 }
 
 // The bf16 fast path for output columns n..n+3 of row m.
