@@ -135,6 +135,12 @@ int mh_embedding_pos(int dt, const int32_t *ids, const void *tok_w, const void *
                      int D, int T, void *stream);
 /* Tensor::to(DataType) (src/tensor.cpp:249-284) on device memory. */
 int mh_convert(int src_dt, const void *in, int dst_dt, void *out, size_t n, void *stream);
+/* No counterpart in the reference: a self-check of the kernels' fast fp16
+ * rounding (zero and the normal half range by a bit trick, the rest by the
+ * full codec that mh_convert uses) against that codec over all 2^32 float
+ * bit patterns; *mismatches receives the count of patterns that differ in any
+ * bit (0 when the fast path is exact).  Synchronises `stream`. */
+int mh_check_f16_rounding(unsigned long long *mismatches, void *stream);
 /* Row argmax, first index of the maximum (the demos' np.argmax). */
 int mh_argmax(int dt, const void *x, int32_t *out, int rows, int cols, void *stream);
 /* Measured matrix-core peak of this GPU in FLOP/s: a full grid of waves

@@ -52,6 +52,7 @@ _SIGS = {
     "mh_embedding": [_i, _vp, _vp, _vp, _i, _i, _i, _vp],
     "mh_embedding_pos": [_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
     "mh_convert": [_i, _vp, _i, _vp, _sz, _vp],
+    "mh_check_f16_rounding": [ctypes.POINTER(ctypes.c_ulonglong), _vp],
     "mh_argmax": [_i, _vp, _vp, _i, _i, _vp],
     "mh_measure_mfma_peak": [_i, _i, ctypes.POINTER(ctypes.c_double), _vp],
     "mh_measure_hbm_read": [_vp, _sz, _i, ctypes.POINTER(ctypes.c_double), _vp],

@@ -242,6 +242,13 @@ class HipBackend:
     def convert(self, x, out, n):
         call("mh_convert", _dt(x), _p(x), _dt(out), _p(out), n, _stream())
 
+    def check_f16_rounding(self) -> int:
+        """Float bit patterns (of all 2^32) where the kernels' fast fp16
+        rounding differs from the full codec (no reference counterpart)."""
+        n = ctypes.c_ulonglong(0)
+        call("mh_check_f16_rounding", ctypes.byref(n), _stream())
+        return n.value
+
     def argmax(self, x, out, rows, cols):
         call("mh_argmax", _dt(x), _p(x), _p(out), rows, cols, _stream())
 

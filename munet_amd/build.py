@@ -25,7 +25,7 @@ PLUGIN = os.path.join(HERE, "libmunet_backend_hip.so")
 ARCH = "gfx950"
 
 KERNEL_SOURCES = ["gemm.hip", "gemm_pipe.hip", "gemm_pipe_fixed_staged.hip", "gemm_pipe_fixed_dma.hip",
-                  "gemm_pipe_wide.hip", "gemm_pipe_big.hip", "gemm_pipe_head.hip", "gemm_dma.hip", "attention.hip", "decode.hip",
+                  "gemm_pipe_wide.hip", "gemm_pipe_big.hip", "gemm_pipe_conv.hip", "gemm_pipe_head.hip", "gemm_dma.hip", "attention.hip", "decode.hip",
                   "eltwise.hip",
                   "norm.hip", "layout.hip", "peak.hip"]
 HOST_SOURCES = ["capi.cpp", "engine.cpp", "artifact.cpp"]
@@ -57,6 +57,7 @@ def _flags():
 _VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 SOURCE_FLAGS = {"attention.hip": _VGPR_FORM, "gemm_pipe.hip": _VGPR_FORM, "gemm_pipe_fixed_staged.hip": _VGPR_FORM,
                 "gemm_pipe_fixed_dma.hip": _VGPR_FORM, "gemm_pipe_wide.hip": _VGPR_FORM,
+                "gemm_pipe_conv.hip": _VGPR_FORM,
                 # the peak loop: with accumulation registers every trip copied
                 # each accumulator through ordinary VGPRs
                 "peak.hip": _VGPR_FORM}

@@ -416,6 +416,12 @@ int mh_convert(int sdt, const void *in, int ddt, void *out, size_t n, void *stre
     hip_check(convert(sdt, in, ddt, out, n, S_(stream)), "convert");
   })
 }
+int mh_check_f16_rounding(unsigned long long *mismatches, void *stream) {
+  MH_TRY({
+    if (!mismatches) throw Error("check_f16_rounding: mismatches must be set");
+    hip_check(check_f16_rounding(mismatches, S_(stream)), "check_f16_rounding");
+  })
+}
 int mh_argmax(int dt, const void *x, int32_t *out, int rows, int cols, void *stream) {
   MH_TRY({
     check_dt(dt);

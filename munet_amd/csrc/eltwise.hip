@@ -302,6 +302,44 @@ hipError_t masked_fill(int dt, const void *x, const int32_t *mask, void *out, si
   return hipGetLastError();
 }
 
+// Every float bit pattern through the kernels' fp16 roundings (the
+// branch-free one, and the four-wide one with its fast path) and through the
+// full codec: counts the patterns where either differs in any bit.  Lane l
+// of a wave takes patterns base + 4 l .. + 3, so a wave covers 256
+// consecutive patterns per trip and fast-path and fallback waves both occur.
+__global__ void __launch_bounds__(256) f16_round_check_kernel(unsigned long long *mismatches) {
+  const uint32_t base = (blockIdx.x * 256u + (threadIdx.x >> 6) * 64u) * 256u + (threadIdx.x & 63u) * 4u;
+  uint32_t bad = 0;
+  for (uint32_t i = 0; i < 64u; ++i) {
+    const uint32_t p0 = base + i * 256u;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = __uint_as_float(p0 + e);
+    round4_f16(v);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float x = __uint_as_float(p0 + e);
+      const uint32_t ref = __float_as_uint(round_f16_ref(x));
+      bad += (__float_as_uint(v[e]) != ref) + (__float_as_uint(round_f16_exact(x)) != ref);
+    }
+  }
+  if (bad) atomicAdd(mismatches, (unsigned long long)bad);
+}
+
+hipError_t check_f16_rounding(unsigned long long *mismatches, hipStream_t st) {
+  unsigned long long *d = nullptr;
+  hipError_t e = hipMalloc(&d, sizeof(*d));
+  if (e != hipSuccess) return e;
+  if ((e = hipMemsetAsync(d, 0, sizeof(*d), st)) == hipSuccess) {
+    hipLaunchKernelGGL(f16_round_check_kernel, dim3(65536), dim3(256), 0, st, d);  // 2^32 patterns
+    if ((e = hipGetLastError()) == hipSuccess &&
+        (e = hipMemcpyAsync(mismatches, d, sizeof(*d), hipMemcpyDeviceToHost, st)) == hipSuccess)
+      e = hipStreamSynchronize(st);
+  }
+  const hipError_t f = hipFree(d);
+  return e != hipSuccess ? e : f;
+}
+
 hipError_t convert(int sdt, const void *in, int ddt, void *out, size_t n, hipStream_t st) {
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(convert_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, in, sdt, out, ddt, n);

@@ -396,6 +396,11 @@ hipError_t conv_nhwc(int dt, const void *x, const void *w_ohwi, const ConvArgs &
                      int tile_hint, hipStream_t st) {
   const int M = cv.B * cv.oH * cv.oW, K = cv.kH * cv.kW * cv.iC;
   if (M <= 0 || oC <= 0) return hipSuccess;
+  // 16-bit convolutions with whole 64-channel slabs run on the pipelined
+  // kernel; MUNET_HIP_CONV_KERNEL=general (read per call) keeps this one
+  const char *ck = std::getenv("MUNET_HIP_CONV_KERNEL");
+  if (tile_hint < 0 && !(ck && std::string(ck) == "general") && gemm_pipe_conv_ok(dt, x, w_ohwi, cv))
+    return gemm_pipe_conv(dt, x, w_ohwi, cv, oC, ep, st);
   switch (dt) {
   case F32: return launch_dt<F32>(x, w_ohwi, M, oC, K, 0, K, 1, 0, 0, 0, ep, &cv, tile_hint, st);
   case F16: return launch_dt<F16>(x, w_ohwi, M, oC, K, 0, K, 1, 0, 0, 0, ep, &cv, tile_hint, st);

@@ -57,6 +57,14 @@ __device__ __forceinline__ uint2 pack4_bf16(const float v[4]) {
   return make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
 }
 
+// fp16 counterparts: decode a packed pair, and pack two values that are
+// already fp16-representable (the round-toward-zero conversion is then exact)
+__device__ __forceinline__ float lo_f16(uint32_t p) { return f16_to_f32(uint16_t(p & 0xffffu)); }
+__device__ __forceinline__ float hi_f16(uint32_t p) { return f16_to_f32(uint16_t(p >> 16)); }
+__device__ __forceinline__ uint32_t pack_f16x2_exact(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+
 // Destination of output element (m, n) for the epilogue modes.
 // `off` is an element offset added to row-major outputs (the batch slice).
 template <typename T>
@@ -90,7 +98,7 @@ __device__ __forceinline__ T *epi_dst(const EpiArgs &ep, int m, int n, long off)
 // Fast-path eligibility: bf16, a full 4-column group, row-major or head-split
 // output, and 8-byte aligned bias / residual rows.
 template <int DT> __device__ __forceinline__ bool epi_fast(const EpiArgs &ep, int n, int N) {
-  return DT == BF16 && n + 4 <= N && ep.mode != EPI_CONVT && (!ep.resid || (ep.ldr & 3) == 0);
+  return (DT == BF16 || DT == F16) && n + 4 <= N && ep.mode != EPI_CONVT && (!ep.resid || (ep.ldr & 3) == 0);
 }
 
 // The bf16 fast path's arithmetic: the rounded, packed 4 output values, with
@@ -129,6 +137,48 @@ __device__ __forceinline__ uint2 epi_fast_bf16_value(const EpiArgs &ep, float v[
   return pack4_bf16(v);
 }
 
+// The fp16 fast path: the same chain with the reference's fp16 rounding
+// (round4_f16) after every op; the rounded values pack exactly.
+__device__ __forceinline__ uint2 epi_fast_f16_value(const EpiArgs &ep, float v[4], uint2 bias, uint2 resid) {
+  if (ep.bias && ep.bias_first) {
+    v[0] += lo_f16(bias.x); v[1] += hi_f16(bias.x); v[2] += lo_f16(bias.y); v[3] += hi_f16(bias.y);
+    round4_f16(v);
+  } else {
+    round4_f16(v);
+    if (ep.bias) {
+      v[0] += lo_f16(bias.x); v[1] += hi_f16(bias.x); v[2] += lo_f16(bias.y); v[3] += hi_f16(bias.y);
+      round4_f16(v);
+    }
+  }
+  if (ep.act == ACT_RELU) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = v[i] > 0.0f ? v[i] : 0.0f;  // exact on rounded values
+  } else if (ep.act == ACT_GELU) {
+    float t[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[i] = v[i] * ep.gelu_c;
+    round4_f16(t);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[i] = sigmoidf_ref(t[i]);
+    round4_f16(t);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] *= t[i];
+    round4_f16(v);
+  }
+  if (ep.resid) {
+    v[0] = lo_f16(resid.x) + v[0]; v[1] = hi_f16(resid.x) + v[1];
+    v[2] = lo_f16(resid.y) + v[2]; v[3] = hi_f16(resid.y) + v[3];
+    round4_f16(v);
+  }
+  return make_uint2(pack_f16x2_exact(v[0], v[1]), pack_f16x2_exact(v[2], v[3]));
+}
+
+template <int DT>
+__device__ __forceinline__ uint2 epi_fast_value(const EpiArgs &ep, float v[4], uint2 bias, uint2 resid) {
+  if constexpr (DT == F16) return epi_fast_f16_value(ep, v, bias, resid);
+  else return epi_fast_bf16_value(ep, v, bias, resid);
+}
+
 // The same chain with the epilogue kind fixed at compile time (bias added
 // after the matmul rounding, activation, residual): no runtime branches per
 // fragment; every step but the last rounds in place (one instruction per
@@ -165,10 +215,11 @@ __device__ __forceinline__ uint2 epi_fast_bf16_fixed(float v[4], uint2 bias, uin
   return pack4_bf16(v);
 }
 
-// The bf16 fast path for output columns n..n+3 of row m.
-__device__ __forceinline__ void epi_fast_bf16(const EpiArgs &ep, int m, int n, float v[4], uint2 bias, uint2 resid,
-                                              long off) {
-  const uint2 pk = epi_fast_bf16_value(ep, v, bias, resid);
+// The 16-bit fast path for output columns n..n+3 of row m.
+template <int DT>
+__device__ __forceinline__ void epi_fast16(const EpiArgs &ep, int m, int n, float v[4], uint2 bias, uint2 resid,
+                                           long off) {
+  const uint2 pk = epi_fast_value<DT>(ep, v, bias, resid);
   uint16_t *dst = epi_dst<uint16_t>(ep, m, n, off);
   if (((uintptr_t)dst & 7) == 0) {
     *reinterpret_cast<uint2 *>(dst) = pk;
@@ -186,7 +237,7 @@ __device__ __forceinline__ void epi_store4(const EpiArgs &ep, int m, int n, int 
     const uint2 b = ep.bias ? *reinterpret_cast<const uint2 *>(static_cast<const T *>(ep.bias) + n) : make_uint2(0, 0);
     const uint2 r = ep.resid ? *reinterpret_cast<const uint2 *>(static_cast<const T *>(ep.resid) + long(m) * ep.ldr + n)
                              : make_uint2(0, 0);
-    epi_fast_bf16(ep, m, n, v, b, r, off);
+    epi_fast16<DT>(ep, m, n, v, b, r, off);
     return;
   }
   // generic path (fp32, fp16, tails, transposed-conv scatter)

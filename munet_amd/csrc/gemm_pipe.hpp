@@ -204,8 +204,8 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
 
   __device__ __forceinline__ PipeEpi(const EpiArgs &ep, const G &g_, int M_, int N_, int m0_, int n0_)
       : g(g_), M(M_), N(N_), m0(m0_), n0(n0_),
-        fast(KT_::FIXED ||
-             (DT == BF16 && ep.mode != EPI_CONVT && N_ % 4 == 0 && (!ep.resid || (ep.ldr & 3) == 0))) {}
+        fast(KT_::FIXED || ((DT == BF16 || DT == F16) && ep.mode != EPI_CONVT && N_ % 4 == 0 &&
+                            (!ep.resid || (ep.ldr & 3) == 0))) {}
 
   __device__ __forceinline__ uint2 bload(const EpiArgs &ep, int j) const {
     const uint16_t *bias = static_cast<const uint16_t *>(ep.bias);
@@ -555,7 +555,7 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
           const int n = n0 + wn * WTN + j * 16 + lg * 4;
           if (m < M && n < N) {
             float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-            const uint2 pk = epi_fast_bf16_value(ep, v, bq[j], RQ(i, j));
+            const uint2 pk = epi_fast_value<DT>(ep, v, bq[j], RQ(i, j));
             uint16_t *dst = cbase[j] + roff[i];
             if (al8) {
               *reinterpret_cast<uint2 *>(dst) = pk;
@@ -580,10 +580,18 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
   _Pragma("unroll") for (int i = 0; i < FM; ++i) _Pragma("unroll") for (int j = 0; j < FN; ++j)   \
       PipeMfma<DT>::mma0(acc[i][j], BF[j], AF[i]);
 
-template <int DT, int BM, int BN, int WGM, int WGN, int EK>
+// CONV: implicit-GEMM convolution (M = output pixels, N = oC, K = kH*kW*iC)
+// on an NHWC activation A with OHWI weights Bt, iC % 64 == 0, so every
+// 64-wide K slab is one filter tap (kh, kw) and 64 consecutive channels.
+// Each thread keeps, per A row, the byte offset of the row's tap (0, 0)
+// chunk and a bit mask of its taps that fall inside the image; a slab adds
+// the tap's offset (a scalar) and loads through a buffer resource, taps in
+// the padding reading an offset past the resource's end, which the hardware
+// returns as zeros.
+template <int DT, int BM, int BN, int WGM, int WGN, int EK, bool CONV = false>
 __global__ void __launch_bounds__(WGM * WGN * 64)
 gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt, int M, int N, int K, long lda,
-                 long ldb, long sa, long sb, long sc, EpiArgs ep) {
+                 long ldb, long sa, long sb, long sc, EpiArgs ep, ConvArgs cv) {
   typedef PipeGeom<BM, BN, WGM, WGN> G;
   constexpr int NT = G::NT, BK = 64, FM = G::FM, FN = G::FN;
   constexpr int ACH = BM * 8 / NT, BCH = BN * 8 / NT;
@@ -606,17 +614,60 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
   // which advance one slab per K step (the host checks they fit).
   constexpr int RSTEP = NT / 8;
   const int c0 = tid & 7, r0 = tid >> 3;
-  uint32_t aoff[ACH], boff[BCH];
+  uint32_t aoff[CONV ? 1 : ACH], boff[BCH];
+  int32_t cvoff[CONV ? ACH : 1];
+  uint32_t cvmask[CONV ? ACH : 1];
+  if constexpr (CONV) {
 #pragma unroll
-  for (int i = 0; i < ACH; ++i) aoff[i] = uint32_t(min(m0 + r0 + RSTEP * i, M - 1)) * uint32_t(lda) + c0 * 8;
+    for (int i = 0; i < ACH; ++i) {
+      const int m = min(m0 + r0 + RSTEP * i, M - 1);
+      const int ow = m % cv.oW, t2 = m / cv.oW, oh = t2 % cv.oH, b = t2 / cv.oH;
+      const int ih0 = oh * cv.s - cv.p, iw0 = ow * cv.s - cv.p;
+      cvoff[i] = ((b * cv.iH + ih0) * cv.iW + iw0) * int(cv.ldx) * 2 + c0 * 16;
+      uint32_t msk = 0;
+      for (int kh = 0; kh < cv.kH; ++kh)
+        for (int kw = 0; kw < cv.kW; ++kw)
+          if (unsigned(ih0 + kh) < unsigned(cv.iH) && unsigned(iw0 + kw) < unsigned(cv.iW)) msk |= 1u << (kh * cv.kW + kw);
+      cvmask[i] = msk;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) aoff[i] = uint32_t(min(m0 + r0 + RSTEP * i, M - 1)) * uint32_t(lda) + c0 * 8;
+  }
 #pragma unroll
   for (int i = 0; i < BCH; ++i) boff[i] = uint32_t(min(n0 + r0 + RSTEP * i, N - 1)) * uint32_t(ldb) + c0 * 8;
+  // CONV slab state (wave-uniform): tap (kh, kw), first channel, and the
+  // tap's byte offset from a row's tap (0, 0)
+  const __amdgpu_buffer_rsrc_t xres =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(A), 0, CONV ? cv.B * cv.iH * cv.iW * int(cv.ldx) * 2 : 0,
+                                        0x00020000);
+  int ckh = 0, ckw = 0, cic = 0, ctap = 0, csoff = 0;
+  auto conv_next = [&]() {
+    cic += 64;
+    if (cic == cv.iC) {
+      cic = 0;
+      if (++ckw == cv.kW) {
+        ckw = 0;
+        ++ckh;
+      }
+      ctap = ckh * cv.kW + ckw;
+    }
+    csoff = ((ckh * cv.iW + ckw) * int(cv.ldx) + cic) * 2;
+  };
+  auto conv_chunk = [&](int i) -> u32x4 {
+    const uint32_t voff = ((cvmask[i] >> ctap) & 1u) ? uint32_t(cvoff[i] + csoff) : 0x80000000u;
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, voff, 0, 0));
+  };
   const int sw = r0 * 8 + (c0 ^ (r0 & 7));  // row r0 + RSTEP * i sits at sw + RSTEP * 8 * i
   const uint16_t *As = A, *Bs = Bt;
   u32x4 ra[ACH], rb[BCH];
 #define MH_PGLOAD()                                                                                \
   {                                                                                                \
-    _Pragma("unroll") for (int i = 0; i < ACH; ++i) ra[i] = ldg16(As + aoff[i]);                   \
+    if constexpr (CONV) {                                                                          \
+      _Pragma("unroll") for (int i = 0; i < ACH; ++i) ra[i] = conv_chunk(i);                       \
+    } else {                                                                                       \
+      _Pragma("unroll") for (int i = 0; i < ACH; ++i) ra[i] = ldg16(As + aoff[i]);                 \
+    }                                                                                              \
     _Pragma("unroll") for (int i = 0; i < BCH; ++i) rb[i] = ldg16(Bs + boff[i]);                   \
   }
 #define MH_PSTORE(L)                                                                               \
@@ -660,7 +711,9 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
   u32x4 *L0 = lds[0], *L1 = lds[1];
   typename Epi::LnIn lnin;
   if constexpr (PipeKindT<EK>::LN) epi.ln_issue(ep, lnin, tid);
-  {
+  if constexpr (CONV) {  // K % 64 == 0: slab 0 is whole
+    MH_PGLOAD();
+  } else {
     const bool cin = c0 * 8 < K0;
 #pragma unroll
     for (int i = 0; i < ACH; ++i) ra[i] = cin ? ldg16(As + aoff[i]) : u32x4{0, 0, 0, 0};
@@ -676,7 +729,8 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
     MH_PMMA0(af0, bf0);
     MH_PMMA(af1, bf1);
   } else {
-    As += K0;
+    if constexpr (CONV) conv_next();
+    else As += K0;
     Bs += K0;
     MH_PGLOAD();
     __syncthreads();
@@ -690,7 +744,8 @@ gemm_pipe_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt
   {                                                                                                \
     MH_PSTORE(L1);                                                                                 \
     if ((KNEXT) < KT) {                                                                            \
-      As += BK;                                                                                    \
+      if constexpr (CONV) conv_next();                                                             \
+      else As += BK;                                                                               \
       Bs += BK;                                                                                    \
     }                                                                                              \
     MH_PGLOAD();                                                                                   \
@@ -894,7 +949,16 @@ void launch(const void *A, const void *Bt, int M, int N, int K, long lda, long l
             long sc, const EpiArgs &ep, hipStream_t st) {
   const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   hipLaunchKernelGGL((gemm_pipe_kernel<DT, BM, BN, WGM, WGN, EK>), dim3(tiles, 1, batch), dim3(WGM * WGN * 64), 0, st,
-                     (const uint16_t *)A, (const uint16_t *)Bt, M, N, K, lda, ldb, sa, sb, sc, ep);
+                     (const uint16_t *)A, (const uint16_t *)Bt, M, N, K, lda, ldb, sa, sb, sc, ep, ConvArgs{});
+}
+
+// implicit-GEMM convolution on the register-staged kernel (x NHWC, w OHWI)
+template <int DT, int BM, int BN, int WGM, int WGN>
+void launch_conv(const void *x, const void *w, const ConvArgs &cv, int oC, const EpiArgs &ep, hipStream_t st) {
+  const int M = cv.B * cv.oH * cv.oW, K = cv.kH * cv.kW * cv.iC;
+  const int tiles = ((M + BM - 1) / BM) * ((oC + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm_pipe_kernel<DT, BM, BN, WGM, WGN, PK_GENERAL, true>), dim3(tiles), dim3(WGM * WGN * 64), 0,
+                     st, (const uint16_t *)x, (const uint16_t *)w, M, oC, K, 0L, long(K), 0L, 0L, 0L, ep, cv);
 }
 
 template <int DT, int BM, int BN, int WGM, int WGN, int S, int EK = PK_GENERAL>

@@ -1,0 +1,60 @@
+// Implicit-GEMM convolution on the register-staged pipelined kernel
+// (gemm_pipe.hpp, CONV): the conv2d of the reference's op layer
+// (src/core/ops/conv2d.cpp, CPU semantics src/backend/cpu_backend.hpp:768-796)
+// as M = B*oH*oW output pixels x N = oC x K = kH*kW*iC on an NHWC activation
+// with OHWI weights.  The epilogue is the general program: the bias added to
+// the fp32 accumulator and one rounding (conv), then the activation.
+#include <cstdlib>
+
+#include "gemm_pipe.hpp"
+
+namespace mh {
+
+namespace {
+
+// Block tile: the largest of 128x128, 128x64, 64x64 that still gives about
+// one tile per CU (the UNet's levels: 131072 x 64, 32768 x 128, 8192 x 256,
+// 2048 x 512 output pixels x channels).
+int conv_tile(int M, int N) {
+  auto tiles = [&](int bm, int bn) { return long((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  if (N > 64 && tiles(128, 128) >= 240) return 0;
+  if (tiles(128, 64) >= 240) return 1;
+  return 2;
+}
+
+template <int DT>
+hipError_t run(const void *x, const void *w, const ConvArgs &cv, int oC, const EpiArgs &ep, hipStream_t st) {
+  const int M = cv.B * cv.oH * cv.oW;
+  int tile = conv_tile(M, oC);
+  // tuning override, read per call: MUNET_HIP_CONV_TILE = 0 128x128, 1 128x64, 2 64x64
+  if (const char *e = std::getenv("MUNET_HIP_CONV_TILE")) {
+    const int t = std::atoi(e);
+    if (t >= 0 && t <= 2) tile = t;
+  }
+  switch (tile) {
+  case 0: launch_conv<DT, 128, 128, 2, 2>(x, w, cv, oC, ep, st); break;
+  case 1: launch_conv<DT, 128, 64, 2, 2>(x, w, cv, oC, ep, st); break;
+  default: launch_conv<DT, 64, 64, 2, 2>(x, w, cv, oC, ep, st); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemm_pipe_conv_ok(int dt, const void *x, const void *w, const ConvArgs &cv) {
+  const long xbytes = long(cv.B) * cv.iH * cv.iW * cv.ldx * 2;
+  return (dt == BF16 || dt == F16) && cv.B > 0 && cv.iC > 0 && cv.iC % 64 == 0 && cv.ldx % 8 == 0 &&
+         cv.ldx >= cv.iC && cv.kH > 0 && cv.kW > 0 && cv.kH * cv.kW <= 32 && cv.s > 0 && cv.oH > 0 && cv.oW > 0 &&
+         (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 && xbytes + 16 < 0x7fffffffL &&
+         long(cv.B) * cv.oH * cv.oW < 0x7fffffffL && long(cv.kH) * cv.kW * cv.iC < 0x7fffffffL;
+}
+
+hipError_t gemm_pipe_conv(int dt, const void *x, const void *w, const ConvArgs &cv, int oC, const EpiArgs &ep,
+                          hipStream_t st) {
+  if (oC <= 0 || long(cv.B) * cv.oH * cv.oW <= 0) return hipSuccess;
+  if (!gemm_pipe_conv_ok(dt, x, w, cv) || ep.stats_out || ep.ln_stats) return hipErrorInvalidValue;
+  if (long(oC - 1) * cv.kH * cv.kW * cv.iC + long(cv.kH) * cv.kW * cv.iC > 0xffffffffL) return hipErrorInvalidValue;
+  return dt == BF16 ? run<BF16>(x, w, cv, oC, ep, st) : run<F16>(x, w, cv, oC, ep, st);
+}
+
+}  // namespace mh

@@ -65,6 +65,44 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f) {
   return uint16_t(sign | v);
 }
 
+// The reference's fp16 rounding of a float, as a float (f16_to_f32 of
+// f32_to_f16), without branches:
+//  * normal half range [2^-14, 65520): adding 0x1000 and clearing the low 13
+//    bits of the float's bits is MuNet's half-ulp rounding of the mantissa to
+//    10 bits, the carry raising the exponent (the sign bit rides along);
+//  * half subnormals [2^-25, 2^-14): multiples of 2^-24, half away from zero:
+//    trunc(|x| 2^24 + 0.5) 2^-24 (exact: the sum only rounds below 2^-25);
+//    below 2^-25, zero;
+//  * 65520 and above: infinity; NaN: the quiet NaN MuNet's 0x7e00 decodes to.
+__device__ __forceinline__ float round_f16_ref(float x) { return f16_to_f32(f32_to_f16(x)); }
+__device__ __forceinline__ float round_f16_exact(float x) {
+  const uint32_t b = __float_as_uint(x), a = b & 0x7fffffffu, s = b & 0x80000000u;
+  const uint32_t rn = (b + 0x1000u) & 0xffffe000u;
+  const float z = __builtin_truncf(__builtin_fmaf(__uint_as_float(a), 16777216.0f, 0.5f)) * 5.9604644775390625e-8f;
+  const uint32_t rs = (a < 0x33000000u ? 0u : __float_as_uint(z)) | s;
+  const uint32_t ro = (a > 0x7f800000u ? 0x7fc00000u : 0x7f800000u) | s;
+  return __uint_as_float(a < 0x38800000u ? rs : a >= 0x477ff000u ? ro : rn);
+}
+// Four values at once: the 2-op normal-range rounding, and the full
+// branch-free rounding for all four only when some lane of the wave has a
+// value outside zero and the normal half range (rare in practice).
+__device__ __forceinline__ void round4_f16(float v[4]) {
+  bool slow = false;
+  float r[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t b = __float_as_uint(v[e]), a = b & 0x7fffffffu;
+    r[e] = __uint_as_float((b + 0x1000u) & 0xffffe000u);
+    slow |= a != 0u && a - 0x38800000u >= 0x477ff000u - 0x38800000u;
+  }
+  if (__builtin_amdgcn_ballot_w64(slow)) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = round_f16_exact(v[e]);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = r[e];
+}
+
 template <int DT> struct Store;
 template <> struct Store<F32> {
   typedef float T;
@@ -77,7 +115,7 @@ template <> struct Store<F16> {
   typedef uint16_t T;
   static __device__ __forceinline__ float load(const uint16_t *p, size_t i) { return f16_to_f32(p[i]); }
   static __device__ __forceinline__ uint16_t enc(float v) { return f32_to_f16(v); }
-  static __device__ __forceinline__ float round(float v) { return f16_to_f32(f32_to_f16(v)); }
+  static __device__ __forceinline__ float round(float v) { return round_f16_exact(v); }
   static __device__ __forceinline__ float dec(uint16_t v) { return f16_to_f32(v); }
 };
 template <> struct Store<BF16> {

@@ -116,6 +116,12 @@ hipError_t gemm_pipe(int dt, const void *A, const void *Bt, int M, int N, int K,
 // direct-to-LDS.  Operands already checked by gemm_pipe.
 hipError_t gemm_pipe_big(int dt, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch,
                          long sa, long sb, long sc, const EpiArgs &ep, int tile, hipStream_t st);
+// Implicit-GEMM convolution on the register-staged pipelined kernel
+// (gemm_pipe_conv.hip): 16-bit, NHWC x and OHWI w 16-byte aligned, iC % 64
+// == 0, ldx % 8 == 0, at most 32 taps, every byte offset of x below 2^31.
+bool gemm_pipe_conv_ok(int dt, const void *x, const void *w, const ConvArgs &cv);
+hipError_t gemm_pipe_conv(int dt, const void *x, const void *w, const ConvArgs &cv, int oC, const EpiArgs &ep,
+                          hipStream_t st);
 hipError_t conv_nhwc(int dt, const void *x, const void *w_ohwi, const ConvArgs &cv, int oC, const EpiArgs &ep,
                      int tile_hint, hipStream_t st);
 
@@ -158,6 +164,9 @@ hipError_t binary(int dt, int op, const void *a, const void *b, void *out, const
 hipError_t unary(int dt, int op, const void *in, void *out, size_t n, float c, hipStream_t st);
 hipError_t masked_fill(int dt, const void *x, const int32_t *mask, void *out, size_t n, float value, hipStream_t st);
 hipError_t convert(int sdt, const void *in, int ddt, void *out, size_t n, hipStream_t st);
+// the fast fp16 rounding against the full codec over all 2^32 float bit
+// patterns (synchronises st)
+hipError_t check_f16_rounding(unsigned long long *mismatches, hipStream_t st);
 // stats (optional): the LayerNorm statistics of each output row, one
 // (mean, M2) partial over all D columns (the stats_out layout of EpiArgs with
 // stats_cols = D).

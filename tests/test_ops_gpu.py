@@ -259,7 +259,10 @@ def test_argmax(hip, dt):
 @pytest.mark.parametrize("dt", DTS)
 @pytest.mark.parametrize("B,iC,H,W,oC,k,s,p", [(2, 3, 9, 9, 4, 3, 1, 1), (2, 3, 9, 9, 4, 3, 2, 1),
                                                (1, 16, 12, 10, 32, 3, 1, 1), (2, 8, 8, 8, 16, 1, 1, 0),
-                                               (1, 32, 16, 16, 16, 3, 2, 1)])
+                                               (1, 32, 16, 16, 16, 3, 2, 1),
+                                               # whole 64-channel slabs: the pipelined implicit GEMM (16-bit)
+                                               (2, 64, 12, 10, 32, 3, 1, 1), (1, 128, 9, 9, 64, 3, 2, 1),
+                                               (1, 64, 8, 8, 2, 1, 1, 0), (2, 192, 7, 5, 96, 3, 1, 1)])
 def test_conv2d(hip, orc, dt, B, iC, H, W, oC, k, s, p):
     x = rand((B, iC, H, W), dt, 100)
     w = rand((oC, iC, k, k), dt, 101, np.sqrt(2.0 / (iC * k * k)))
@@ -268,6 +271,37 @@ def test_conv2d(hip, orc, dt, B, iC, H, W, oC, k, s, p):
     out = empty(ref.shape, dt)
     hip.conv2d(to_device(x, dt), to_device(w, dt), to_device(b, dt), out, B, iC, H, W, oC, k, k, s, p)
     assert_close(to_host(out, dt), ref, dt, what="conv2d")
+
+
+@pytest.mark.parametrize("dt", [F16, BF16])
+@pytest.mark.parametrize("B,iC,H,W,oC,k,s,p,act", [(8, 64, 32, 32, 64, 3, 1, 1, 1), (2, 128, 16, 16, 256, 3, 2, 1, 1),
+                                                   (1, 512, 8, 8, 512, 3, 1, 1, 1), (4, 64, 20, 12, 128, 3, 1, 1, 0),
+                                                   (3, 256, 9, 7, 64, 3, 2, 1, 1), (2, 64, 16, 16, 2, 1, 1, 0, 0),
+                                                   (1, 64, 5, 6, 40, 5, 1, 2, 1)])
+def test_conv_pipelined_kernel_bits(hip, dt, B, iC, H, W, oC, k, s, p, act, monkeypatch):
+    """The pipelined implicit-GEMM convolution (iC % 64 == 0) gives the bits
+    of the general implicit-GEMM kernel (same MFMA sequence, bias added to the
+    fp32 accumulator, one rounding, ReLU) on NHWC inputs, over the block
+    tiles it picks (128x128, 128x64, 64x64), strides, 1x1 and 5x5 filters,
+    ragged pixel counts and padding on every side."""
+    x = rand((B, H, W, iC), dt, 120)
+    w = rand((oC, iC, k, k), dt, 121, np.sqrt(2.0 / (iC * k * k)))
+    b = rand((oC,), dt, 122, 0.1)
+    oh, ow = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+    wo = empty((oC, k, k, iC), dt)
+    hip.pack_conv_weight(to_device(w, dt), wo, oC, iC, k, k)
+    xd, bd = to_device(x, dt), to_device(b, dt)
+    outs = {}
+    for name in ("pipelined", "general"):
+        monkeypatch.delenv("MUNET_HIP_CONV_KERNEL", raising=False)
+        if name == "general":
+            monkeypatch.setenv("MUNET_HIP_CONV_KERNEL", "general")
+        out = empty((B, oh, ow, oC), dt)
+        hip.conv2d_nhwc(xd, wo, bd, out, B, iC, H, W, oC, k, k, s, p, act)
+        hip.synchronize()
+        outs[name] = to_host(out, dt)
+    assert np.all(np.isfinite(dec(outs["pipelined"], dt)))
+    assert np.array_equal(outs["pipelined"], outs["general"]), "pipelined conv differs from the general kernel"
 
 
 def test_conv2d_closed_form(hip):
@@ -342,6 +376,14 @@ def test_to_contiguous(hip, dt):
     flat = x.reshape(-1)
     ref = np.array([[flat[7 + 30 * i + 6 * j] for j in range(5)] for i in range(3)])
     assert np.array_equal(to_host(out2, dt), ref)
+
+
+def test_fast_f16_rounding_is_exhaustively_exact(hip):
+    """The kernels' fast fp16 rounding (a bit trick for zero and the normal
+    half range, the codec for the rest) equals the full codec, which
+    test_convert_codecs pins to the reference, on all 2^32 float bit
+    patterns: ties, half subnormals, overflow to infinity, NaN, signed zero."""
+    assert hip.check_f16_rounding() == 0
 
 
 def test_convert_codecs(hip, orc):
