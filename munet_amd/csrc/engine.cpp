@@ -251,14 +251,17 @@ struct EngineImpl {
     return t;
   }
   // Conv weight OIHW -> OHWI.
-  std::vector<uint8_t> pack_conv(const Param &p, int oC, int iC, int k) const {
+  // Conv weight [oC, iC, k, k] -> OHWI [oC, k, k, iCp], channels iC .. iCp-1
+  // zero (iCp = iC unless the input layout is channel-padded).
+  std::vector<uint8_t> pack_conv(const Param &p, int oC, int iC, int k, int iCp = 0) const {
     const size_t es = dt_size(dt);
+    if (iCp < iC) iCp = iC;
     if (p.host.size() != size_t(oC) * iC * k * k * es) throw Error("conv weight has the wrong size");
-    std::vector<uint8_t> t(p.host.size());
+    std::vector<uint8_t> t(size_t(oC) * k * k * iCp * es, 0);
     for (int o = 0; o < oC; ++o)
       for (int c = 0; c < iC; ++c)
         for (int q = 0; q < k * k; ++q)
-          std::memcpy(&t[((size_t(o) * k * k + q) * iC + c) * es], &p.host[((size_t(o) * iC + c) * k * k + q) * es], es);
+          std::memcpy(&t[((size_t(o) * k * k + q) * iCp + c) * es], &p.host[((size_t(o) * iC + c) * k * k + q) * es], es);
     return t;
   }
   // ConvTranspose weight [iC, oC, k, k] -> [k, k, oC, iC].
@@ -286,13 +289,17 @@ struct EngineImpl {
     o.a[0] = s[0]; o.a[1] = s[1]; o.a[2] = s[2] * s[3];
     return y;
   }
-  int to_nhwc(int x, const std::string &name) {
+  // pad_to > C: the NHWC copy has pad_to channels, the extra ones zero (its
+  // shape keeps the padded channel count; only a convolution reads it)
+  int to_nhwc(int x, const std::string &name, int pad_to = 0) {
     if (vals[x].layout == NHWC) return x;
-    const Shape s = vals[x].shape;
+    Shape s = vals[x].shape;
     if (s.size() != 4) throw Error(name + ": expected a 4-D [B,C,H,W] input");
+    const long C = s[1];
+    if (pad_to > C) s[1] = pad_to;
     int y = new_val(s, vals[x].dt, NHWC);
     Op &o = emit(OP_TO_NHWC, name + ".to_nhwc", {x}, {y});
-    o.a[0] = s[0]; o.a[1] = s[1]; o.a[2] = s[2] * s[3];
+    o.a[0] = s[0]; o.a[1] = C; o.a[2] = s[2] * s[3]; o.a[3] = s[1];
     return y;
   }
 
@@ -410,14 +417,26 @@ struct EngineImpl {
   }
 
   int conv(int x, const std::string &pfx, int iC, int oC, int k, int s, int p, int act, int out_view = -1) {
-    x = to_nhwc(x, pfx);
+    // an NCHW input with a channel count that is not a whole 16-byte chunk
+    // (the image's 3 channels) converts to NHWC padded with zero channels, so
+    // the convolution takes the vectorised im2col loader
+    const int chunk = dt == F32 ? 4 : 8, padded = (iC + chunk - 1) / chunk * chunk;
+    int iCp = iC;
+    if (vals[x].layout == NHWC) {
+      iCp = int(vals[x].shape[1]);  // an NHWC input may already carry the padding
+      if (iCp != iC && iCp != padded) throw Error(pfx + ": channel mismatch");
+    } else {
+      if (vals[x].shape.size() == 4 && vals[x].shape[1] != iC) throw Error(pfx + ": channel mismatch");
+      iCp = padded;
+      x = to_nhwc(x, pfx, iCp);
+    }
     const Shape xs = vals[x].shape;
-    if (xs[1] != iC) throw Error(pfx + ": channel mismatch");
     const int oH = (xs[2] + 2 * p - k) / s + 1, oW = (xs[3] + 2 * p - k) / s + 1;
     const int y = out_view >= 0 ? out_view : new_val({xs[0], oC, oH, oW}, dt, NHWC);
     Op &o = emit(OP_CONV, pfx.substr(0, pfx.size() - 1), {x}, {y});
-    o.a[0] = xs[0]; o.a[1] = iC; o.a[2] = xs[2]; o.a[3] = xs[3]; o.a[4] = oC; o.a[5] = k; o.a[6] = s; o.a[7] = p;
-    o.w = upload(pack_conv(param(pfx + "weight"), oC, iC, k));
+    o.a[0] = xs[0]; o.a[1] = iCp; o.a[2] = xs[2]; o.a[3] = xs[3]; o.a[4] = oC; o.a[5] = k; o.a[6] = s; o.a[7] = p;
+    o.a[8] = iC;  // the model's channels (the algorithmic work)
+    o.w = upload(pack_conv(param(pfx + "weight"), oC, iC, k, iCp));
     o.b = bias_or_zero(pfx + "bias", oC);
     o.act = act;
     if (act != ACT_NONE) ++fused_epilogues;
@@ -603,7 +622,8 @@ struct EngineImpl {
     for (const auto &c : m.at("channels").arr) ch.push_back(c.as_int());
     const int L = int(ch.size());
     int prev = m.at("in_channels").as_int();
-    x = to_nhwc(x, pfx + "input");
+    const int chunk = dt == F32 ? 4 : 8;
+    x = to_nhwc(x, pfx + "input", (prev + chunk - 1) / chunk * chunk);
     std::vector<int> cat(L, -1);
     for (int l = 0; l < L; ++l) {
       const int c = ch[l];
@@ -809,8 +829,14 @@ struct EngineImpl {
       hip_check(softmax_rows(dt, dptr(o.in[0]), dptr(o.out[0]), int(o.a[0]), int(o.a[1]), st), o.name.c_str());
       break;
     case OP_TO_NHWC:
-      hip_check(nchw_to_nhwc(vals[o.in[0]].dt, dptr(o.in[0]), dptr(o.out[0]), int(o.a[0]), int(o.a[1]), int(o.a[2]), st),
-                o.name.c_str());
+      if (o.a[3] > o.a[1])
+        hip_check(nchw_to_nhwc_pad(vals[o.in[0]].dt, dptr(o.in[0]), dptr(o.out[0]), int(o.a[0]), int(o.a[1]),
+                                   int(o.a[2]), int(o.a[3]), st),
+                  o.name.c_str());
+      else
+        hip_check(nchw_to_nhwc(vals[o.in[0]].dt, dptr(o.in[0]), dptr(o.out[0]), int(o.a[0]), int(o.a[1]),
+                               int(o.a[2]), st),
+                  o.name.c_str());
       break;
     case OP_TO_NCHW:
       hip_check(nhwc_to_nchw(vals[o.in[0]].dt, dptr(o.in[0]), dptr(o.out[0]), int(o.a[0]), int(o.a[1]), int(o.a[2]), st),
@@ -923,7 +949,7 @@ struct EngineImpl {
     case OP_CONV: {  // 2 (B oH oW) oC (k k iC)
       const double oH = double((o.a[2] + 2 * o.a[7] - o.a[5]) / o.a[6] + 1),
                    oW = double((o.a[3] + 2 * o.a[7] - o.a[5]) / o.a[6] + 1);
-      flops = 2.0 * o.a[0] * oH * oW * o.a[4] * double(o.a[5]) * o.a[5] * o.a[1];
+      flops = 2.0 * o.a[0] * oH * oW * o.a[4] * double(o.a[5]) * o.a[5] * o.a[8];
       break;
     }
     case OP_CONVT: flops = 2.0 * o.a[0] * o.a[2] * o.a[3] * double(o.a[5]) * o.a[5] * o.a[4] * o.a[1]; break;

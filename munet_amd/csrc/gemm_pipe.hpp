@@ -204,12 +204,14 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
 
   __device__ __forceinline__ PipeEpi(const EpiArgs &ep, const G &g_, int M_, int N_, int m0_, int n0_)
       : g(g_), M(M_), N(N_), m0(m0_), n0(n0_),
-        fast(KT_::FIXED || ((DT == BF16 || DT == F16) && ep.mode != EPI_CONVT && N_ % 4 == 0 &&
-                            (!ep.resid || (ep.ldr & 3) == 0))) {}
+        fast(KT_::FIXED || ((DT == BF16 || DT == F16) && N_ % 4 == 0 && (!ep.resid || (ep.ldr & 3) == 0) &&
+                            (ep.mode != EPI_CONVT || (ep.convt_oc % 4 == 0 && !ep.resid)))) {}
 
   __device__ __forceinline__ uint2 bload(const EpiArgs &ep, int j) const {
     const uint16_t *bias = static_cast<const uint16_t *>(ep.bias);
-    return *reinterpret_cast<const uint2 *>(bias + min(n0 + g.wn * WTN + j * 16 + g.lg * 4, N - 4));
+    int n = min(n0 + g.wn * WTN + j * 16 + g.lg * 4, N - 4);
+    if (!KT_::FIXED && ep.mode == EPI_CONVT) n %= ep.convt_oc;  // column (tap, oc): the bias of oc
+    return *reinterpret_cast<const uint2 *>(bias + n);
   }
   __device__ __forceinline__ uint2 rload(const EpiArgs &ep, int i, int j) const {
     const uint16_t *resid = static_cast<const uint16_t *>(ep.resid);
@@ -491,6 +493,24 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
       }
       al8 = (ep.hd & 3) == 0 && ((uintptr_t)ep.outs[0] & 7) == 0 && ((uintptr_t)ep.outs[1] & 7) == 0 &&
             ((uintptr_t)ep.outs[2] & 7) == 0;
+    } else if (!KT_::FIXED && ep.mode == EPI_CONVT) {
+      // transposed convolution: row m = input pixel (b, ih, iw), column n =
+      // (kh k + kw) oC + oc lands on output pixel (b, ih k + kh, iw k + kw),
+      // channel oc; the output offset splits into a row part and a column part
+      const int k = ep.convt_k, oW = ep.convt_iw * k;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = min(n0 + wn * WTN + j * 16 + lg * 4, N - 4);
+        const int oc = n % ep.convt_oc, ph = n / ep.convt_oc, kh = ph / k, kw = ph - kh * k;
+        cbase[j] = static_cast<uint16_t *>(ep.out) + (long(kh) * oW + kw) * ep.ldc + oc;
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int m = min(m0 + wm * WTM + i * 16 + li, M - 1);
+        const int iw = m % ep.convt_iw, rest = m / ep.convt_iw, ih = rest % ep.convt_ih, b = rest / ep.convt_ih;
+        roff[i] = ((long(b) * ep.convt_ih + ih) * k * oW + long(iw) * k) * ep.ldc;
+      }
+      al8 = ((uintptr_t)ep.out & 7) == 0 && (ep.ldc & 3) == 0;
     } else {
 #pragma unroll
       for (int j = 0; j < FN; ++j) cbase[j] = static_cast<uint16_t *>(ep.out) + off + n0 + wn * WTN + j * 16 + lg * 4;

@@ -217,6 +217,33 @@ hipError_t upsample2d(int dt, int nhwc, const void *in, void *out, int B, int C,
   return hipGetLastError();
 }
 
+// NCHW [B, C, HW] -> NHWC [B, HW, Cp] with channels C .. Cp-1 zero (the
+// padded layout lets an implicit-GEMM convolution over few input channels
+// take whole 16-byte chunks per pixel).
+template <typename T>
+__global__ void __launch_bounds__(256) nchw_to_nhwc_pad_kernel(const T *__restrict__ in, T *__restrict__ out, int C,
+                                                               int HW, int Cp, size_t total) {
+  for (size_t i = blockIdx.x * size_t(256) + threadIdx.x; i < total; i += size_t(gridDim.x) * 256) {
+    const int c = int(i % Cp);
+    const size_t pix = i / Cp, b = pix / HW, hw = pix - b * HW;
+    out[i] = c < C ? in[(b * C + c) * HW + hw] : T(0);
+  }
+}
+
+hipError_t nchw_to_nhwc_pad(int dt, const void *in, void *out, int B, int C, int HW, int Cp, hipStream_t st) {
+  if (Cp < C) return hipErrorInvalidValue;
+  const size_t total = size_t(B) * HW * Cp;
+  if (total == 0) return hipSuccess;
+  const int blocks = grid_for(total, 256);
+  if (dtype_size(dt) == 2)
+    hipLaunchKernelGGL(nchw_to_nhwc_pad_kernel<uint16_t>, dim3(blocks), dim3(256), 0, st, (const uint16_t *)in,
+                       (uint16_t *)out, C, HW, Cp, total);
+  else
+    hipLaunchKernelGGL(nchw_to_nhwc_pad_kernel<uint32_t>, dim3(blocks), dim3(256), 0, st, (const uint32_t *)in,
+                       (uint32_t *)out, C, HW, Cp, total);
+  return hipGetLastError();
+}
+
 // NCHW [B, C, HW] <-> NHWC [B, HW, C] is a batched 2-D transpose.
 hipError_t nchw_to_nhwc(int dt, const void *in, void *out, int B, int C, int HW, hipStream_t st) {
   return transpose2d(dt, in, out, B, C, HW, st);

@@ -191,6 +191,8 @@ hipError_t max_pool2d(int dt, int nhwc, const void *in, void *out, int B, int C,
 hipError_t upsample2d(int dt, int nhwc, const void *in, void *out, int B, int C, int iH, int iW, int scale,
                       hipStream_t st);
 hipError_t nchw_to_nhwc(int dt, const void *in, void *out, int B, int C, int HW, hipStream_t st);
+// NCHW [B, C, HW] -> NHWC [B, HW, Cp], channels C .. Cp-1 written as zero
+hipError_t nchw_to_nhwc_pad(int dt, const void *in, void *out, int B, int C, int HW, int Cp, hipStream_t st);
 hipError_t nhwc_to_nchw(int dt, const void *in, void *out, int B, int C, int HW, hipStream_t st);
 
 inline size_t dt_size(int dt) { return (dt == 1 || dt == 2) ? 2 : 4; }

@@ -334,6 +334,31 @@ def test_conv_transpose2d(hip, orc, dt):
     assert_close(to_host(out, dt), ref, dt, what="conv_transpose2d")
 
 
+@pytest.mark.parametrize("dt", [F16, BF16])
+@pytest.mark.parametrize("B,iC,H,W,oC", [(8, 128, 32, 32, 64), (2, 512, 8, 8, 256), (3, 64, 5, 7, 12)])
+def test_conv_transpose_pipelined_epilogue_bits(hip, dt, B, iC, H, W, oC, monkeypatch):
+    """The pipelined kernel's register epilogue for the transposed-conv
+    scatter (row and column parts of the output offset, bias of column
+    n mod oC) gives the bits of the general kernel's staged store, including
+    a ragged tile and 12 output channels."""
+    x = rand((B, H, W, iC), dt, 130)
+    w = rand((iC, oC, 2, 2), dt, 131, 0.3)
+    b = rand((oC,), dt, 132, 0.1)
+    wp = empty((4 * oC, iC), dt)
+    hip.pack_convt_weight(to_device(w, dt), wp, iC, oC, 2)
+    xd, bd = to_device(x, dt), to_device(b, dt)
+    outs = {}
+    for name in ("pipelined", "general"):
+        monkeypatch.delenv("MUNET_HIP_GEMM_TILE", raising=False)
+        if name == "general":
+            monkeypatch.setenv("MUNET_HIP_GEMM_TILE", "104")
+        on = empty((B, 2 * H, 2 * W, oC), dt)
+        hip.conv_transpose2d_nhwc(xd, wp, bd, on, B, iC, H, W, oC, 2)
+        hip.synchronize()
+        outs[name] = to_host(on, dt)
+    assert np.array_equal(outs["pipelined"], outs["general"]), "pipelined transposed conv differs from the general kernel"
+
+
 @pytest.mark.parametrize("dt", DTS)
 def test_pool_upsample_concat(hip, orc, dt):
     B, C, H, W = 2, 3, 8, 6
