@@ -98,6 +98,8 @@ struct Op {
   int stats_out = -1, stats_cols = 16, ln_stats = -1, ln_parts = 0, ln_cols = 16;
   const void *ln_cs = nullptr, *ln_bw = nullptr;
   float ln_eps = 0.f;
+  // split-K GEMM: fp32 workspace value [splits, M, N] (live for this op only)
+  int ws = -1, splits = 1;
 };
 
 // A LayerNorm folded into the Linear that consumes it (stats: the value that
@@ -413,6 +415,11 @@ struct EngineImpl {
       o.in.push_back(resid);
     }
     if (act != ACT_NONE || resid >= 0) ++fused_epilogues;
+    const int S = ln ? 1 : splitk_count(dt, int(o.a[0]), out_f, in_f);
+    if (S > 1) {
+      o.ws = new_val({S, int(o.a[0]), out_f}, F32);
+      o.splits = S;
+    }
     return y;
   }
 
@@ -673,6 +680,7 @@ struct EngineImpl {
     for (int i = 0; i < int(ops.size()); ++i) {
       for (int v : ops[i].out) touch(v, i);
       for (int v : ops[i].in) touch(v, i);
+      if (ops[i].ws >= 0) touch(ops[i].ws, i);
     }
     touch(input, int(ops.size()));
     touch(output, int(ops.size()));
@@ -740,9 +748,14 @@ struct EngineImpl {
       }
       set_fold(o, ep);
       ep.stream_out = o.out[0] == output && stream_out;
-      hip_check(gemm_nt(dt, dptr(o.in[0]), wptr(o.w), int(o.a[0]), int(o.a[1]), int(o.a[2]), o.a[2], o.a[2], 1, 0,
-                        0, 0, ep, -1, st),
-                o.name.c_str());
+      if (o.splits > 1)
+        hip_check(gemm_splitk(dt, dptr(o.in[0]), wptr(o.w), int(o.a[0]), int(o.a[1]), int(o.a[2]), o.splits,
+                              static_cast<float *>(dptr(o.ws)), ep, st),
+                  o.name.c_str());
+      else
+        hip_check(gemm_nt(dt, dptr(o.in[0]), wptr(o.w), int(o.a[0]), int(o.a[1]), int(o.a[2]), o.a[2], o.a[2], 1, 0,
+                          0, 0, ep, -1, st),
+                  o.name.c_str());
       break;
     }
     case OP_QKV: {

@@ -390,6 +390,68 @@ hipError_t gemm_nt(int dt, const void *A, const void *Bt, int M, int N, int K, l
   }
 }
 
+// ---- split-K for small fp32 products --------------------------------------
+// A product with few output tiles and a long K (the CNN's 32 x 4096 x 128
+// Linear: two 64x64 tiles, 128 K steps each) leaves most CUs idle.  Split-K
+// runs S <= 64 slices of K as a batch of partial products into an fp32
+// workspace [S, M, N], then one kernel sums the slices in a fixed tree order
+// (deterministic) and applies the epilogue chain.
+int splitk_count(int dt, int M, int N, int K) {
+  if (dt != F32 || M <= 0 || N <= 0 || K < 512) return 1;
+  const long tiles = long((M + 63) / 64) * ((N + 63) / 64);
+  if (tiles >= 32) return 1;
+  int best = 1;
+  for (int S = 2; S <= 64; ++S) {
+    if (tiles * S > 256) break;
+    if (K % S || (K / S) % 4 || K / S < 64) continue;
+    best = S;
+  }
+  return best;
+}
+
+namespace {
+// One wave per output quad (m, n .. n+3): lane s loads slice s's partial quad
+// (all slices in flight at once), a fixed xor-tree sums them, lane 0 applies
+// the epilogue.
+template <int DT>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const float *__restrict__ ws, int S, int M, int N,
+                                                             EpiArgs ep) {
+  const int n4 = (N + 3) / 4, lane = threadIdx.x & 63;
+  const long item = long(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (item >= long(M) * n4) return;
+  const int m = int(item / n4), n = int(item - long(m) * n4) * 4;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (lane < S) {
+    const float *p = ws + long(lane) * M * N + long(m) * N + n;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (n + e < N) v[e] = p[e];
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] += __shfl_xor(v[e], o, 64);
+  if (lane == 0) epi_store4<DT>(ep, m, n, N, v, 0);
+}
+}  // namespace
+
+hipError_t gemm_splitk(int dt, const void *A, const void *Bt, int M, int N, int K, int S, float *ws, const EpiArgs &ep,
+                       hipStream_t st) {
+  if (M <= 0 || N <= 0) return hipSuccess;
+  if (dt != F32 || S < 1 || S > 64 || K % S || (K / S) % 4 || !ws || ep.mode != EPI_ROWMAJOR || ep.stats_out ||
+      ep.ln_stats)
+    return hipErrorInvalidValue;
+  const int Kc = K / S;
+  EpiArgs part;  // raw fp32 partial products, slice s at ws + s M N
+  part.out = ws;
+  part.ldc = N;
+  hipError_t e = launch_dt<F32>(A, Bt, M, N, Kc, K, K, S, Kc, Kc, long(M) * N, part, nullptr, -1, st);
+  if (e != hipSuccess) return e;
+  const long items = long(M) * ((N + 3) / 4);
+  hipLaunchKernelGGL(splitk_reduce_kernel<F32>, dim3(unsigned((items + 3) / 4)), dim3(256), 0, st, ws, S, M, N, ep);
+  return hipGetLastError();
+}
+
 // Implicit-GEMM convolution on an NHWC activation with OHWI-packed weights:
 // M = B*oH*oW output pixels, N = oC, K = kH*kW*iC.  Output row m, column oc.
 hipError_t conv_nhwc(int dt, const void *x, const void *w_ohwi, const ConvArgs &cv, int oC, const EpiArgs &ep,

@@ -124,6 +124,12 @@ hipError_t gemm_pipe_conv(int dt, const void *x, const void *w, const ConvArgs &
                           hipStream_t st);
 hipError_t conv_nhwc(int dt, const void *x, const void *w_ohwi, const ConvArgs &cv, int oC, const EpiArgs &ep,
                      int tile_hint, hipStream_t st);
+// Split-K for small fp32 products (gemm.hip): the slice count for M x N x K
+// (1: no split), and the product itself through an fp32 workspace of
+// S * M * N floats (row-major epilogue only).
+int splitk_count(int dt, int M, int N, int K);
+hipError_t gemm_splitk(int dt, const void *A, const void *Bt, int M, int N, int K, int S, float *ws, const EpiArgs &ep,
+                       hipStream_t st);
 
 // Fused attention core (q, k, v in the head-split [B*H, T, hd] layout).
 // textbook = 0: MuNet's scores, k's buffer read as a [hd, B*H*T] matrix;
