@@ -452,6 +452,41 @@ hipError_t gemm_splitk(int dt, const void *A, const void *Bt, int M, int N, int 
   return hipGetLastError();
 }
 
+// ---- 1x1 convolution to a few output channels -------------------------------
+// A 1x1 convolution to oC <= 8 channels (the UNet's output head: 64 -> 2) is
+// a dot product per pixel: a matrix-core tile would waste all but oC of its
+// columns.  One thread per output pixel reads its iC channels in 16-byte
+// chunks, the weights sit in LDS as floats (every lane reads the same
+// address), fp32 sums in channel order, then the epilogue chain.
+namespace {
+template <int DT>
+__global__ void __launch_bounds__(256) conv1x1_smalln_kernel(const uint16_t *__restrict__ x,
+                                                              const uint16_t *__restrict__ w, int M, int iC, long ldx,
+                                                              int oC, EpiArgs ep) {
+  __shared__ float wl[8 * 512];
+  for (int i = threadIdx.x; i < oC * iC; i += 256) wl[i] = Store<DT>::dec(w[i]);
+  __syncthreads();
+  const int m = blockIdx.x * 256 + threadIdx.x;
+  if (m >= M) return;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const uint16_t *row = x + long(m) * ldx;
+  for (int c0 = 0; c0 < iC; c0 += 8) {
+    const uint4 q = *reinterpret_cast<const uint4 *>(row + c0);
+    const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float xv = Store<DT>::dec(uint16_t(wd[e >> 1] >> (16 * (e & 1))));
+#pragma unroll
+      for (int o = 0; o < 8; ++o)
+        if (o < oC) acc[o] = __fmaf_rn(xv, wl[o * iC + c0 + e], acc[o]);
+    }
+  }
+  float lo[4] = {acc[0], acc[1], acc[2], acc[3]}, hi[4] = {acc[4], acc[5], acc[6], acc[7]};
+  epi_store4<DT>(ep, m, 0, oC, lo, 0);
+  if (oC > 4) epi_store4<DT>(ep, m, 4, oC, hi, 0);
+}
+}  // namespace
+
 // Implicit-GEMM convolution on an NHWC activation with OHWI-packed weights:
 // M = B*oH*oW output pixels, N = oC, K = kH*kW*iC.  Output row m, column oc.
 hipError_t conv_nhwc(int dt, const void *x, const void *w_ohwi, const ConvArgs &cv, int oC, const EpiArgs &ep,
@@ -461,7 +496,19 @@ hipError_t conv_nhwc(int dt, const void *x, const void *w_ohwi, const ConvArgs &
   // 16-bit convolutions with whole 64-channel slabs run on the pipelined
   // kernel; MUNET_HIP_CONV_KERNEL=general (read per call) keeps this one
   const char *ck = std::getenv("MUNET_HIP_CONV_KERNEL");
-  if (tile_hint < 0 && !(ck && std::string(ck) == "general") && gemm_pipe_conv_ok(dt, x, w_ohwi, cv))
+  const bool general = ck && std::string(ck) == "general";
+  if (tile_hint < 0 && !general && (dt == F16 || dt == BF16) && cv.kH == 1 && cv.kW == 1 && cv.s == 1 && cv.p == 0 &&
+      oC <= 8 && cv.iC % 8 == 0 && cv.iC <= 512 && cv.ldx % 8 == 0 && (uintptr_t)x % 16 == 0 &&
+      ep.mode == EPI_ROWMAJOR && !ep.resid) {
+    if (dt == F16)
+      hipLaunchKernelGGL(conv1x1_smalln_kernel<F16>, dim3((M + 255) / 256), dim3(256), 0, st, (const uint16_t *)x,
+                         (const uint16_t *)w_ohwi, M, cv.iC, cv.ldx, oC, ep);
+    else
+      hipLaunchKernelGGL(conv1x1_smalln_kernel<BF16>, dim3((M + 255) / 256), dim3(256), 0, st, (const uint16_t *)x,
+                         (const uint16_t *)w_ohwi, M, cv.iC, cv.ldx, oC, ep);
+    return hipGetLastError();
+  }
+  if (tile_hint < 0 && !general && gemm_pipe_conv_ok(dt, x, w_ohwi, cv))
     return gemm_pipe_conv(dt, x, w_ohwi, cv, oC, ep, st);
   switch (dt) {
   case F32: return launch_dt<F32>(x, w_ohwi, M, oC, K, 0, K, 1, 0, 0, 0, ep, &cv, tile_hint, st);

@@ -262,7 +262,9 @@ def test_argmax(hip, dt):
                                                (1, 32, 16, 16, 16, 3, 2, 1),
                                                # whole 64-channel slabs: the pipelined implicit GEMM (16-bit)
                                                (2, 64, 12, 10, 32, 3, 1, 1), (1, 128, 9, 9, 64, 3, 2, 1),
-                                               (1, 64, 8, 8, 2, 1, 1, 0), (2, 192, 7, 5, 96, 3, 1, 1)])
+                                               (1, 64, 8, 8, 2, 1, 1, 0), (2, 192, 7, 5, 96, 3, 1, 1),
+                                               # 1x1 to few channels: the per-pixel dot-product kernel
+                                               (3, 128, 10, 9, 6, 1, 1, 0), (1, 512, 4, 4, 1, 1, 1, 0)])
 def test_conv2d(hip, orc, dt, B, iC, H, W, oC, k, s, p):
     x = rand((B, iC, H, W), dt, 100)
     w = rand((oC, iC, k, k), dt, 101, np.sqrt(2.0 / (iC * k * k)))
@@ -276,13 +278,13 @@ def test_conv2d(hip, orc, dt, B, iC, H, W, oC, k, s, p):
 @pytest.mark.parametrize("dt", [F16, BF16])
 @pytest.mark.parametrize("B,iC,H,W,oC,k,s,p,act", [(8, 64, 32, 32, 64, 3, 1, 1, 1), (2, 128, 16, 16, 256, 3, 2, 1, 1),
                                                    (1, 512, 8, 8, 512, 3, 1, 1, 1), (4, 64, 20, 12, 128, 3, 1, 1, 0),
-                                                   (3, 256, 9, 7, 64, 3, 2, 1, 1), (2, 64, 16, 16, 2, 1, 1, 0, 0),
+                                                   (3, 256, 9, 7, 64, 3, 2, 1, 1), (2, 64, 16, 16, 16, 1, 1, 0, 0),
                                                    (1, 64, 5, 6, 40, 5, 1, 2, 1)])
 def test_conv_pipelined_kernel_bits(hip, dt, B, iC, H, W, oC, k, s, p, act, monkeypatch):
     """The pipelined implicit-GEMM convolution (iC % 64 == 0) gives the bits
     of the general implicit-GEMM kernel (same MFMA sequence, bias added to the
     fp32 accumulator, one rounding, ReLU) on NHWC inputs, over the block
-    tiles it picks (128x128, 128x64, 64x64), strides, 1x1 and 5x5 filters,
+    tile it picks (64x64), strides, 1x1 and 5x5 filters,
     ragged pixel counts and padding on every side."""
     x = rand((B, H, W, iC), dt, 120)
     w = rand((oC, iC, k, k), dt, 121, np.sqrt(2.0 / (iC * k * k)))
