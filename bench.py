@@ -349,6 +349,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip BASELINE configs 0-3")
     ap.add_argument("--probe", default=None, help="run one kernel of the forward for rocprofv3 --pmc and exit")
+    ap.add_argument("--config", default=None,
+                    help="measure only this BASELINE config (mlp, cnn, encoder_bf16, encoder_fp16, unet, decode), "
+                         "print its JSON row and exit (for profiling one config)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -362,6 +365,18 @@ def main():
     from munet_amd import _lib, models
     from munet_amd.backend import HipBackend
     from munet_amd.engine import Engine
+
+    if args.config:
+        keys = {k: (i, c) for k, i, c in CONFIG_ROWS}
+        if args.config == "decode":
+            row = decode_line()
+        elif args.config in keys:
+            idx, cpu_batch = keys[args.config]
+            row = config_line(torch, args.config, idx, cpu_batch, args.steps, args.warmup, not args.no_cpu_baseline)
+        else:
+            sys.exit(f"bench: unknown config {args.config!r} (one of {sorted(keys) + ['decode']})")
+        print(json.dumps({"config": args.config, **row}), flush=True)
+        return
 
     cfg = models.decoder_config(**CFG)
     log("bench: initialising weights")
