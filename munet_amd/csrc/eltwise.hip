@@ -60,6 +60,54 @@ __global__ void binary_contig_kernel(const typename Store<DT>::T *__restrict__ a
   }
 }
 
+// 16-byte chunks: 8 values of a 16-bit type, 4 of fp32, decoded to floats
+// and encoded back with the reference codecs.
+template <int DT> struct Vec16 {
+  typedef typename Store<DT>::T T;
+  static constexpr int E = 16 / int(sizeof(T));
+  static __device__ __forceinline__ void dec(uint4 q, float v[E]) {
+    if constexpr (DT == F32) {
+      v[0] = __uint_as_float(q.x); v[1] = __uint_as_float(q.y); v[2] = __uint_as_float(q.z); v[3] = __uint_as_float(q.w);
+    } else {
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = Store<DT>::dec(uint16_t(w[i] & 0xffffu));
+        v[2 * i + 1] = Store<DT>::dec(uint16_t(w[i] >> 16));
+      }
+    }
+  }
+  static __device__ __forceinline__ uint4 enc(const float v[E]) {
+    if constexpr (DT == F32) {
+      return make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
+    } else {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = uint32_t(Store<DT>::enc(v[2 * i])) | (uint32_t(Store<DT>::enc(v[2 * i + 1])) << 16);
+      return make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+};
+
+// Contiguous same-shape operands, whole 16-byte chunks (the host checks the
+// alignment and n % E == 0): one chunk per thread per step, the op fixed at
+// compile time.
+template <int DT, int OP>
+__global__ void __launch_bounds__(256) binary_vec_kernel(const uint4 *__restrict__ a, const uint4 *__restrict__ b,
+                                                          uint4 *__restrict__ o, size_t chunks) {
+  typedef Vec16<DT> V;
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < chunks; i += stride) {
+    float x[V::E], y[V::E];
+    V::dec(a[i], x);
+    V::dec(b[i], y);
+#pragma unroll
+    for (int e = 0; e < V::E; ++e) x[e] = binop(OP, x[e], y[e]);
+    o[i] = V::enc(x);
+  }
+}
+
 template <int DT>
 __global__ void binary_bcast_kernel(const typename Store<DT>::T *__restrict__ a,
                                     const typename Store<DT>::T *__restrict__ b, typename Store<DT>::T *__restrict__ o,
@@ -116,6 +164,35 @@ __global__ void unary_kernel(const typename Store<DT>::T *__restrict__ in, typen
     default: y = cosf(x); break;
     }
     out[i] = S::enc(y);
+  }
+}
+
+template <int DT, int OP>
+__device__ __forceinline__ float unop(float x, float c) {
+  typedef Store<DT> S;
+  if constexpr (OP == UN_RELU) return x > 0.0f ? x : 0.0f;
+  else if constexpr (OP == UN_SIGMOID) return sigmoidf_ref(x);
+  else if constexpr (OP == UN_GELU) return x * S::round(sigmoidf_ref(S::round(x * c)));
+  else if constexpr (OP == UN_EXP) return __expf(x);
+  else if constexpr (OP == UN_LOG) return __logf(x);
+  else if constexpr (OP == UN_SQRT) return sqrtf(x);
+  else if constexpr (OP == UN_RSQRT) return rsqrtf(x);
+  else if constexpr (OP == UN_SIN) return sinf(x);
+  else return cosf(x);
+}
+
+// unary_kernel on whole 16-byte chunks, the op fixed at compile time
+template <int DT, int OP>
+__global__ void __launch_bounds__(256) unary_vec_kernel(const uint4 *__restrict__ in, uint4 *__restrict__ out,
+                                                         size_t chunks, float c) {
+  typedef Vec16<DT> V;
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < chunks; i += stride) {
+    float x[V::E];
+    V::dec(in[i], x);
+#pragma unroll
+    for (int e = 0; e < V::E; ++e) x[e] = unop<DT, OP>(x[e], c);
+    out[i] = V::enc(x);
   }
 }
 
@@ -261,6 +338,28 @@ hipError_t binary(int dt, int op, const void *a, const void *b, void *out, const
   }
   const int blocks = grid_for(g.total, 256);
   const int cols = g.ndim ? g.shape[g.ndim - 1] : 1;
+  const size_t per = dt == F32 ? 4 : 8;
+  if (contig && g.total % per == 0 && (uintptr_t)a % 16 == 0 && (uintptr_t)b % 16 == 0 && (uintptr_t)out % 16 == 0 &&
+      (dt == F32 || dt == F16 || dt == BF16)) {
+    const size_t chunks = g.total / per;
+    const int vb = grid_for(chunks, 256);
+    const uint4 *a4 = static_cast<const uint4 *>(a), *b4 = static_cast<const uint4 *>(b);
+    uint4 *o4 = static_cast<uint4 *>(out);
+#define MH_BV(DTV, OPV) hipLaunchKernelGGL((binary_vec_kernel<DTV, OPV>), dim3(vb), dim3(256), 0, st, a4, b4, o4, chunks)
+#define MH_BOP(DTV)                                                                                          \
+  switch (op) {                                                                                              \
+  case BIN_ADD: MH_BV(DTV, BIN_ADD); break;                                                                  \
+  case BIN_SUB: MH_BV(DTV, BIN_SUB); break;                                                                  \
+  case BIN_MUL: MH_BV(DTV, BIN_MUL); break;                                                                  \
+  default: MH_BV(DTV, BIN_DIV); break;                                                                       \
+  }
+    if (dt == F32) { MH_BOP(F32) }
+    else if (dt == F16) { MH_BOP(F16) }
+    else { MH_BOP(BF16) }
+#undef MH_BOP
+#undef MH_BV
+    return hipGetLastError();
+  }
 #define MH_BIN(DTV)                                                                                          \
   {                                                                                                          \
     typedef typename Store<DTV>::T T;                                                                        \
@@ -284,8 +383,35 @@ hipError_t binary(int dt, int op, const void *a, const void *b, void *out, const
   return hipGetLastError();
 }
 
+template <int DT>
+void launch_unary_vec(int op, const void *in, void *out, size_t chunks, float c, hipStream_t st) {
+  const int blocks = grid_for(chunks, 256);
+  const uint4 *i4 = static_cast<const uint4 *>(in);
+  uint4 *o4 = static_cast<uint4 *>(out);
+#define MH_UN(OPV) hipLaunchKernelGGL((unary_vec_kernel<DT, OPV>), dim3(blocks), dim3(256), 0, st, i4, o4, chunks, c)
+  switch (op) {
+  case UN_RELU: MH_UN(UN_RELU); break;
+  case UN_SIGMOID: MH_UN(UN_SIGMOID); break;
+  case UN_GELU: MH_UN(UN_GELU); break;
+  case UN_EXP: MH_UN(UN_EXP); break;
+  case UN_LOG: MH_UN(UN_LOG); break;
+  case UN_SQRT: MH_UN(UN_SQRT); break;
+  case UN_RSQRT: MH_UN(UN_RSQRT); break;
+  case UN_SIN: MH_UN(UN_SIN); break;
+  default: MH_UN(UN_COS); break;
+  }
+#undef MH_UN
+}
+
 hipError_t unary(int dt, int op, const void *in, void *out, size_t n, float c, hipStream_t st) {
   if (n == 0) return hipSuccess;
+  const size_t per = dt == F32 ? 4 : 8;
+  if (n % per == 0 && (uintptr_t)in % 16 == 0 && (uintptr_t)out % 16 == 0 && (dt == F32 || dt == F16 || dt == BF16)) {
+    if (dt == F32) launch_unary_vec<F32>(op, in, out, n / per, c, st);
+    else if (dt == F16) launch_unary_vec<F16>(op, in, out, n / per, c, st);
+    else launch_unary_vec<BF16>(op, in, out, n / per, c, st);
+    return hipGetLastError();
+  }
   const int blocks = grid_for(n, 256);
   switch (dt) {
   case F32: hipLaunchKernelGGL(unary_kernel<F32>, dim3(blocks), dim3(256), 0, st, (const float *)in, (float *)out, n, op, c); break;

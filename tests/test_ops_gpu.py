@@ -199,6 +199,39 @@ def test_unary(hip, orc, dt):
             assert_close(to_host(out, dt), ref, dt, what=name)
 
 
+@pytest.mark.parametrize("dt", DTS)
+def test_elementwise_vector_path_bits(hip, dt):
+    """Whole 16-byte chunks of contiguous operands take the vectorised
+    kernels; the same values one element off a 16-byte boundary take the
+    scalar ones: bit for bit the same for every unary op and the four binary
+    ops (and the 1003-element tail case through the scalar kernel)."""
+    n = 4096
+    x = rand((n,), dt, 71, 2.0)
+    y = synth.encode(np.abs(dec(rand((n,), dt, 72, 2.0), dt)) + 0.5, dt)
+    # the same values at element 0 (aligned) and at element 1 (misaligned)
+    dev = {off: (to_device(np.concatenate([x[:off], x]), dt), to_device(np.concatenate([y[:off], y]), dt))
+           for off in (0, 1)}
+    for name in ("relu", "sigmoid", "gelu"):
+        outs = []
+        for off in (0, 1):
+            out = empty((n + off,), dt)
+            getattr(hip, name)(dev[off][0][off:], out[off:], n)
+            outs.append(to_host(out, dt)[off:])
+        assert np.array_equal(outs[0], outs[1]), name
+    info = BroadcastInfo((n,), (1,), (1,))
+    for fn in (hip.add, hip.sub, hip.mul, hip.div):
+        outs = []
+        for off in (0, 1):
+            out = empty((n + off,), dt)
+            fn(dev[off][0][off:], dev[off][1][off:], out[off:], info)
+            outs.append(to_host(out, dt)[off:])
+        assert np.array_equal(outs[0], outs[1])
+    xt = rand((1003,), dt, 73, 3.0)
+    out = empty((1003,), dt)
+    hip.relu(to_device(xt, dt), out, 1003)
+    assert np.array_equal(to_host(out, dt), np.where(dec(xt, dt) > 0, xt, synth.encode(np.zeros(1003), dt)))
+
+
 def test_gelu_known_values(hip):
     """x*sigmoid(1.702x) at -2, 0, 2 (reference tests/test_nn.cpp:385-402)."""
     x = synth.encode(np.array([-2.0, 0.0, 2.0]), F32)
