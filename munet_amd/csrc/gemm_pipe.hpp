@@ -308,6 +308,24 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
     in.cs = ep.ln_cs[c];
     in.bw = ep.ln_bw[c];
   }
+  // Chan's in-order combine of one chunk's partials (slots i < NI of chunk
+  // slot c; with CHECK only those below `chunk`)
+  template <int NI, bool CHECK>
+  static __device__ __forceinline__ void chunk_stats(const LnIn &in, int c, int chunk, int k0, int k1, float &mean,
+                                                     float &m2, float &m2x) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int j = c * LPC + i;  // index into this thread's loaded partials
+      if ((!CHECK || i < chunk) && k0 + i < k1) {
+        const float pm = j & 1 ? in.part[j / 2].z : in.part[j / 2].x;
+        const float p2 = j & 1 ? in.part[j / 2].w : in.part[j / 2].y;
+        const float d = __fsub_rn(pm, mean);
+        mean = __fmaf_rn(d, 1.0f / float(i + 1), mean);
+        m2 = __fadd_rn(m2, p2);
+        m2x = __fmaf_rn(__fmul_rn(d, d), float(i) / float(i + 1), m2x);
+      }
+    }
+  }
   __device__ __forceinline__ void ln_finish(const EpiArgs &ep, const LnIn &in, float2 *lnrow, float *lncs,
                                             float *lnbw, int tid) const {
     const int r = tid / TPR, q = tid % TPR, P = ep.ln_parts, chunk = ln_chunk(P);
@@ -319,18 +337,15 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
     for (int c = 0; c < CH; ++c) {
       const int k0 = (q * CH + c) * chunk, k1 = min(k0 + chunk, P);
       float mean = 0.f, m2 = 0.f, m2x = 0.f;  // m2x: the between-partial term / w
-#pragma unroll
-      for (int i = 0; i < LPC; ++i) {
-        const int j = c * LPC + i;  // index into this thread's loaded partials
-        if (i < chunk && k0 + i < k1) {
-          const float pm = j & 1 ? in.part[j / 2].z : in.part[j / 2].x;
-          const float p2 = j & 1 ? in.part[j / 2].w : in.part[j / 2].y;
-          const float d = __fsub_rn(pm, mean);
-          mean = __fmaf_rn(d, 1.0f / float(i + 1), mean);
-          m2 = __fadd_rn(m2, p2);
-          m2x = __fmaf_rn(__fmul_rn(d, d), float(i) / float(i + 1), m2x);
-        }
-      }
+      // the chunk length is the same for every lane: the usual lengths (the
+      // decoder's 8 and 16 partials per row) take loops of exactly that many
+      // slots; the rest run all LPC slots predicated
+      if (chunk == 2)
+        chunk_stats<2, false>(in, c, 2, k0, k1, mean, m2, m2x);
+      else if (chunk == 4)
+        chunk_stats<4, false>(in, c, 4, k0, k1, mean, m2, m2x);
+      else
+        chunk_stats<LPC, true>(in, c, chunk, k0, k1, mean, m2, m2x);
       cm[c] = mean;
       c2[c] = __fmaf_rn(m2x, w, m2);
       cn[c] = float(max(k1 - k0, 0)) * w;
@@ -478,18 +493,54 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
       // private memory.
       const uintptr_t o0 = reinterpret_cast<uintptr_t>(ep.outs[0]), o1 = reinterpret_cast<uintptr_t>(ep.outs[1]),
                       o2 = reinterpret_cast<uintptr_t>(ep.outs[2]);
+      const long thd = long(ep.T) * ep.hd;
+      if (ep.hd >= 16) {
+        // one division for the lane's first column, then 16-column steps
+        // (hd >= 16: a step crosses at most one head boundary); column
+        // n = which E + h hd + dd with E = H hd.  Columns past N keep
+        // counting: their stores are masked.
+        const int hq = (n0 + wn * WTN + lg * 4) / ep.hd, which = hq / ep.H, h0 = hq - which * ep.H;
+        int dd = n0 + wn * WTN + lg * 4 - hq * ep.hd, hleft = ep.H - h0;  // heads left in this output
+        // p: byte address of the column in the current output; next: the
+        // following output's base
+        uintptr_t p = (which == 0 ? o0 : which == 1 ? o1 : o2) + 2 * (h0 * thd + dd);
+        uintptr_t next = which == 0 ? o1 : o2;
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int n = min(n0 + wn * WTN + j * 16 + lg * 4, N - 4);
-        const int which = n / ep.E, e = n - which * ep.E, h = e / ep.hd, dd = e - h * ep.hd;
-        const uintptr_t o = which == 0 ? o0 : which == 1 ? o1 : o2;
-        cbase[j] = reinterpret_cast<uint16_t *>(o) + long(h) * ep.T * ep.hd + dd;
+        for (int j = 0; j < FN; ++j) {
+          cbase[j] = reinterpret_cast<uint16_t *>(p);
+          dd += 16;
+          p += 32;
+          if (dd >= ep.hd) {  // next head: skip the rest of this head's T rows
+            dd -= ep.hd;
+            p += 2 * (thd - ep.hd);
+            if (--hleft == 0) hleft = ep.H, p = next + 2 * dd, next = o2;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int n = min(n0 + wn * WTN + j * 16 + lg * 4, N - 4);
+          const int which = n / ep.E, e = n - which * ep.E, h = e / ep.hd, dd = e - h * ep.hd;
+          const uintptr_t o = which == 0 ? o0 : which == 1 ? o1 : o2;
+          cbase[j] = reinterpret_cast<uint16_t *>(o) + h * thd + dd;
+        }
       }
+      if (ep.T >= 16) {
+        // rows m = b T + t, in 16-row steps from the lane's first
+        int b = (m0 + wm * WTM + li) / ep.T, t = m0 + wm * WTM + li - b * ep.T;
 #pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int m = min(m0 + wm * WTM + i * 16 + li, M - 1);
-        const int b = m / ep.T, t = m - b * ep.T;
-        roff[i] = (long(b) * ep.H * ep.T + t) * ep.hd;
+        for (int i = 0; i < FM; ++i) {
+          roff[i] = (long(b) * ep.H * ep.T + t) * ep.hd;
+          t += 16;
+          if (t >= ep.T) t -= ep.T, ++b;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const int m = min(m0 + wm * WTM + i * 16 + li, M - 1);
+          const int b = m / ep.T, t = m - b * ep.T;
+          roff[i] = (long(b) * ep.H * ep.T + t) * ep.hd;
+        }
       }
       al8 = (ep.hd & 3) == 0 && ((uintptr_t)ep.outs[0] & 7) == 0 && ((uintptr_t)ep.outs[1] & 7) == 0 &&
             ((uintptr_t)ep.outs[2] & 7) == 0;

@@ -96,6 +96,31 @@ def _mha_params(E, dt, seed):
 
 
 @pytest.mark.parametrize("dt", [F16, BF16, F32])
+@pytest.mark.parametrize("B,T,E,H", [(2, 40, 64, 2), (1, 3, 8, 2), (3, 20, 48, 3), (1, 16, 40, 2), (1, 17, 96, 6),
+                                     (2, 9, 96, 2), (2, 1024, 768, 12)])
+def test_qkv_headsplit_bits(hip, dt, B, T, E, H):
+    """The head-split projection stores exactly the bits of the row-major
+    Linear with the concatenated weight, each column at [which][b, h, t, d]:
+    head widths below 16 and sequences below 16 take the per-element index
+    divisions, the rest the stepped column and row offsets (heads of 16, 20,
+    32 and 64 columns; the decoder's shape on its 128x288 tile)."""
+    hd = E // H
+    x = rand((B * T, E), dt, 120)
+    w = rand((E, 3 * E), dt, 121, 1.0 / np.sqrt(E))
+    b = rand((3 * E,), dt, 122, 0.1)
+    wt = empty((3 * E, E), dt)
+    hip.pack_linear_weight(to_device(w, dt), wt, E, 3 * E)
+    xd, bd = to_device(x, dt), to_device(b, dt)
+    flat = empty((B * T, 3 * E), dt)
+    hip.linear(xd, wt, bd, flat, B * T, E, 3 * E)
+    q, k, v = (empty((B * H * T * hd,), dt) for _ in range(3))
+    hip.qkv_projection(xd, wt, bd, q, k, v, B, T, E, H)
+    ref = to_host(flat, dt).reshape(B, T, 3, H, hd).transpose(2, 0, 3, 1, 4)
+    for i, t in enumerate((q, k, v)):
+        assert np.array_equal(to_host(t, dt).reshape(B, H, T, hd), ref[i]), "qkv"[i]
+
+
+@pytest.mark.parametrize("dt", [F16, BF16, F32])
 @pytest.mark.parametrize("B,T,H,hd", [(2, 64, 2, 64), (1, 200, 3, 64), (64, 72, 4, 64), (1, 77, 2, 64),
                                       (2, 40, 2, 32), (1, 3, 2, 4),
                                       (1, 128, 2, 64), (2, 192, 3, 64), (1, 320, 2, 64), (5, 256, 16, 64),
