@@ -961,6 +961,12 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
   // and pinned with sched_barrier (the scheduler cannot place inline assembly
   // in sched_group_barrier slots).
   constexpr int NMM = FM * FN, NRD = FM + FN;
+  // Two stages: slab k + 1 is fetched during step k and read in step k's
+  // second half.  Its wait and barrier come LATE MFMAs before the end of that
+  // half (two fragment reads per MFMA after them) rather than at its start,
+  // so the fetch has most of the step to land instead of half of it.
+  constexpr int LATE = S == 2 ? (NRD + 1) / 2 : 0;
+  static_assert(LATE <= NMM, "late wait");
   constexpr int STAGE4 = (BM + BN) * 8;  // u32x4 per stage
   const int c1 = 4 + g.lg, c0f = g.lg;
 #define MH_FRAG(L, C, X, AF, BF)                                                                   \
@@ -989,14 +995,27 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
       if (t < NDMA) MH_DMA(t, kf_, sf_)                                                            \
       else MH_FRAG(Ls_, c1, t - NDMA, af1, bf1)                                                    \
     }                                                                                              \
-    dma_wait<NDMA * (S - 2)>();                                                                    \
-    __syncthreads();                                                                               \
+    if constexpr (LATE == 0) {                                                                     \
+      dma_wait<NDMA * (S - 2)>();                                                                  \
+      __syncthreads();                                                                             \
+    }                                                                                              \
     _Pragma("unroll") for (int t = 0; t < NMM; ++t) {                                              \
+      if (LATE > 0 && t == NMM - LATE) {                                                           \
+        dma_wait<0>();                                                                             \
+        __syncthreads();                                                                           \
+      }                                                                                            \
       PipeMfma<DT>::mma(acc[t / FN][t % FN], bf1[t % FN], af1[t / FN]);                            \
-      if (t < NRD) MH_FRAG(Ln_, c0f, t, af0, bf0)                                                  \
+      if (LATE == 0) {                                                                             \
+        if (t < NRD) MH_FRAG(Ln_, c0f, t, af0, bf0)                                                \
+      } else if (t >= NMM - LATE) {                                                                \
+        MH_FRAG(Ln_, c0f, 2 * (t - (NMM - LATE)), af0, bf0)                                        \
+        if (2 * (t - (NMM - LATE)) + 1 < NRD) MH_FRAG(Ln_, c0f, 2 * (t - (NMM - LATE)) + 1, af0, bf0) \
+      }                                                                                            \
       __builtin_amdgcn_sched_barrier(0);                                                           \
     }                                                                                              \
-    _Pragma("unroll") for (int t = NMM; t < NRD; ++t) MH_FRAG(Ln_, c0f, t, af0, bf0)               \
+    if constexpr (LATE == 0) {                                                                     \
+      _Pragma("unroll") for (int t = NMM; t < NRD; ++t) MH_FRAG(Ln_, c0f, t, af0, bf0)             \
+    }                                                                                              \
   }
   MH_DSTEP(0, true);
   for (int k = 1; k < KT; ++k) MH_DSTEP(k, false);

@@ -18,7 +18,7 @@ hipError_t run(int tile, const void *A, const void *Bt, int M, int N, int K, lon
   switch (tile) {
   case 16: launch_dma<DT, 256, 192, 4, 2, 2, EK>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;
   case 17: launch_dma<DT, 128, 96, 4, 2, 4, EK>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;
-  case 19: launch_dma<DT, 128, 288, 4, 2, 2, EK>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;
+  case 19: launch_dma<DT, 128, 288, 4, 2, 3, EK>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;
   default: return hipErrorNotSupported;
   }
   return hipGetLastError();
