@@ -5,7 +5,6 @@
 // are instantiated in gemm_pipe_fixed_*.hip, 256-row tiles in
 // gemm_pipe_big.hip.
 #include <algorithm>
-#include <cstdlib>
 #include "gemm_pipe.hpp"
 
 namespace mh {
@@ -39,8 +38,8 @@ int pipe_wave_cols(int tile) {
 //  * otherwise register-staged: 128x128 when N tiles evenly by 128 and there
 //    are >= 2.5 tiles per CU (FFN up, LM head), 128x96 when N tiles evenly by
 //    96 (QKV), else 128x128 / 128x64 / 64x64 by tile count.
-// (Direct-to-LDS 128x128 with 2 stages runs the LM head 5% faster replayed on
-// its own, and 20 us slower inside the forward.)
+// (The vocabulary head, a non-temporal output, takes direct-to-LDS 128x128
+// with two stages: see launch_dt.)
 int auto_tile(bool dma, int M, int N, int K, int batch) {
   const long t128 = long((M + 127) / 128) * ((N + 127) / 128) * batch;
   const long t96 = long((M + 127) / 128) * ((N + 95) / 96) * batch;
@@ -90,6 +89,10 @@ hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long ld
   // tile only has the plain, bias and non-temporal bias ones: a forced tile
   // without the program takes the automatic choice
   const bool head_prog = kind == PK_PLAIN || kind == PK_BIAS || kind == PK_BIAS_NT;
+  // a large streamed output (the vocabulary head): direct-to-LDS 128x128,
+  // two stages (with the late wait for the next slab: forward 1.506 ->
+  // 1.491 ms against the register-staged 128x128, 1.497 on the 256x256 tile)
+  if (tile < 0 && kind == PK_BIAS_NT && dma) tile = 9;
   if (tile == 18 && !(DT == BF16 && dma && head_prog)) tile = -1;
   if (tile < 0 || (kind >= PK_LN_BIAS && !fixed_tile(tile) && tile != 18)) tile = auto_tile(dma, M, N, K, batch);
   if (tile >= 7 && !dma) tile = 0;
