@@ -223,6 +223,9 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
   __device__ __forceinline__ bool has_resid(const EpiArgs &ep) const {
     return KT_::FIXED ? KT_::RESID : ep.resid != nullptr;
   }
+  // vector loads prefetch() issues for a fixed program (one 8-byte load per
+  // bias fragment column and per residual fragment)
+  static constexpr int NPRE = (PRE_B && KT_::BIAS ? FN : 0) + (PRE_R && KT_::RESID ? FM * FN : 0);
   __device__ __forceinline__ void prefetch(const EpiArgs &ep) {
     if (PRE_B && fast && has_bias(ep)) {
 #pragma unroll
@@ -1017,7 +1020,14 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
   u32x4 af0[FM], bf0[FN], af1[FM], bf1[FN];
   typedef PipeEpi<DT, BM, BN, WGM, WGN, EK> Epi;
   Epi epi(ep, g, M, N, m0, n0);
-  epi.prefetch(ep);
+  // a fixed program's bias / residual prefetch goes after the first slabs'
+  // loads, and the wait for slab 0 leaves it in flight (issued first, the
+  // residual's scattered 8-byte loads held slab 0's wait back: 1.3 us of
+  // the prologue on the 128x96 tile); the general program's load count is
+  // known only at run time, so it prefetches first
+  constexpr bool LATE_PRE = PipeKindT<EK>::FIXED;
+  static_assert(NDMA * (S - 2) + Epi::NPRE < 64, "vmcnt range");
+  if constexpr (!LATE_PRE) epi.prefetch(ep);
 
   typename Epi::LnIn lnin;
   if constexpr (PipeKindT<EK>::LN) epi.ln_issue(ep, lnin, tid);
@@ -1029,7 +1039,12 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
 #pragma unroll
     for (int t = 0; t < NDMA; ++t) MH_DMA(t, kt, s);
   }
-  dma_wait<NDMA * (S - 2)>();
+  if constexpr (LATE_PRE) {
+    epi.prefetch(ep);
+    dma_wait<NDMA * (S - 2) + Epi::NPRE>();
+  } else {
+    dma_wait<NDMA * (S - 2)>();
+  }
   if constexpr (PipeKindT<EK>::LN) epi.ln_finish(ep, lnin, lnrow, lncs, lnbw, tid);
   __syncthreads();
   g.template frags<0>(lds[0], af0, bf0);
