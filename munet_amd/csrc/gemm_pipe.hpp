@@ -1062,7 +1062,9 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
   // second half.  Its wait and barrier come LATE MFMAs before the end of that
   // half (two fragment reads per MFMA after them) rather than at its start,
   // so the fetch has most of the step to land instead of half of it.
-  constexpr int LATE = S == 2 ? (NRD + 1) / 2 : 0;
+  // fragment reads per MFMA after the late wait (3 and 5 measured the same)
+  constexpr int RPM = 2;
+  constexpr int LATE = S == 2 ? (NRD + RPM - 1) / RPM : 0;
   static_assert(LATE <= NMM, "late wait");
   constexpr int STAGE4 = (BM + BN) * 8;  // u32x4 per stage
   const int c1 = 4 + g.lg, c0f = g.lg;
@@ -1105,8 +1107,8 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
       if (LATE == 0) {                                                                             \
         if (t < NRD) MH_FRAG(Ln_, c0f, t, af0, bf0)                                                \
       } else if (t >= NMM - LATE) {                                                                \
-        MH_FRAG(Ln_, c0f, 2 * (t - (NMM - LATE)), af0, bf0)                                        \
-        if (2 * (t - (NMM - LATE)) + 1 < NRD) MH_FRAG(Ln_, c0f, 2 * (t - (NMM - LATE)) + 1, af0, bf0) \
+        _Pragma("unroll") for (int q_ = 0; q_ < RPM; ++q_)                                          \
+          if (RPM * (t - (NMM - LATE)) + q_ < NRD) MH_FRAG(Ln_, c0f, RPM * (t - (NMM - LATE)) + q_, af0, bf0) \
       }                                                                                            \
       __builtin_amdgcn_sched_barrier(0);                                                           \
     }                                                                                              \
