@@ -70,8 +70,11 @@ template <> struct AttnMfma<F16> {
   static __device__ __forceinline__ uint16_t cvt(float v) {
     return __builtin_bit_cast(uint16_t, _Float16(v));
   }
+  // two floats -> packed fp16 in one v_cvt_pk_f16_f32 (the same RNE as cvt)
   static __device__ __forceinline__ uint32_t cvt2(float a, float b) {
-    return uint32_t(cvt(a)) | (uint32_t(cvt(b)) << 16);
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, h2));
   }
 };
 
@@ -86,10 +89,9 @@ template <> __device__ __forceinline__ void round4<BF16>(float v[4]) {
   v[0] = __uint_as_float(p0 << 16); v[1] = __uint_as_float(p0 & 0xffff0000u);
   v[2] = __uint_as_float(p1 << 16); v[3] = __uint_as_float(p1 & 0xffff0000u);
 }
-template <> __device__ __forceinline__ void round4<F16>(float v[4]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = Store<F16>::round(v[i]);
-}
+// (MuNet's half-away codec: the 2-op normal-range form, the exact form only
+// when some lane of the wave needs it; the same bits as Store<F16>::round)
+template <> __device__ __forceinline__ void round4<F16>(float v[4]) { round4_f16(v); }
 
 // LDS tiles: 64 rows x 8 chunks of 16 bytes, chunk c of row r stored at
 // c ^ (r & 7).
@@ -688,9 +690,17 @@ flash_attn_pipe_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restric
   // round the scores and take this lane's max
   auto round_scores16 = [&](const f32x4 (&s)[4], float (&v)[16]) -> float {
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
+    for (int jt = 0; jt < 4; ++jt) {
+      if constexpr (DT == BF16) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[jt * 4 + e] = round1<DT>(s[jt][e]);
+        for (int e = 0; e < 4; ++e) v[jt * 4 + e] = round1<DT>(s[jt][e]);
+      } else {
+        float w[4] = {s[jt][0], s[jt][1], s[jt][2], s[jt][3]};
+        round4<DT>(w);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[jt * 4 + e] = w[e];
+      }
+    }
     return lane_max(v);
   };
   // the diagonal tile (j0 = q0): key j0 + 16 jt + 4 lg + e is masked above
