@@ -215,6 +215,44 @@ __device__ __forceinline__ uint2 epi_fast_bf16_fixed(float v[4], uint2 bias, uin
   return pack4_bf16(v);
 }
 
+// fp16: the same fixed chain with the reference's fp16 rounding (round4_f16)
+// after every op, the last one included (the rounded values pack exactly);
+// the bits of epi_fast_f16_value for the same chain.
+template <bool BIAS, int ACT, bool RESID>
+__device__ __forceinline__ uint2 epi_fast_f16_fixed(float v[4], uint2 bias, uint2 resid, float gelu_c) {
+  round4_f16(v);
+  if constexpr (BIAS) {
+    v[0] += lo_f16(bias.x); v[1] += hi_f16(bias.x); v[2] += lo_f16(bias.y); v[3] += hi_f16(bias.y);
+    round4_f16(v);
+  }
+  if constexpr (ACT == ACT_RELU) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = v[i] > 0.0f ? v[i] : 0.0f;  // exact on rounded values
+  } else if constexpr (ACT == ACT_GELU) {
+    float t[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[i] = v[i] * gelu_c;
+    round4_f16(t);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[i] = sigmoidf_ref(t[i]);
+    round4_f16(t);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] *= t[i];
+    round4_f16(v);
+  }
+  if constexpr (RESID) {
+    v[0] = lo_f16(resid.x) + v[0]; v[1] = hi_f16(resid.x) + v[1];
+    v[2] = lo_f16(resid.y) + v[2]; v[3] = hi_f16(resid.y) + v[3];
+    round4_f16(v);
+  }
+  return make_uint2(pack_f16x2_exact(v[0], v[1]), pack_f16x2_exact(v[2], v[3]));
+}
+template <int DT, bool BIAS, int ACT, bool RESID>
+__device__ __forceinline__ uint2 epi_fast_fixed(float v[4], uint2 bias, uint2 resid, float gelu_c) {
+  if constexpr (DT == F16) return epi_fast_f16_fixed<BIAS, ACT, RESID>(v, bias, resid, gelu_c);
+  else return epi_fast_bf16_fixed<BIAS, ACT, RESID>(v, bias, resid, gelu_c);
+}
+
 // The 16-bit fast path for output columns n..n+3 of row m.
 template <int DT>
 __device__ __forceinline__ void epi_fast16(const EpiArgs &ep, int m, int n, float v[4], uint2 bias, uint2 resid,

@@ -65,13 +65,14 @@ bool fixed_tile(int tile) {
 // outside the fixed programs (it has no general form).
 int pipe_kind(int dt, int N, int batch, long sc, const EpiArgs &ep) {
   const bool fold = ep.ln_stats || ep.stats_out;
-  const bool fast = dt == BF16 && N % 4 == 0 && ep.mode != EPI_CONVT && (!ep.resid || (ep.ldr & 3) == 0);
+  const bool fast = (dt == BF16 || dt == F16) && N % 4 == 0 && ep.mode != EPI_CONVT && (!ep.resid || (ep.ldr & 3) == 0);
   const bool al8 = ep.mode == EPI_HEADSPLIT
                        ? (ep.hd & 3) == 0 && ((uintptr_t)ep.outs[0] & 7) == 0 && ((uintptr_t)ep.outs[1] & 7) == 0 &&
                              ((uintptr_t)ep.outs[2] & 7) == 0
                        : ((uintptr_t)ep.out & 7) == 0 && (ep.ldc & 3) == 0 && (batch == 1 || (sc & 3) == 0);
   if (!fast || !al8 || (ep.bias && ep.bias_first)) return fold ? -1 : PK_GENERAL;
   const bool hb = ep.bias != nullptr, hr = ep.resid != nullptr;
+  if (fold && dt != BF16) return -1;  // the folded LayerNorm programs are bf16 only
   if (ep.ln_stats) {
     if (ep.stats_out || !hb || hr) return -1;
     return ep.act == ACT_NONE ? PK_LN_BIAS : ep.act == ACT_GELU ? PK_LN_BIAS_GELU : -1;
@@ -105,8 +106,8 @@ hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long ld
     return gemm_pipe_wide(DT, kind, tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
   if (tile == 18) return gemm_pipe_head(kind, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
   if (kind > PK_GENERAL && fixed_tile(tile))
-    return tile <= 3 ? gemm_pipe_fixed_staged(kind, tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st)
-                     : gemm_pipe_fixed_dma(kind, tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
+    return tile <= 3 ? gemm_pipe_fixed_staged(DT, kind, tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st)
+                     : gemm_pipe_fixed_dma(DT, kind, tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
   if (tile >= 4 && tile <= 6) return gemm_pipe_big(DT, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile - 4, st);
   if (tile >= 13) return gemm_pipe_big(DT, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile - 4, st);
   switch (tile) {

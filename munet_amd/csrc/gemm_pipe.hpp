@@ -452,7 +452,7 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
         for (int j = 0; j < FN; ++j) {
           float v[4] = {acc[p * FMP + i][j][0], acc[p * FMP + i][j][1], acc[p * FMP + i][j][2],
                         acc[p * FMP + i][j][3]};
-          const uint2 pk = epi_fast_bf16_fixed<KT_::BIAS, ACT_NONE, false>(v, bq[j], make_uint2(0, 0), ep.gelu_c);
+          const uint2 pk = epi_fast_fixed<DT, KT_::BIAS, ACT_NONE, false>(v, bq[j], make_uint2(0, 0), ep.gelu_c);
           *reinterpret_cast<uint2 *>(stage + (i * 16 + g.li) * NT_RB + (j * 16 + g.lg * 4) * 2) = pk;
         }
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
@@ -512,7 +512,7 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
           v[2] = __fmaf_rn(rs.y, __fmaf_rn(-rs.x, lcs[j].z, v[2]), lbw[j].z);
           v[3] = __fmaf_rn(rs.y, __fmaf_rn(-rs.x, lcs[j].w, v[3]), lbw[j].w);
         }
-        const uint2 pk = epi_fast_bf16_fixed<KT_::BIAS, KT_::ACT, KT_::RESID>(v, bq[j], RQL(i, j), ep.gelu_c);
+        const uint2 pk = epi_fast_fixed<DT, KT_::BIAS, KT_::ACT, KT_::RESID>(v, bq[j], RQL(i, j), ep.gelu_c);
         *reinterpret_cast<uint2 *>(stage + r * LN_RB + (wn * WTN + j * 16 + lg * 4) * 2) = pk;
         if constexpr (KT_::ST) stats_add(ep, sa, pk, m0 + r, j);
       }
@@ -691,7 +691,7 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
             v[2] = __fmaf_rn(rs.y, __fmaf_rn(-rs.x, lcs[j].z, v[2]), lbw[j].z);
             v[3] = __fmaf_rn(rs.y, __fmaf_rn(-rs.x, lcs[j].w, v[3]), lbw[j].w);
           }
-          const uint2 pk = epi_fast_bf16_fixed<KT_::BIAS, KT_::ACT, KT_::RESID>(v, bq[j], RQ(i, j), ep.gelu_c);
+          const uint2 pk = epi_fast_fixed<DT, KT_::BIAS, KT_::ACT, KT_::RESID>(v, bq[j], RQ(i, j), ep.gelu_c);
           if (interior || (m < M && n < N)) {
             if constexpr (KT_::NT)
               __builtin_nontemporal_store((uint64_t(pk.y) << 32) | pk.x, reinterpret_cast<uint64_t *>(cbase[j] + roff[i]));
@@ -1160,18 +1160,18 @@ void launch_dma(const void *A, const void *Bt, int M, int N, int K, long lda, lo
 
 }  // namespace
 
-// Fixed epilogue programs (kind != PK_GENERAL) for bf16 on the tiles the
-// automatic choice uses: 0 128x128, 1 128x64, 2 64x64, 3 128x96
+// Fixed epilogue programs (kind != PK_GENERAL; fp16: those without a folded
+// LayerNorm) on the tiles the automatic choice uses: 0 128x128, 1 128x64, 2 64x64, 3 128x96
 // (register-staged, gemm_pipe_fixed_staged.hip) and 8 128x96 4 stages,
 // 9 128x128 2 stages (direct-to-LDS, gemm_pipe_fixed_dma.hip).  They return
 // hipErrorNotSupported for any other tile.
-hipError_t gemm_pipe_fixed_staged(int kind, int tile, const void *A, const void *Bt, int M, int N, int K, long lda,
+hipError_t gemm_pipe_fixed_staged(int dt, int kind, int tile, const void *A, const void *Bt, int M, int N, int K, long lda,
                                   long ldb, int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st);
 // Eight-wave direct-to-LDS tiles, every program (gemm_pipe_wide.hip): 16
 // 256x192 two stages, 17 128x96 four stages.
 hipError_t gemm_pipe_wide(int dt, int kind, int tile, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb,
                           int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st);
-hipError_t gemm_pipe_fixed_dma(int kind, int tile, const void *A, const void *Bt, int M, int N, int K, long lda,
+hipError_t gemm_pipe_fixed_dma(int dt, int kind, int tile, const void *A, const void *Bt, int M, int N, int K, long lda,
                                long ldb, int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st);
 // Direct-to-LDS 256x256, two stages, AGPR accumulators (gemm_pipe_head.hip,
 // tile 18): the plain, bias and non-temporal bias programs.

@@ -32,8 +32,16 @@ hipError_t gemm_pipe_wide(int dt, int kind, int tile, const void *A, const void 
                           int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st) {
 #define MH_RUN(EK) return run<BF16, EK>(tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st)
   if (dt == F16) {
-    if (kind != PK_GENERAL) return hipErrorInvalidValue;
-    return run<F16, PK_GENERAL>(tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
+    // fp16: the general program and the fixed ones without a folded LayerNorm
+    switch (kind) {
+    case PK_GENERAL: return run<F16, PK_GENERAL>(tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
+    case PK_PLAIN: return run<F16, PK_PLAIN>(tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
+    case PK_BIAS: return run<F16, PK_BIAS>(tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
+    case PK_BIAS_GELU: return run<F16, PK_BIAS_GELU>(tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
+    case PK_BIAS_RESID: return run<F16, PK_BIAS_RESID>(tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
+    case PK_BIAS_NT: return run<F16, PK_BIAS_NT>(tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
+    default: return hipErrorInvalidValue;
+    }
   }
   switch (kind) {
   case PK_GENERAL: MH_RUN(PK_GENERAL);

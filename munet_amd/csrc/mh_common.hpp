@@ -85,17 +85,20 @@ __device__ __forceinline__ float round_f16_exact(float x) {
 }
 // Four values at once: the 2-op normal-range rounding, and the full
 // branch-free rounding for all four only when some lane of the wave has a
-// value outside zero and the normal half range (rare in practice).
+// value outside the normal half range [2^-14, 65520) (rare in practice;
+// zero takes the full rounding too).  The range test is one clamp and one
+// compare per value: med3(|x|, 2^-14, the float below 65520) == |x|.
 __device__ __forceinline__ void round4_f16(float v[4]) {
-  bool slow = false;
+  uint64_t slow = 0;  // lanes of the wave with a value outside the range (scalar masks)
   float r[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const uint32_t b = __float_as_uint(v[e]), a = b & 0x7fffffffu;
+    const uint32_t b = __float_as_uint(v[e]);
     r[e] = __uint_as_float((b + 0x1000u) & 0xffffe000u);
-    slow |= a != 0u && a - 0x38800000u >= 0x477ff000u - 0x38800000u;
+    const float t = __builtin_fabsf(v[e]);
+    slow |= __builtin_amdgcn_ballot_w64(__builtin_amdgcn_fmed3f(t, 6.103515625e-05f, __uint_as_float(0x477fefffu)) != t);
   }
-  if (__builtin_amdgcn_ballot_w64(slow)) {
+  if (slow) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) r[e] = round_f16_exact(v[e]);
   }

@@ -103,3 +103,31 @@ def test_xcd_tile_enumeration_bit_identical(tile, hip, monkeypatch):
                 outs.append(out.view(torch.int16).clone())
             for gn, o in zip(("1", "3", "8", "16", "64"), outs[1:]):
                 assert torch.equal(outs[0], o), f"tile {tile} gn {gn} {M}x{K}x{N} act={act}"
+
+
+@pytest.mark.parametrize("tile", [200, 201, 202, 203, 208, 209, 216, 217])
+def test_f16_fixed_programs_bit_identical_to_general(tile, hip, monkeypatch):
+    """fp16 runs the fixed epilogue programs (plain, bias, bias+GELU,
+    bias+ReLU, bias+residual) when the destination is 8-byte aligned; an
+    output one element off that alignment takes the general program on the
+    same tile.  Both round every step with MuNet's half-away fp16 codec, so the
+    outputs are bit-identical."""
+    import torch
+    from munet_amd.backend import empty
+    monkeypatch.setenv("MUNET_HIP_GEMM_TILE", str(tile))
+    g = torch.Generator(device="cuda").manual_seed(11)
+    M, K, N = 512, 320, 384
+    h = torch.float16
+    x = torch.randn(M, K, device="cuda", generator=g).to(h)
+    wt = (torch.randn(N, K, device="cuda", generator=g) * 0.1).to(h)
+    bias = (torch.randn(N, device="cuda", generator=g) * 0.1).to(h)
+    r = torch.randn(M, N, device="cuda", generator=g).to(h)
+    for act, resid, use_bias in [(0, None, False), (0, None, True), (2, None, True), (1, None, True), (0, r, True)]:
+        outs = []
+        for shift in (0, 1):
+            buf = empty((M * N + 1,), 1)
+            out = buf[shift:shift + M * N]
+            hip.linear(x, wt, bias if use_bias else None, out, M, K, N, act, resid)
+            torch.cuda.synchronize()
+            outs.append(out.view(torch.int16).clone())
+        assert torch.equal(outs[0], outs[1]), f"tile {tile} act={act} resid={resid is not None} bias={use_bias}"
