@@ -50,6 +50,23 @@ def test_mlp_full(orc):
     assert np.array_equal(y, y2)  # graph replays are deterministic
 
 
+@pytest.mark.parametrize("sizes,batch", [((784, 256, 256, 10), 50), ((512, 200, 36), 64), ((4096, 128, 6), 32),
+                                         ((1024, 72, 130), 70)])
+def test_splitk_linears(orc, sizes, batch):
+    """Small fp32 Linears with K >= 512 take split-K (fewer than 32 64x64
+    output tiles): K slices of 784/7, 512/8, 4096/64 and 1024/16 as a batched
+    partial product, then the slice sum and bias + ReLU in a second kernel;
+    ragged M and N tails and Linears below the split threshold included.
+    Against the oracle, and repeated runs give the same bits."""
+    cfg = models.mlp_config(sizes)
+    eng, p, x = _build(cfg, (batch, sizes[0]), "mlp", seed_scope=f"sk{sizes[0]}")
+    y = eng.run(x)
+    ref = omodels.forward(orc, cfg, p, x)
+    assert_close(y, ref, synth.F32, what=f"split-K mlp {sizes}")
+    for _ in range(3):
+        assert np.array_equal(eng.run(x), y)
+
+
 def test_cnn_full(orc):
     """small CNN fp32, batch 32, 3x32x32."""
     cfg = models.cnn_config()
