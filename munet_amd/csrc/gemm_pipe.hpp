@@ -248,7 +248,9 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
   // the shares with Chan's parallel-variance formula, then across adjacent
   // lanes, and writes (mean, rstd) per row and the column terms to LDS; the
   // K loop's barriers make them visible to the epilogue.
-  static constexpr int TPR = G::NT / BM, LNCH = 32, CH = 4 / TPR;
+  // (tiles of fewer rows than NT / 4, which never fold a LayerNorm, size the
+  // slots as for 4 threads per row; ln_issue / ln_finish reject them)
+  static constexpr int TPR = G::NT / BM < 4 ? G::NT / BM : 4, LNCH = 32, CH = 4 / TPR;
   static_assert(TPR == 1 || TPR == 2 || TPR == 4, "threads per row");
   // A row's partials are split into 4 chunks of `chunk` (even) partials; each
   // chunk is combined in order, then the chunks pairwise, (0 1) (2 3) and
@@ -278,6 +280,7 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
   // per chunk slot), so every index below is a compile-time constant
   static constexpr int LPC = LNCH / CH;
   __device__ __forceinline__ void ln_issue(const EpiArgs &ep, LnIn &in, int tid) const {
+    static_assert(G::NT / BM <= 4, "a folded LayerNorm needs at most 4 threads per tile row");
     // a chunk holds up to ln_chunk(64) = 16 partials (the host admits 64 per
     // row): every tile that folds a LayerNorm needs room for all of them
     static_assert(LPC >= 16, "LayerNorm chunk slot smaller than the largest chunk");

@@ -342,8 +342,9 @@ def test_conv_pipelined_kernel_bits(hip, dt, B, iC, H, W, oC, k, s, p, act, monk
     """The pipelined implicit-GEMM convolution (iC % 64 == 0) gives the bits
     of the general implicit-GEMM kernel (same MFMA sequence, bias added to the
     fp32 accumulator, one rounding, ReLU) on NHWC inputs, over the block
-    tile it picks (64x64), strides, 1x1 and 5x5 filters,
-    ragged pixel counts and padding on every side."""
+    tiles (the automatic choice, and the 32x64 / 64x32 tiles forced),
+    strides, 1x1 and 5x5 filters, ragged pixel counts and padding on every
+    side."""
     x = rand((B, H, W, iC), dt, 120)
     w = rand((oC, iC, k, k), dt, 121, np.sqrt(2.0 / (iC * k * k)))
     b = rand((oC,), dt, 122, 0.1)
@@ -352,16 +353,20 @@ def test_conv_pipelined_kernel_bits(hip, dt, B, iC, H, W, oC, k, s, p, act, monk
     hip.pack_conv_weight(to_device(w, dt), wo, oC, iC, k, k)
     xd, bd = to_device(x, dt), to_device(b, dt)
     outs = {}
-    for name in ("pipelined", "general"):
+    for name in ("pipelined", "tile3", "tile4", "general"):
         monkeypatch.delenv("MUNET_HIP_CONV_KERNEL", raising=False)
+        monkeypatch.delenv("MUNET_HIP_CONV_TILE", raising=False)
         if name == "general":
             monkeypatch.setenv("MUNET_HIP_CONV_KERNEL", "general")
+        elif name.startswith("tile"):
+            monkeypatch.setenv("MUNET_HIP_CONV_TILE", name[4:])
         out = empty((B, oh, ow, oC), dt)
         hip.conv2d_nhwc(xd, wo, bd, out, B, iC, H, W, oC, k, k, s, p, act)
         hip.synchronize()
         outs[name] = to_host(out, dt)
     assert np.all(np.isfinite(dec(outs["pipelined"], dt)))
-    assert np.array_equal(outs["pipelined"], outs["general"]), "pipelined conv differs from the general kernel"
+    for name in ("pipelined", "tile3", "tile4"):
+        assert np.array_equal(outs[name], outs["general"]), f"{name} conv differs from the general kernel"
 
 
 def test_conv2d_closed_form(hip):
