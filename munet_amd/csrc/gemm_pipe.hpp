@@ -1063,9 +1063,9 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
   constexpr int NMM = FM * FN, NRD = FM + FN;
   // Two stages: slab k + 1 is fetched during step k and read in step k's
   // second half.  Its wait and barrier come LATE MFMAs before the end of that
-  // half (two fragment reads per MFMA after them) rather than at its start,
-  // so the fetch has most of the step to land instead of half of it.
-  // fragment reads per MFMA after the late wait (3 and 5 measured the same)
+  // half (RPM fragment reads per MFMA after them) rather than at its start,
+  // so the fetch has most of the step to land instead of half of it.  RPM =
+  // 2 (3 and 5 measured the same).
   constexpr int RPM = 2;
   constexpr int LATE = S == 2 ? (NRD + RPM - 1) / RPM : 0;
   static_assert(LATE <= NMM, "late wait");
