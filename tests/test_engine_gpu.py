@@ -67,6 +67,26 @@ def test_splitk_linears(orc, sizes, batch):
         assert np.array_equal(eng.run(x), y)
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_streamed_output_linear(orc, dtype, monkeypatch):
+    """A final output of at least 64 MiB is stored non-temporally in whole
+    lines (the vocabulary head's program, fp16 included): a 1024 x 64 ->
+    32768 Linear against the oracle, and bit for bit against the same engine
+    with ordinary stores (MUNET_HIP_STREAM_OUT=0)."""
+    from munet_amd import engine as meng
+    cfg = models.mlp_config((64, 32768), dtype=dtype)
+    eng, p, x = _build(cfg, (1024, 64), "mlp", seed_scope=f"so{dtype}")
+    assert eng.stats()["stream_out"] is True
+    y = eng.run(x)
+    dt = synth.DTYPE_CODES[dtype]
+    ref = omodels.forward(orc, cfg, p, x)
+    assert_close(y, ref, dt, what=f"streamed {dtype} linear")
+    monkeypatch.setenv("MUNET_HIP_STREAM_OUT", "0")
+    eng2 = meng.Engine(0).load(cfg, p).compile((1024, 64))
+    assert eng2.stats()["stream_out"] is False
+    assert np.array_equal(eng2.run(x), y)
+
+
 def test_cnn_full(orc):
     """small CNN fp32, batch 32, 3x32x32."""
     cfg = models.cnn_config()
