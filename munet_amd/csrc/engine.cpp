@@ -148,6 +148,7 @@ struct EngineImpl {
   std::vector<Op> ops;
   int input = -1, output = -1;
   bool stream_out = false;  // the final GEMM stores the output non-temporally
+  bool prefetch = true;     // each GEMM touches the next GEMM's weights
   Shape in_shape;
 
   // device state
@@ -732,6 +733,27 @@ struct EngineImpl {
     }
   }
 
+  // The weights of the first GEMM after op o, as o's GEMM prefetch target
+  // (none past a convolution: its weights are read by other kernels).
+  void set_prefetch(const Op &o, EpiArgs &ep) const {
+    if (!prefetch || ops.empty() || &o < ops.data() || &o >= ops.data() + ops.size()) return;
+    const long es = long(dt_size(dt));
+    for (size_t i = size_t(&o - ops.data()) + 1; i < ops.size(); ++i) {
+      const Op &n = ops[i];
+      if (n.kind == OP_GEMM) {
+        ep.pf = wptr(n.w);
+        ep.pf_bytes = n.a[1] * n.a[2] * es;
+        return;
+      }
+      if (n.kind == OP_QKV) {
+        ep.pf = wptr(n.w);
+        ep.pf_bytes = 3 * n.a[2] * n.a[2] * es;
+        return;
+      }
+      if (n.kind == OP_CONV || n.kind == OP_CONVT) return;
+    }
+  }
+
   void enqueue(const Op &o) {
     hipStream_t st = stream;
     switch (o.kind) {
@@ -747,6 +769,7 @@ struct EngineImpl {
         ep.ldr = o.a[1];
       }
       set_fold(o, ep);
+      set_prefetch(o, ep);
       ep.stream_out = o.out[0] == output && stream_out;
       if (o.splits > 1)
         hip_check(gemm_splitk(dt, dptr(o.in[0]), wptr(o.w), int(o.a[0]), int(o.a[1]), int(o.a[2]), o.splits,
@@ -768,6 +791,7 @@ struct EngineImpl {
       ep.bias = wptr(o.b);
       ep.T = T; ep.H = H; ep.hd = E / H; ep.E = E;
       set_fold(o, ep);
+      set_prefetch(o, ep);
       hip_check(gemm_nt(dt, dptr(o.in[0]), wptr(o.w), B * T, 3 * E, E, E, E, 1, 0, 0, 0, ep, -1, st), o.name.c_str());
       break;
     }
@@ -884,6 +908,11 @@ struct EngineImpl {
     // written with non-temporal stores (MUNET_HIP_STREAM_OUT=0 turns it off)
     const char *so = std::getenv("MUNET_HIP_STREAM_OUT");
     stream_out = vals[output].bytes() >= (size_t(64) << 20) && !(so && std::string(so) == "0");
+    // the weights of a layer arrive cold from HBM (the forward's other
+    // traffic evicts them between forwards): the GEMM before touches them
+    // first (MUNET_HIP_PREFETCH=0 turns it off)
+    const char *pfe = std::getenv("MUNET_HIP_PREFETCH");
+    prefetch = !(pfe && std::string(pfe) == "0");
     plan();
     if (!plan_only) {
       hip_check(hipSetDevice(device), "hipSetDevice");
@@ -1124,6 +1153,7 @@ struct EngineImpl {
       << ",\"compiled_output_shape\":" << (output >= 0 ? shape_str(vals[output].shape) : "[]")
       << ",\"arena_bytes\":" << arena_bytes << ",\"weight_bytes\":" << wbytes << ",\"ops\":" << ops.size()
       << ",\"fused_epilogues\":" << fused_epilogues << ",\"ln_folds\":" << ln_folds << ",\"stream_out\":" << (stream_out ? "true" : "false")
+      << ",\"prefetch\":" << (prefetch ? "true" : "false")
       << ",\"zero_copy_concats\":" << zero_copy_concats
       << ",\"current_memory_bytes\":" << (arena_bytes + wbytes) << ",\"peak_memory_bytes\":" << (arena_bytes + wbytes)
       << "}";

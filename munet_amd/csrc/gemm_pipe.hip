@@ -164,6 +164,7 @@ hipError_t gemm_pipe(int dt, const void *A, const void *Bt, int M, int N, int K,
   EpiArgs e = ep;
   e.xcd_gn = 2L * N >= M ? (N >= 4L * M ? 16 : 8) : 0;
   if (const char *gn = std::getenv("MUNET_HIP_XCD_GN")) e.xcd_gn = std::max(0, std::atoi(gn));
+  if (e.pf_bytes <= 0 || e.pf_bytes > (16L << 20)) e.pf = nullptr;
   if (dt == BF16) return launch_dt<BF16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, e, tile, kd, st);
   return launch_dt<F16>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, e, tile, kd, st);
 }

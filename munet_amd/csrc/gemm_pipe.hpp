@@ -950,6 +950,13 @@ __device__ __forceinline__ void dma16(const uint16_t *base, uint32_t voff, uint3
                : "memory", "m0");
 }
 
+// One wave instruction: 64 lanes x 4 bytes from base + voff into LDS bytes
+// [m0, m0 + 256).
+__device__ __forceinline__ void dma4(const void *base, uint32_t voff, uint32_t ldsaddr) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(ldsaddr)
+               : "memory", "m0");
+}
+
 template <int DT, int BM, int BN, int WGM, int WGN, int S, int EK>
 __global__ void __launch_bounds__(WGM * WGN * 64)
 gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt, int M, int N, int K, long lda,
@@ -1023,6 +1030,16 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
   u32x4 af0[FM], bf0[FN], af1[FM], bf1[FN];
   typedef PipeEpi<DT, BM, BN, WGM, WGN, EK> Epi;
   Epi epi(ep, g, M, N, m0, n0);
+  // the next GEMM's weights: this workgroup's share of their 128-byte lines,
+  // one 4-byte load each into a scratch row of LDS (lnrow, written only after
+  // the first wait, which this oldest load precedes), issued first
+  if (ep.pf) {
+    const uint32_t lines = uint32_t((ep.pf_bytes + 127) >> 7), nwg = gridDim.x * gridDim.z;
+    const uint32_t per = min((lines + nwg - 1) / nwg, 4u * G::NT), first = (blockIdx.z * gridDim.x + blockIdx.x) * per;
+    const uint32_t lsc = uint32_t(reinterpret_cast<uintptr_t>((lds_void_t *)&lnrow[0]));
+    for (uint32_t i = tid; i < per; i += G::NT)
+      if (first + i < lines) dma4(ep.pf, (first + i) << 7, lsc);
+  }
   // a fixed program's bias / residual prefetch goes after the first slabs'
   // loads, and the wait for slab 0 leaves it in flight (issued first, the
   // residual's scattered 8-byte loads held slab 0's wait back: 1.3 us of

@@ -67,6 +67,12 @@ struct EpiArgs {
   // later): the bias epilogue stores it with non-temporal stores, so it does
   // not sit in the caches for the next forward's kernels to write back
   int stream_out = 0;
+  // the next GEMM's weights (direct-to-LDS kernels): each workgroup touches
+  // its share of these bytes, one 4-byte load per 128-byte line, before its
+  // own loads, so they come from the memory-side cache instead of HBM when
+  // that GEMM starts (0 bytes or more than 16 MiB: nothing)
+  const void *pf = nullptr;
+  long pf_bytes = 0;
 };
 
 // Implicit-GEMM convolution geometry (NHWC activation, ldx = pixel stride).

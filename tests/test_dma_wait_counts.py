@@ -1,7 +1,8 @@
 """Static check of the direct-to-LDS GEMM's first wait (CPU; needs hipcc).
 
 The kernel issues the loads of slabs 0 .. S-2 with inline assembly
-(global_load_lds_dwordx4), then, for the fixed epilogue programs, the bias /
+(global_load_lds_dwordx4), after the optional 4-byte loads that touch the
+next GEMM's weights, then, for the fixed epilogue programs, the bias /
 residual prefetch, and waits with ``s_waitcnt vmcnt(N)`` for slab 0.  vmcnt
 counts outstanding vector-memory operations and they complete in order, so
 slab 0 has landed exactly when N is at most the number of vector-memory
@@ -48,7 +49,9 @@ def test_first_slab_wait_covers_slab0(src, tmp_path):
                if ln.strip() and not ln.strip().startswith((";", ".")) and not re.match(r"^\S+:$", ln.strip())]
         first_mfma = next(i for i, x in enumerate(ins) if "mfma" in x)
         pro = ins[:first_mfma]
-        dma = [i for i, x in enumerate(pro) if x.startswith("global_load_lds")]
+        # the slabs' 16-byte DMAs (the 4-byte loads issued before them touch
+        # the next GEMM's weights; being older, they only add to the wait)
+        dma = [i for i, x in enumerate(pro) if x.startswith("global_load_lds_dwordx4")]
         assert dma and len(dma) % (stages - 1) == 0, (name, len(dma))
         ndma = len(dma) // (stages - 1)
         last0 = dma[ndma - 1]  # slab 0's last load
