@@ -101,6 +101,24 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// acc + the dot product of two 16-byte chunks of 16-bit values (8 pairs), as
+// four packed two-term dot products (v_dot2c_f32_bf16 / _f16: the products
+// of 16-bit values are exact in fp32)
+template <int DT> __device__ __forceinline__ float dot8(uint4 w, uint4 x, float acc) {
+  const uint32_t wv[4] = {w.x, w.y, w.z, w.w}, xv[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if constexpr (DT == BF16) {
+      typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+      acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, wv[j]), __builtin_bit_cast(b2, xv[j]), acc, false);
+    } else {
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, wv[j]), __builtin_bit_cast(h2, xv[j]), acc, false);
+    }
+  }
+  return acc;
+}
+
 enum DecIn : int { IN_ROW = 0, IN_LN = 1, IN_ATTN = 2 };
 enum DecOut : int { OUT_ROW = 0, OUT_QKV = 1, OUT_ARGMAX = 2 };
 
@@ -165,7 +183,33 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
       const int i = tid + 256 * r;
       xq[r] = i < M * KC ? xc[i] : zero4;
     }
-  } else if constexpr (IN == IN_LN) {
+  }
+  // IN_ATTN with at most PS key blocks and at most PG groups of 4 context
+  // values per thread: every share load is issued here, ahead of the
+  // weights, instead of in trips of the input stage
+  constexpr int PG = 3, PS = 4;
+  float4 po[IN == IN_ATTN ? PG : 1][IN == IN_ATTN ? PS : 1];
+  float2 pml[IN == IN_ATTN ? PG : 1][IN == IN_ATTN ? PS : 1];
+  const int PG4 = M * K / 4;
+  const bool pre = IN == IN_ATTN && a.nsplit <= PS && PG4 <= PG * 256;
+  if constexpr (IN == IN_ATTN) {
+    if (pre) {
+      const int ns = a.nsplit;
+#pragma unroll
+      for (int u = 0; u < PG; ++u) {
+        const int g = min(tid + 256 * u, PG4 - 1), e4 = g * 4, m = e4 / K, e = e4 - m * K, h = e / a.hd,
+                  d = e - h * a.hd;
+        const long bh = long(m) * a.H + h;
+#pragma unroll
+        for (int sp = 0; sp < PS; ++sp)
+          if (sp < ns) {
+            po[u][sp] = *reinterpret_cast<const float4 *>(a.part_o + (bh * ns + sp) * a.hd + d);
+            pml[u][sp] = a.part_ml[bh * ns + sp];
+          }
+      }
+    }
+  }
+  if constexpr (IN == IN_LN) {
     const uint4 *g = static_cast<const uint4 *>(a.ln_w), *bb = static_cast<const uint4 *>(a.ln_b);
     const uint4 *xr = static_cast<const uint4 *>(a.x) + long(min(wave, M - 1)) * KC;
 #pragma unroll
@@ -244,11 +288,38 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
       }
     }
   } else {
-    // groups of 4 consecutive context values of one head, two groups per
-    // trip with every share load of both issued together
+    // groups of 4 consecutive context values of one head: from the shares
+    // loaded up front, else two groups per trip with every share load of
+    // both issued together
     T *xl = reinterpret_cast<T *>(xs);
     const int H = a.H, hd = a.hd, ns = a.nsplit, G4 = M * K / 4;
-    for (int g0 = tid; g0 < G4; g0 += 512) {
+    if (pre) {
+#pragma unroll
+      for (int u = 0; u < PG; ++u) {
+        const int g = tid + 256 * u;
+        if (g < G4) {
+          float mx = pml[u][0].x;
+#pragma unroll
+          for (int sp = 1; sp < PS; ++sp)
+            if (sp < ns) mx = fmaxf(mx, pml[u][sp].x);
+          float den = 0.f, num[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int sp = 0; sp < PS; ++sp)
+            if (sp < ns && pml[u][sp].y > 0.f) {
+              const float f = __expf(pml[u][sp].x - mx);
+              den += pml[u][sp].y * f;
+              num[0] += po[u][sp].x * f;
+              num[1] += po[u][sp].y * f;
+              num[2] += po[u][sp].z * f;
+              num[3] += po[u][sp].w * f;
+            }
+          const float r = 1.0f / den;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xl[g * 4 + e] = S::enc(num[e] * r);
+        }
+      }
+    }
+    for (int g0 = pre ? G4 : tid; g0 < G4; g0 += 512) {
       float4 o[2][kMaxSplit];
       float2 ml[2][kMaxSplit];
 #pragma unroll
@@ -300,18 +371,31 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
   for (int i = 0; i < KCH; ++i) {
     const int c = rl + 16 * (q + WS * i);
     if (c < KC) {
-      float w[CPL][C::E];
+      if constexpr (DT == F32) {
+        float w[CPL][C::E];
 #pragma unroll
-      for (int cc = 0; cc < CPL; ++cc) C::dec(wv[cc][i], w[cc]);
+        for (int cc = 0; cc < CPL; ++cc) C::dec(wv[cc][i], w[cc]);
 #pragma unroll
-      for (int m = 0; m < MB; ++m) {
-        if (m < M) {
-          float xv[C::E];
-          C::dec(xs[m * KC + c], xv);
+        for (int m = 0; m < MB; ++m) {
+          if (m < M) {
+            float xv[C::E];
+            C::dec(xs[m * KC + c], xv);
 #pragma unroll
-          for (int cc = 0; cc < CPL; ++cc)
+            for (int cc = 0; cc < CPL; ++cc)
 #pragma unroll
-            for (int e = 0; e < C::E; ++e) acc[cc][m] = fmaf(w[cc][e], xv[e], acc[cc][m]);
+              for (int e = 0; e < C::E; ++e) acc[cc][m] = fmaf(w[cc][e], xv[e], acc[cc][m]);
+          }
+        }
+      } else {
+        // one wave per SIMD runs this loop: four packed dot products per
+        // chunk and row instead of 16 decodes and 8 FMAs
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+          if (m < M) {
+            const uint4 xr = xs[m * KC + c];
+#pragma unroll
+            for (int cc = 0; cc < CPL; ++cc) acc[cc][m] = dot8<DT>(wv[cc][i], xr, acc[cc][m]);
+          }
         }
       }
     }
