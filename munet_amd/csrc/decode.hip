@@ -119,6 +119,20 @@ template <int DT> __device__ __forceinline__ float dot8(uint4 w, uint4 x, float 
   return acc;
 }
 
+// A zero chunk as a prvalue: `c ? p[i] : zero` with an lvalue zero is a
+// glvalue conditional, compiled as a load through a selected address (a
+// scratch copy of the zero, flat 4-byte loads) instead of a selected value.
+__device__ __forceinline__ uint4 z4() { return make_uint4(0, 0, 0, 0); }
+
+// Barrier that waits only for this wave's LDS operations: a __syncthreads()
+// also waits for every outstanding global load, and those complete in issue
+// order, so it would hold the input stage back until the last weight load
+// of the block had arrived.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+}
+
 enum DecIn : int { IN_ROW = 0, IN_LN = 1, IN_ATTN = 2 };
 enum DecOut : int { OUT_ROW = 0, OUT_QKV = 1, OUT_ARGMAX = 2 };
 
@@ -170,7 +184,6 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
   const int grp = WS == 1 ? wave : 0, q = WS == 1 ? 0 : wave;
   const int rl = lane & 15, row = lane >> 4;  // lane within its DPP row, row of the wave
   const int nbase = (blockIdx.x * (4 / WS) + grp) * 4 * CPL + row * CPL;  // this row's CPL columns
-  const uint4 zero4 = make_uint4(0, 0, 0, 0);
 
   // ---- 1. the input stage's loads
   constexpr int XR = 8;  // IN_ROW chunks per thread held in registers
@@ -181,7 +194,7 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
 #pragma unroll
     for (int r = 0; r < XR; ++r) {
       const int i = tid + 256 * r;
-      xq[r] = i < M * KC ? xc[i] : zero4;
+      xq[r] = i < M * KC ? xc[i] : z4();
     }
   }
   // IN_ATTN with at most PS key blocks and at most PG groups of 4 context
@@ -215,9 +228,9 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
 #pragma unroll
     for (int i = 0; i < LCH; ++i) {
       const int c = lane + 64 * i;
-      xr0[i] = c < KC ? xr[c] : zero4;
-      gq[i] = c < KC ? g[c] : zero4;
-      bq[i] = c < KC ? bb[c] : zero4;
+      xr0[i] = c < KC ? xr[c] : z4();
+      gq[i] = c < KC ? g[c] : z4();
+      bq[i] = c < KC ? bb[c] : z4();
     }
   }
 
@@ -229,18 +242,22 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
       const int c = rl + 16 * (q + WS * i);
-      wv[cc][i] = c < KC ? wr[c] : zero4;
+      wv[cc][i] = wr[min(c, KC - 1)];  // (chunks past K are never used)
     }
   }
 
   // ---- 3. the epilogue's operands (lane rl finishes row rl of its columns)
-  float bia[CPL], res[CPL];
+  // (kept raw: decoding them here would make the input stage wait for every
+  // weight load issued before them)
+  T braw[CPL], rraw[CPL];
 #pragma unroll
   for (int cc = 0; cc < CPL; ++cc) {
     const int nn = min(nbase + cc, N - 1), mm = min(rl, M - 1);
-    bia[cc] = a.bias ? S::dec(static_cast<const T *>(a.bias)[nn]) : 0.f;
-    res[cc] = RESID ? S::dec(static_cast<const T *>(a.resid)[long(mm) * N + nn]) : 0.f;
+    braw[cc] = static_cast<const T *>(a.bias)[nn];
+    rraw[cc] = RESID ? static_cast<const T *>(a.resid)[long(mm) * N + nn] : T(0);
   }
+  // every load above stays ahead of the input stage's arithmetic
+  asm volatile("" ::: "memory");
 
   // ---- 4. stage the input in LDS
   if constexpr (IN == IN_ROW) {
@@ -258,7 +275,7 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
 #pragma unroll
       for (int i = 0; i < LCH; ++i) {
         const int c = lane + 64 * i;
-        C::dec(m == wave ? xr0[i] : (c < KC ? static_cast<const uint4 *>(a.x)[long(m) * KC + c] : zero4), v[i]);
+        C::dec(m == wave ? xr0[i] : (c < KC ? static_cast<const uint4 *>(a.x)[long(m) * KC + c] : z4()), v[i]);
 #pragma unroll
         for (int e = 0; e < C::E; ++e) sum += v[i][e];
       }
@@ -359,7 +376,7 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 5. products, reductions, epilogue
   float acc[CPL][MB];
@@ -432,7 +449,8 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
       if (rl == m) mine = acc[cc][m];
     if (rl < M && n < N) {
       const int m = rl;
-      const T y = S::enc(linear_chain<DT, ACT, RESID>(mine, bia[cc], a.gelu_c, res[cc]));
+      const float bia = S::dec(braw[cc]), res = RESID ? S::dec(rraw[cc]) : 0.f;
+      const T y = S::enc(linear_chain<DT, ACT, RESID>(mine, bia, a.gelu_c, res));
       if constexpr (OUT == OUT_QKV) {
         const int which = n / a.E, e = n - which * a.E, h = e / a.hd, dd = e - h * a.hd;
         if (which == 0) {
@@ -499,12 +517,17 @@ dec_attn_kernel(const typename Store<DT>::T *__restrict__ q, const typename Stor
     return;
   }
   const int kcn = hd / C::E;
+  // q first, then K, then V: loads complete in issue order, so the scores
+  // wait only for q and K, and V arrives during the softmax
+  const T qraw = q[long(b) * H * hd + long(h) * hd + min(tid, hd - 1)];
+  asm volatile("" ::: "memory");
   // K row of this thread's key, V elements dq..dq+3 of keys jg, jg+16, ...
   const int j = j0 + tid, jg = tid >> 4, dq = (tid & 15) * 4;
   uint4 kr[KCH];
   const uint4 *krow = reinterpret_cast<const uint4 *>(kc + (long(bh) * Lmax + min(j, L - 1)) * hd);
 #pragma unroll
-  for (int c = 0; c < KCH; ++c) kr[c] = c < kcn ? krow[c] : make_uint4(0, 0, 0, 0);
+  for (int c = 0; c < KCH; ++c) kr[c] = krow[min(c, kcn - 1)];  // (chunks past hd are never used)
+  asm volatile("" ::: "memory");
   typedef typename std::conditional<sizeof(T) == 2, uint2, uint4>::type V4;
   V4 vr[kSplit / 16];
   const int dqc = min(dq, hd - 4);
@@ -513,8 +536,9 @@ dec_attn_kernel(const typename Store<DT>::T *__restrict__ q, const typename Stor
     const int jj = min(jg + 16 * t, jn - 1);
     vr[t] = *reinterpret_cast<const V4 *>(vc + (long(bh) * Lmax + j0 + jj) * hd + dqc);
   }
-  if (tid < hd) qs[tid] = S::dec(q[long(b) * H * hd + long(h) * hd + tid]);
-  __syncthreads();
+  asm volatile("" ::: "memory");
+  if (tid < hd) qs[tid] = S::dec(qraw);
+  lds_barrier();
 
   float sc = -INFINITY;
   if (tid < jn) {
@@ -531,14 +555,14 @@ dec_attn_kernel(const typename Store<DT>::T *__restrict__ q, const typename Stor
   }
   float mx = wave_max(sc);
   if (lane == 0) red[wave] = mx;
-  __syncthreads();
+  lds_barrier();
   mx = red[0];
 #pragma unroll
   for (int w = 1; w < kSplit / 64; ++w) mx = fmaxf(mx, red[w]);
   const float p = tid < jn ? S::round(__expf(sc - mx)) : 0.f;
   ps[tid] = p;
   const float l = wave_sum(p);
-  __syncthreads();
+  lds_barrier();
   if (lane == 0) red[wave] = l;
   float o[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -631,7 +655,7 @@ hipError_t dec_embed(int dt, const int32_t *ids, const void *tok, const void *po
 hipError_t dec_linear(int dt, int kind, const DecLinear &p, hipStream_t st) {
   const size_t es = dt_size(dt);
   const int ce = int(16 / es);
-  if (p.M < 1 || p.M > 16 || p.K % ce != 0 || size_t(p.M) * p.K * es > 65536) return hipErrorInvalidValue;
+  if (p.M < 1 || p.M > 16 || p.K % ce != 0 || size_t(p.M) * p.K * es > 65536 || !p.bias) return hipErrorInvalidValue;
   const int KC = p.K / ce;
   if (kind == 4 && (p.nsplit < 1 || p.nsplit > kMaxSplit || p.hd % 4 != 0 || p.K % 4 != 0)) return hipErrorInvalidValue;
   DecLinArgs a{p.x, p.w, p.bias, p.ln_w, p.ln_b, p.resid, p.part_o, p.part_ml, p.out, p.kc, p.vc, p.best, p.state,
