@@ -73,7 +73,7 @@ def test_textbook_prefill_vs_oracle(orc, dt):
     _argmax_clear(y, ref, d)
 
 
-@pytest.mark.parametrize("dt", ["bfloat16", "float32"])
+@pytest.mark.parametrize("dt", ["bfloat16", "float16", "float32"])
 def test_decode_steps_vs_oracle(orc, dt):
     """Prefill 20 tokens, then 12 greedy steps; the oracle runs the whole
     fed sequence at once (teacher forcing on the decoder's own tokens) and
