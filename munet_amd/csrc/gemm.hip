@@ -456,10 +456,12 @@ hipError_t gemm_splitk(int dt, const void *A, const void *Bt, int M, int N, int 
 // A 1x1 convolution to oC <= 8 channels (the UNet's output head: 64 -> 2) is
 // a dot product per pixel: a matrix-core tile would waste all but oC of its
 // columns.  One thread per output pixel reads its iC channels in 16-byte
-// chunks, the weights sit in LDS as floats (every lane reads the same
-// address), fp32 sums in channel order, then the epilogue chain.
+// chunks (with NCH = iC / 8 known at compile time, all of them before the
+// first product, so the chunks' latencies overlap), the weights sit in LDS as
+// floats (every lane reads the same address), fp32 sums in channel order,
+// then the epilogue chain.
 namespace {
-template <int DT>
+template <int DT, int NCH>
 __global__ void __launch_bounds__(256) conv1x1_smalln_kernel(const uint16_t *__restrict__ x,
                                                               const uint16_t *__restrict__ w, int M, int iC, long ldx,
                                                               int oC, EpiArgs ep) {
@@ -470,8 +472,7 @@ __global__ void __launch_bounds__(256) conv1x1_smalln_kernel(const uint16_t *__r
   if (m >= M) return;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   const uint16_t *row = x + long(m) * ldx;
-  for (int c0 = 0; c0 < iC; c0 += 8) {
-    const uint4 q = *reinterpret_cast<const uint4 *>(row + c0);
+  auto chunk = [&](const uint4 q, int c0) {
     const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -480,11 +481,34 @@ __global__ void __launch_bounds__(256) conv1x1_smalln_kernel(const uint16_t *__r
       for (int o = 0; o < 8; ++o)
         if (o < oC) acc[o] = __fmaf_rn(xv, wl[o * iC + c0 + e], acc[o]);
     }
+  };
+  if constexpr (NCH > 0) {
+    uint4 q[NCH];
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) q[j] = *reinterpret_cast<const uint4 *>(row + 8 * j);
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) chunk(q[j], 8 * j);
+  } else {
+    for (int c0 = 0; c0 < iC; c0 += 8) chunk(*reinterpret_cast<const uint4 *>(row + c0), c0);
   }
   float lo[4] = {acc[0], acc[1], acc[2], acc[3]}, hi[4] = {acc[4], acc[5], acc[6], acc[7]};
   epi_store4<DT>(ep, m, 0, oC, lo, 0);
   if (oC > 4) epi_store4<DT>(ep, m, 4, oC, hi, 0);
 }
+
+template <int DT>
+hipError_t conv1x1_smalln(const uint16_t *x, const uint16_t *w, int M, int iC, long ldx, int oC, const EpiArgs &ep,
+                          hipStream_t st) {
+  const dim3 grid((M + 255) / 256), block(256);
+  switch (iC) {
+  case 32: hipLaunchKernelGGL((conv1x1_smalln_kernel<DT, 4>), grid, block, 0, st, x, w, M, iC, ldx, oC, ep); break;
+  case 64: hipLaunchKernelGGL((conv1x1_smalln_kernel<DT, 8>), grid, block, 0, st, x, w, M, iC, ldx, oC, ep); break;
+  case 128: hipLaunchKernelGGL((conv1x1_smalln_kernel<DT, 16>), grid, block, 0, st, x, w, M, iC, ldx, oC, ep); break;
+  default: hipLaunchKernelGGL((conv1x1_smalln_kernel<DT, 0>), grid, block, 0, st, x, w, M, iC, ldx, oC, ep); break;
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
 
 // Implicit-GEMM convolution on an NHWC activation with OHWI-packed weights:
@@ -500,13 +524,8 @@ hipError_t conv_nhwc(int dt, const void *x, const void *w_ohwi, const ConvArgs &
   if (tile_hint < 0 && !general && (dt == F16 || dt == BF16) && cv.kH == 1 && cv.kW == 1 && cv.s == 1 && cv.p == 0 &&
       oC <= 8 && cv.iC % 8 == 0 && cv.iC <= 512 && cv.ldx % 8 == 0 && (uintptr_t)x % 16 == 0 &&
       ep.mode == EPI_ROWMAJOR && !ep.resid) {
-    if (dt == F16)
-      hipLaunchKernelGGL(conv1x1_smalln_kernel<F16>, dim3((M + 255) / 256), dim3(256), 0, st, (const uint16_t *)x,
-                         (const uint16_t *)w_ohwi, M, cv.iC, cv.ldx, oC, ep);
-    else
-      hipLaunchKernelGGL(conv1x1_smalln_kernel<BF16>, dim3((M + 255) / 256), dim3(256), 0, st, (const uint16_t *)x,
-                         (const uint16_t *)w_ohwi, M, cv.iC, cv.ldx, oC, ep);
-    return hipGetLastError();
+    return dt == F16 ? conv1x1_smalln<F16>((const uint16_t *)x, (const uint16_t *)w_ohwi, M, cv.iC, cv.ldx, oC, ep, st)
+                     : conv1x1_smalln<BF16>((const uint16_t *)x, (const uint16_t *)w_ohwi, M, cv.iC, cv.ldx, oC, ep, st);
   }
   if (tile_hint < 0 && !general && gemm_pipe_conv_ok(dt, x, w_ohwi, cv))
     return gemm_pipe_conv(dt, x, w_ohwi, cv, oC, ep, st);
