@@ -1031,12 +1031,16 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
   typedef PipeEpi<DT, BM, BN, WGM, WGN, EK> Epi;
   Epi epi(ep, g, M, N, m0, n0);
   // the next GEMM's weights: this workgroup's share of their 128-byte lines,
-  // one 4-byte load each into a scratch row of LDS (lnrow, written only after
-  // the first wait, which this oldest load precedes), issued first
+  // one 4-byte load each, issued first, into the first 256 bytes of the last
+  // stage.  Every wave waits for its own loads (the oldest) before the first
+  // barrier, and the last stage is first written (slab S - 1) and first read
+  // only after that barrier, so no wave's prefetch can land on data that
+  // another wave has written or will read (the LayerNorm row buffer, written
+  // by every wave before the barrier, could be overwritten that way).
   if (ep.pf) {
     const uint32_t lines = uint32_t((ep.pf_bytes + 127) >> 7), nwg = gridDim.x * gridDim.z;
     const uint32_t per = min((lines + nwg - 1) / nwg, 4u * G::NT), first = (blockIdx.z * gridDim.x + blockIdx.x) * per;
-    const uint32_t lsc = uint32_t(reinterpret_cast<uintptr_t>((lds_void_t *)&lnrow[0]));
+    const uint32_t lsc = lds0 + (S - 1) * STAGE;
     for (uint32_t i = tid; i < per; i += G::NT)
       if (first + i < lines) dma4(ep.pf, (first + i) << 7, lsc);
   }

@@ -108,6 +108,29 @@ def test_weight_prefetch_same_bits(orc, dtype, monkeypatch):
         assert np.array_equal(eng.run(x), y)
 
 
+def test_weight_prefetch_same_bits_headline_tiles(monkeypatch):
+    """The prefetch at the headline layer shapes (B4 T1024 d768, 12 heads,
+    FFN 3072), where the LayerNorm-folded QKV and FFN up run on the
+    eight-wave 128x288 and 256x192 tiles: every wave writes the LayerNorm row
+    statistics to LDS before the first barrier, and the prefetch loads of
+    the other waves must not land on them.  Two layers; prefetch on and off
+    give the same bits over repeated replays (the prefetch-off forward has
+    no prefetch loads at all)."""
+    from munet_amd import engine as meng
+    cfg = models.decoder_config(vocab=1000, ctx=1024, d_model=768, num_heads=12, num_layers=2, ffn=3072,
+                                dtype="bfloat16")
+    eng, p, x = _build(cfg, (4, 1024), "gpt", seed_scope="pfh")
+    assert eng.stats()["prefetch"] is True and eng.stats()["ln_folds"] == 4
+    y = eng.run(x)
+    monkeypatch.setenv("MUNET_HIP_PREFETCH", "0")
+    eng2 = meng.Engine(0).load(cfg, p).compile((4, 1024))
+    assert eng2.stats()["prefetch"] is False
+    y2 = eng2.run(x)
+    assert np.array_equal(y2, y)
+    for _ in range(4):
+        assert np.array_equal(eng.run(x), y)
+
+
 def test_cnn_full(orc):
     """small CNN fp32, batch 32, 3x32x32."""
     cfg = models.cnn_config()
