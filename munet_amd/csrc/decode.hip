@@ -85,9 +85,11 @@ __device__ __forceinline__ float linear_chain(float acc, float bias, float gelu_
 
 // Float -> unsigned key with the same order (NaN excluded by the caller);
 // the argmax key is (key << 32) | ~index: the largest value, then the first
-// index.
+// index.  -0.0 takes +0.0's key: the two compare equal, so the first index
+// of either must win, as in the prefill's argmax.
 __device__ __forceinline__ uint32_t order_key(float v) {
-  const uint32_t u = __float_as_uint(v);
+  uint32_t u = __float_as_uint(v);
+  if (u == 0x80000000u) u = 0u;
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
@@ -128,9 +130,13 @@ __device__ __forceinline__ uint4 z4() { return make_uint4(0, 0, 0, 0); }
 // also waits for every outstanding global load, and those complete in issue
 // order, so it would hold the input stage back until the last weight load
 // of the block had arrived.
+// The compiler fences keep LDS accesses on their side of the barrier (the
+// two builtins alone do not order memory for the optimiser).
 __device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
   __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 enum DecIn : int { IN_ROW = 0, IN_LN = 1, IN_ATTN = 2 };
