@@ -12,13 +12,11 @@
 // `__tensor_names__` manifest.  The same checks as the reference reject
 // anything else, plus tensor names carrying training-state tokens.
 //
-// Differences from the reference loader, both deliberate:
-//   * bf16 tensors (absent from the reference, :459-471 and :739-750) are
-//     stored as `<u2` arrays of bf16 bit patterns; MuNet has no uint16 type,
-//     so the mapping is unambiguous;
-//   * `__producer__` may be any "munet…" tag (the reference's own Python
-//     writers emit "munet_nn" and "munet_pytorch_interop", which its C++
-//     loader's exact "munet" check would refuse).
+// One deliberate difference from the reference loader: bf16 tensors (absent
+// from the reference, :459-471 and :739-750) are stored as `<u2` arrays of
+// bf16 bit patterns; MuNet has no uint16 type, so the mapping is
+// unambiguous.  `__producer__`, when present, must be exactly "munet", as the
+// reference's C++ loader requires (:997-1000).
 //
 // The file is memory-mapped; member payloads are handed to
 // mh_engine_set_param without an intermediate copy.
