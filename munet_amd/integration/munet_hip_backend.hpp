@@ -11,6 +11,13 @@
 // they throw.  query_support reports the library's own table
 // (mh_query_support): fp32 / fp16 / bf16 natively, nothing sent to the CPU.
 //
+// Against a MuNet core carrying munet_core_hip.patch (this directory), whose
+// core/backend.hpp declares BackendTransformerCapability, the class also
+// provides that capability: LayerNorm, masked_fill, the embedding gather and
+// the attention core on the device (mh_layer_norm, mh_masked_fill,
+// mh_embedding, mh_attention), which the patched op layer calls instead of
+// its host loops.  Against an unpatched core it compiles without it.
+//
 // Include with MuNet's src/ and this repository's include/ on the path.
 #pragma once
 
@@ -44,6 +51,9 @@ class HIPBackend final : public Backend,
                          public BackendElementwiseCapability,
                          public BackendBlasCapability,
                          public BackendShapeCapability,
+#ifdef MUNET_BACKEND_HAS_TRANSFORMER_CAPABILITY
+                         public BackendTransformerCapability,
+#endif
                          public BackendSpatialCapability {
  public:
   explicit HIPBackend(int index = 0, void *stream = nullptr) : stream_(stream) { check(mh_init(index)); }
@@ -59,6 +69,10 @@ class HIPBackend final : public Backend,
   const BackendShapeCapability *shape_capability() const override { return this; }
   BackendSpatialCapability *spatial_capability() override { return this; }
   const BackendSpatialCapability *spatial_capability() const override { return this; }
+#ifdef MUNET_BACKEND_HAS_TRANSFORMER_CAPABILITY
+  BackendTransformerCapability *transformer_capability() override { return this; }
+  const BackendTransformerCapability *transformer_capability() const override { return this; }
+#endif
 
   BackendSupport query_support(BackendFeature feature, DataType dtype, const Shape *) const override {
     int available = 0, policy = 0, accumulation = 0;
@@ -185,6 +199,32 @@ class HIPBackend final : public Backend,
   void upsample2d_backward(const Storage &, Storage &, int, int, int, int, int) override {
     training_only("upsample2d_backward");
   }
+
+#ifdef MUNET_BACKEND_HAS_TRANSFORMER_CAPABILITY
+  // ---- BackendTransformerCapability (munet_core_hip.patch) ---------------
+  void layer_norm(const Storage &x, const Storage &weight, const Storage &bias, Storage &out, int rows, int cols,
+                  float eps) override {
+    check(mh_layer_norm(code(x), x.data(), weight.data(), bias.data(), out.data(), rows, cols, eps, stream_));
+  }
+  void masked_fill(const Storage &x, const Storage &mask, Storage &out, size_t n, double value) override {
+    if (mask.dtype() != DataType::Int32) throw std::runtime_error("hip backend: masked_fill takes an Int32 mask");
+    check(mh_masked_fill(code(x), x.data(), static_cast<const int32_t *>(mask.data()), out.data(), n, value, stream_));
+  }
+  // an id outside the table raises the library's device error flag, read
+  // back here (a synchronisation) so the call throws the core's message
+  void embedding(const Storage &ids, const Storage &weight, Storage &out, int n, int num_embeddings,
+                 int dim) override {
+    if (ids.dtype() != DataType::Int32) throw std::runtime_error("hip backend: embedding takes Int32 ids");
+    check(mh_embedding(code(weight), static_cast<const int32_t *>(ids.data()), weight.data(), out.data(), n,
+                       num_embeddings, dim, stream_));
+    check(mh_check_device_errors());
+  }
+  void attention(const Storage &q, const Storage &k, const Storage &v, Storage &merged, int B, int H, int T,
+                 int head_dim, bool causal) override {
+    check(mh_attention(code(q), q.data(), k.data(), v.data(), merged.data(), B, H, T, head_dim, causal ? 1 : 0,
+                       stream_));
+  }
+#endif
 
  private:
   void *stream_;
