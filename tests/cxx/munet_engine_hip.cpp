@@ -35,6 +35,7 @@
 #include <string>
 #include <vector>
 
+#include "backend/plugin_loader.hpp"
 #include "core/backend.hpp"
 #include "core/grad_mode.hpp"
 #include "core/op_dispatch.hpp"
@@ -241,6 +242,8 @@ int main(int argc, char **argv) {
   try {
     const Device hip = DeviceSpec::parse("hip:0");
     std::printf("device %s %d\n", hip.to_string().c_str(), int(hip.type == DeviceType::HIP));
+    for (const auto &st : plugin::plugins_for_device("hip"))
+      std::printf("plugin %s %s %s\n", st.name.c_str(), st.device.c_str(), st.reason_code.c_str());
     for (const std::string &b : BackendManager::list_available_backends()) std::printf("available %s\n", b.c_str());
     const Device dev = DeviceSpec::parse(argc == 3 ? argv[2] : "hip:0");
     std::printf("backend %s\n", BackendManager::get(dev)->name());

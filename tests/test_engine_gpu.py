@@ -120,7 +120,7 @@ def test_weight_prefetch_same_bits_headline_tiles(monkeypatch):
     cfg = models.decoder_config(vocab=1000, ctx=1024, d_model=768, num_heads=12, num_layers=2, ffn=3072,
                                 dtype="bfloat16")
     eng, p, x = _build(cfg, (4, 1024), "gpt", seed_scope="pfh")
-    assert eng.stats()["prefetch"] is True and eng.stats()["ln_folds"] == 4
+    assert eng.stats()["prefetch"] is True and eng.stats()["ln_folds"] >= 4
     y = eng.run(x)
     monkeypatch.setenv("MUNET_HIP_PREFETCH", "0")
     eng2 = meng.Engine(0).load(cfg, p).compile((4, 1024))

@@ -36,12 +36,13 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 REF = "/root/reference"
 PATCH = os.path.join(ROOT, "munet_amd", "integration", "munet_core_hip.patch")
 BIN = os.path.join(ROOT, "oracle", "_ref", "munet_engine_hip")
-PLUGIN = os.path.join(ROOT, "munet_amd", "libmunet_backend_hip.so")
+# the directory MuNet's plugin loader searches for libmunet_backend_hip.so
+PLUGIN_DIR = os.path.join(ROOT, "munet_amd")
 
 
 def _env():
     env = dict(os.environ)
-    env["MUNET_BACKEND_PLUGIN_PATH"] = PLUGIN
+    env["MUNET_BACKEND_PLUGIN_PATH"] = PLUGIN_DIR
     env["MUNET_FAIL_FAST_ACCELERATOR_CPU_FALLBACK"] = "1"
     return env
 
@@ -72,6 +73,8 @@ def test_no_hip_backend_without_a_gpu(tmp_path):
     lines = r.stdout.splitlines()
     assert lines[0] == "device hip:0 1"
     assert "available hip" not in lines
+    # discovered by MuNet's loader, its probe refusing the machine
+    assert any(ln.startswith("plugin hip hip runtime_dependency_missing") for ln in lines), lines
     assert lines[-1] == "error Requested backend not compiled or registered."
 
 
@@ -160,6 +163,7 @@ def test_munet_engine_on_hip_device(tmp_path, orc, hip):
     out = r.stdout.splitlines()
     assert out[0] == "device hip:0 1"
     assert "available hip" in out and "backend hip" in out
+    assert "plugin hip hip ok" in out
     trips = [ln.split() for ln in out if ln.startswith("roundtrip ")]
     assert len(trips) == 4 and all(t[2:] == ["1", "1", "1"] for t in trips), trips
     assert "accelerator_cpu_fallbacks 0" in out
