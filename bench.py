@@ -25,12 +25,14 @@ and against the measured ones (the register-only MFMA loop of
 mh_measure_mfma_peak; a read-only stream over 2 GiB, mh_measure_hbm_read; a
 1 GiB device copy).
 
-CPU baseline: the C++ restatement of MuNet's CPU backend (oracle/, "port")
-in its reference-threading mode (MuNet's own split: CPUBackend::parallel_for
-inline below 1024 iterations, the fp16/bf16 fallbacks, LayerNorm and gathers
-serial), on a bounded sample of the same forward, on this host.  Where
-oracle/_ref (MuNet's CPU sources compiled by oracle/Makefile) is present, the
-same bf16 Linear is timed in it and in the port ("reference_check").
+CPU baseline: MuNet's own CPU code (oracle/_ref: the reference sources
+compiled by oracle/Makefile, kind "reference") on a bounded sample of the
+same forward on this host, with the C++ restatement of MuNet's CPU backend
+(oracle/, kind "port", in its reference-threading mode: CPUBackend::
+parallel_for inline below 1024 iterations, the fp16/bf16 fallbacks,
+LayerNorm and gathers serial) beside it as a second figure; the port alone
+where oracle/_ref is absent or MuNet cannot run the model (the UNet).  One
+bf16 Linear is also timed in both ("reference_check").
 
 "configs": BASELINE configs[0..3] (MLP, CNN, encoder block bf16 / fp16,
 UNet) at their full sizes: forward time, samples/s, MFMA / HBM fractions of
@@ -171,6 +173,21 @@ def reference_check():
                 munet_over_port=round(t_ref / t_port, 3), same_bits=bool(np.array_equal(y_ref, y_port)))
 
 
+_GPT_SAMPLE = {}
+
+
+def gpt_cpu_sample():
+    """The one-layer decoder (headline dimensions), its seeded parameters and
+    one 1024-token sequence, shared by both CPU baselines (generating the
+    parameters takes seconds)."""
+    if not _GPT_SAMPLE:
+        from munet_amd import models
+        cfg = models.decoder_config(**{**CFG, "num_layers": 1})
+        _GPT_SAMPLE.update(cfg=cfg, p=models.init_params(cfg, "gpt", scope="cpu"),
+                           ids=models.make_input(cfg, (1, T), "gpt", scope="cpu_in"))
+    return _GPT_SAMPLE["cfg"], _GPT_SAMPLE["p"], _GPT_SAMPLE["ids"]
+
+
 def cpu_baseline_gpt(rows=32):
     """Port in reference-threading mode on one 1024-token sequence: the row-
     wise ops of one decoder layer (embedding, LayerNorms, residual adds) on all
@@ -178,13 +195,11 @@ def cpu_baseline_gpt(rows=32):
     (per (b, h) block: a lower bound on MuNet's dense [B*H*T]^2 path) on all
     rows; the layer time x 12 plus ln_f and the LM head (on `rows` rows,
     scaled).  In MuNet every one of these bf16 ops is a serial fallback."""
-    from munet_amd import models, synth
+    from munet_amd import synth
     from oracle import CpuOracle
     from oracle import models as om
     orc = CpuOracle("restatement")
-    cfg = models.decoder_config(**{**CFG, "num_layers": 1})
-    p = models.init_params(cfg, "gpt", scope="cpu")
-    ids = models.make_input(cfg, (1, T), "gpt", scope="cpu_in")
+    cfg, p, ids = gpt_cpu_sample()
     dt, d, H, pre = synth.BF16, CFG["d_model"], CFG["num_heads"], "blocks.0."
     scale = T / rows
     lin = lambda x, n: orc.linear(x, p[n + ".weight"], p[n + ".bias"], dt)  # noqa: E731
@@ -225,6 +240,67 @@ def cpu_baseline_gpt(rows=32):
                 seconds_per_forward_of_one_sequence=fwd)
 
 
+def cpu_reference_gpt(rows=32, t_fit=(64, 128)):
+    """MuNet's own compiled CPU code (oracle/_ref: the reference sources built
+    by oracle/Makefile, the ops driven through ref_driver.cpp) on one
+    1024-token sequence, the same sample as the port's: the row-wise ops of
+    one decoder layer on all 1024 rows, its Linears and GELU on `rows` rows
+    scaled to 1024, the layer x 12 plus ln_f and the LM head (`rows` rows,
+    scaled).  nn::MultiHeadAttention is MuNet's dense path (the [H*T]^2 mask,
+    masked_fill, softmax and both products over every head pair): its time
+    is a*T + c*T^2 (projections linear in T, the rest quadratic), measured
+    on the first t_fit[0] and t_fit[1] tokens of the same layer, solved for
+    a and c and evaluated at T = 1024.  Every bf16 op here is one of MuNet's
+    serial fallbacks (one core)."""
+    from munet_amd import synth
+    from oracle import CpuOracle, available
+    from oracle import models as om
+    if not available("reference"):
+        return None
+    ref = CpuOracle("reference")
+    cfg, p, ids = gpt_cpu_sample()
+    dt, d, H, pre = synth.BF16, CFG["d_model"], CFG["num_heads"], "blocks.0."
+    scale = T / rows
+    lin = lambda x, n: ref.linear(x, p[n + ".weight"], p[n + ".bias"], dt)  # noqa: E731
+    tm = {}
+    x, tm["embed"] = _timed(lambda: om.decoder_embed(ref, cfg, p, ids).reshape(T, d))
+    h, tm["ln1"] = _timed(lambda: ref.layer_norm(x, p[pre + "ln1.weight"], p[pre + "ln1.bias"], dt))
+    (t1, t2), ts = t_fit, []
+    for tt in (t1, t2):
+        ts.append(_timed(lambda tt=tt: ref.mha(h[None, :tt], p, H, True, dt, prefix=pre + "attn."))[1])
+    c = (ts[1] - ts[0] * t2 / t1) / (t2 * t2 - t1 * t2)
+    a = (ts[0] - c * t1 * t1) / t1
+    mha_t = a * T + c * T * T
+    x2, tm["residual1"] = _timed(lambda: ref.add(x, h, dt))  # the add's cost does not depend on the values
+    h2, tm["ln2"] = _timed(lambda: ref.layer_norm(x2, p[pre + "ln2.weight"], p[pre + "ln2.bias"], dt))
+    f, tm["ffn_up"] = _timed(lambda: lin(h2[:rows], pre + "ff.0"))
+    g, tm["gelu"] = _timed(lambda: ref.gelu(f, dt))
+    f2, tm["ffn_down"] = _timed(lambda: lin(g, pre + "ff.2"))
+    _, tm["residual2"] = _timed(lambda: ref.add(x2, np.resize(f2, x2.shape), dt))
+    hf, tm["ln_f"] = _timed(lambda: ref.layer_norm(x2, p["ln_f.weight"], p["ln_f.bias"], dt))
+    _, tm["head"] = _timed(lambda: lin(hf[:rows], "head"))
+    sampled = ("ffn_up", "gelu", "ffn_down", "head")
+    full = {k: v * (scale if k in sampled else 1.0) for k, v in tm.items()}
+    full["attention"] = mha_t
+    layer = sum(v for k, v in full.items() if k not in ("embed", "ln_f", "head"))
+    fwd = full["embed"] + CFG["num_layers"] * layer + full["ln_f"] + full["head"]
+    measured = sum(tm.values()) + sum(ts)
+    return dict(value=T / fwd, unit="tokens/s", cores=1, kind="reference",
+                threading="MuNet's own CPU backend (every bf16 op of this model is one of its serial fallbacks)",
+                host_threads=ref_threads(), cpu_model=cpu_model(),
+                sample=(f"MuNet's compiled CPU code on one 1024-token sequence through one decoder layer: "
+                        f"nn::MultiHeadAttention (dense mask) timed on {t1} and {t2} tokens "
+                        f"({ts[0]:.2f} s, {ts[1]:.2f} s) and fitted as a*T + c*T^2 to T = 1024 "
+                        f"({mha_t:.1f} s), Linears, GELU and the LM head on {rows} rows scaled x{scale:.0f}, "
+                        f"row-wise ops on all rows ({measured:.1f} s measured: layer {layer:.1f} s, head "
+                        f"{full['head']:.1f} s as extrapolated), extrapolated to 12 layers"),
+                seconds_per_forward_of_one_sequence=fwd)
+
+
+def ref_threads():
+    return os.cpu_count() or 1
+
+
 def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -233,6 +309,20 @@ def cpu_model():
     except OSError:
         pass
     return "unknown"
+
+
+def cpu_reference_forward(cfg, params, x):
+    """Whole-forward time of MuNet's own compiled CPU code (oracle/_ref) on
+    `x`, the model composed from its ops as the oracle composes it, or None
+    when oracle/_ref is absent or MuNet cannot run the model (the UNet's
+    ConvTranspose2d and 16-bit concat have no MuNet CPU path)."""
+    from oracle import CpuOracle, available
+    from oracle import models as om
+    if not available("reference") or cfg["type"] == "UNet":
+        return None
+    ref = CpuOracle("reference")
+    _, t = _timed(lambda: om.forward(ref, cfg, params, x))
+    return t
 
 
 def cpu_port_forward(cfg, params, x, threading):
@@ -293,11 +383,19 @@ def config_line(torch, key, idx, cpu_batch, steps, warmup, with_cpu):
     if with_cpu:
         n = cpu_batch or batch
         xs = np.ascontiguousarray(x[:n])
-        t_ref = cpu_port_forward(cfg, params, xs, "reference")
-        row["cpu_baseline"] = dict(value=n / t_ref, unit="samples/s", kind="port", threading="reference",
-                                   sample=f"batch {n} of {batch}" + (" (samples are independent)" if n < batch else ""),
-                                   seconds=t_ref)
-        row["speedup_vs_cpu"] = row["samples_per_s"] / (n / t_ref)
+        sample = f"batch {n} of {batch}" + (" (samples are independent)" if n < batch else "")
+        t_port = cpu_port_forward(cfg, params, xs, "reference")
+        port = dict(value=n / t_port, unit="samples/s", kind="port", threading="reference", sample=sample,
+                    seconds=t_port)
+        t_munet = cpu_reference_forward(cfg, params, xs)
+        if t_munet is not None:
+            row["cpu_baseline"] = dict(value=n / t_munet, unit="samples/s", kind="reference",
+                                       threading="MuNet's own CPU backend", host_threads=ref_threads(),
+                                       sample=sample, seconds=t_munet, port=port)
+        else:
+            row["cpu_baseline"] = dict(port, note="MuNet's CPU code has no ConvTranspose2d and refuses 16-bit "
+                                                  "concat: the port stands in")
+        row["speedup_vs_cpu"] = row["samples_per_s"] / row["cpu_baseline"]["value"]
     eng.close()
     return row
 
@@ -463,9 +561,14 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        log("bench: timing the CPU baseline sample")
-        cpu = cpu_baseline_gpt()
-        cpu["reference_check"] = reference_check()
+        log("bench: timing the CPU baseline sample (MuNet's compiled code, then the port)")
+        port = cpu_baseline_gpt()
+        port["reference_check"] = reference_check()
+        cpu = cpu_reference_gpt()
+        if cpu is None:
+            cpu = port
+        else:
+            cpu["port"] = port
         cpu["speedup_vs_cpu"] = tokens_s / cpu["value"]
     configs = None
     if not args.no_configs:

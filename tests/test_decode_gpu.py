@@ -73,18 +73,15 @@ def test_textbook_prefill_vs_oracle(orc, dt):
     _argmax_clear(y, ref, d)
 
 
-@pytest.mark.parametrize("dt", ["bfloat16", "float16", "float32"])
-def test_decode_steps_vs_oracle(orc, dt):
-    """Prefill 20 tokens, then 12 greedy steps; the oracle runs the whole
-    fed sequence at once (teacher forcing on the decoder's own tokens) and
-    each step's logits must match its position's row."""
-    cfg = _small(dt)
-    d = synth.DTYPE_CODES[dt]
-    p = models.init_params(cfg, "gpt", scope="tbd")
-    B, T0, n = 2, 20, 12
-    prompt = models.make_input(cfg, (B, T0), "gpt", scope="tbd_in")
+def _steps_vs_oracle(orc, cfg, B, max_len, scope, T0=20, n=12):
+    """Prefill T0 tokens, then n greedy steps; the oracle runs the whole fed
+    sequence at once (teacher forcing on the decoder's own tokens) and each
+    step's logits must match its position's row."""
+    d = synth.DTYPE_CODES[cfg["dtype"]]
+    p = models.init_params(cfg, "gpt", scope=scope)
+    prompt = models.make_input(cfg, (B, T0), "gpt", scope=scope + "_in")
     eng = Engine(0).load(cfg, p).compile((B, T0))
-    dcd = Decoder(eng, B, 64)
+    dcd = Decoder(eng, B, max_len)
     pre = dcd.prefill(prompt)
     assert dcd.position() == T0
     fed = [np.argmax(dec(pre[:, -1], d), axis=-1).astype(np.int32)]
@@ -100,6 +97,37 @@ def test_decode_steps_vs_oracle(orc, dt):
     got = np.stack(logits, axis=1)  # [B, n, V]
     assert_close(got, ref[:, T0:], d, what="decode logits")
     _argmax_clear(got, ref[:, T0:], d)
+
+
+@pytest.mark.parametrize("dt", ["bfloat16", "float16", "float32"])
+def test_decode_steps_vs_oracle(orc, dt):
+    _steps_vs_oracle(orc, _small(dt), 2, 64, "tbd")
+
+
+@pytest.mark.parametrize("case", ["wide_batch_bf16", "long_cache_f32", "four_wave_f16", "four_wave_f32"])
+def test_decode_launch_shapes_vs_oracle(orc, case):
+    """The step's other launch shapes against the oracle:
+    wide_batch_bf16: batch 8 at d 512 (the 16-row kernels, and B*d > 3072,
+    so the out-projection combines the attention shares in its input-stage
+    loop instead of loading them ahead of the weights);
+    long_cache_f32: a 1280-position cache (five 256-key shares per head:
+    the same combine loop);
+    four_wave_f16 / four_wave_f32: FFN down with K past 128 chunks (its K
+    split over the block's four waves), batches 5 and 3, and a vocabulary of
+    8192 (the head's four-columns-per-row kernel)."""
+    if case == "wide_batch_bf16":
+        cfg = models.decoder_config(vocab=500, ctx=96, d_model=512, num_heads=8, num_layers=2, ffn=1024,
+                                    dtype="bfloat16", attention="textbook")
+        _steps_vs_oracle(orc, cfg, 8, 64, "dls_wb")
+    elif case == "long_cache_f32":
+        cfg = models.decoder_config(vocab=500, ctx=1280, d_model=128, num_heads=2, num_layers=2, ffn=256,
+                                    dtype="float32", attention="textbook")
+        _steps_vs_oracle(orc, cfg, 2, 1280, "dls_lc")
+    else:
+        dt = "float16" if case.endswith("f16") else "float32"
+        cfg = models.decoder_config(vocab=8192, ctx=96, d_model=128, num_heads=2, num_layers=2,
+                                    ffn=1536 if dt == "float16" else 1024, dtype=dt, attention="textbook")
+        _steps_vs_oracle(orc, cfg, 5 if dt == "float16" else 3, 64, "dls_" + case)
 
 
 def test_decode_explicit_ids_and_generate_repeat_step(orc):
