@@ -515,22 +515,21 @@ dec_attn_kernel(const typename Store<DT>::T *__restrict__ q, const typename Stor
   __shared__ float red[kSplit / 64];
   __shared__ float osh[16][65];
   const int s = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int b = bh / H, h = bh - b * H, L = state[0] + 1, ns = gridDim.x;
-  const int j0 = s * kSplit, jn = min(kSplit, L - j0);
-  if (jn <= 0) {  // past the position: an empty share
-    if (tid < hd) part_o[(long(bh) * ns + s) * hd + tid] = 0.f;
-    if (tid == 0) part_ml[long(bh) * ns + s] = make_float2(-INFINITY, 0.f);
-    return;
-  }
+  const int b = bh / H, h = bh - b * H, ns = gridDim.x;
+  const int j0 = s * kSplit;
   const int kcn = hd / C::E;
-  // q first, then K, then V: loads complete in issue order, so the scores
-  // wait only for q and K, and V arrives during the softmax
+  // The position, q, K and V are loaded together: the cache addresses are
+  // clamped to the cache's rows, not to the position, so no load waits for
+  // the position's (a block past the position loads rows it does not use).
+  // Loads complete in issue order, so the scores wait only for the
+  // position, q and K, and V arrives during the softmax.
+  const int pos = state[0];
   const T qraw = q[long(b) * H * hd + long(h) * hd + min(tid, hd - 1)];
   asm volatile("" ::: "memory");
   // K row of this thread's key, V elements dq..dq+3 of keys jg, jg+16, ...
   const int j = j0 + tid, jg = tid >> 4, dq = (tid & 15) * 4;
   uint4 kr[KCH];
-  const uint4 *krow = reinterpret_cast<const uint4 *>(kc + (long(bh) * Lmax + min(j, L - 1)) * hd);
+  const uint4 *krow = reinterpret_cast<const uint4 *>(kc + (long(bh) * Lmax + min(j, Lmax - 1)) * hd);
 #pragma unroll
   for (int c = 0; c < KCH; ++c) kr[c] = krow[min(c, kcn - 1)];  // (chunks past hd are never used)
   asm volatile("" ::: "memory");
@@ -539,10 +538,16 @@ dec_attn_kernel(const typename Store<DT>::T *__restrict__ q, const typename Stor
   const int dqc = min(dq, hd - 4);
 #pragma unroll
   for (int t = 0; t < kSplit / 16; ++t) {
-    const int jj = min(jg + 16 * t, jn - 1);
-    vr[t] = *reinterpret_cast<const V4 *>(vc + (long(bh) * Lmax + j0 + jj) * hd + dqc);
+    const int jj = min(j0 + jg + 16 * t, Lmax - 1);
+    vr[t] = *reinterpret_cast<const V4 *>(vc + (long(bh) * Lmax + jj) * hd + dqc);
   }
   asm volatile("" ::: "memory");
+  const int L = pos + 1, jn = min(kSplit, L - j0);
+  if (jn <= 0) {  // past the position: an empty share
+    if (tid < hd) part_o[(long(bh) * ns + s) * hd + tid] = 0.f;
+    if (tid == 0) part_ml[long(bh) * ns + s] = make_float2(-INFINITY, 0.f);
+    return;
+  }
   if (tid < hd) qs[tid] = S::dec(qraw);
   lds_barrier();
 
@@ -669,9 +674,16 @@ hipError_t dec_linear(int dt, int kind, const DecLinear &p, hipStream_t st) {
   // Launch shape: K up to 128 chunks per column on one wave's 16-lane row
   // (8 chunks per lane), longer K split over the block's four waves (up to
   // 512 chunks); the vocabulary head (N >= 8192, short K) takes 4 columns per
-  // row so each block amortises its LayerNorm stage over 64 columns.
+  // row so each block amortises its LayerNorm stage over 64 columns.  The
+  // out-projection, whose 16-column blocks would leave CUs idle (48 blocks
+  // at d 768), also splits K over four waves: four times the blocks, each
+  // streaming a quarter of the bytes (5.19 -> 4.72 us at d 768, B 4).  The
+  // LayerNorm-input products do not: four waves per column group slowed
+  // QKV and FFN up from 4.8 to 12.9 us (their input stage holds 8 chunks per
+  // lane for every row).
   if (KC > 512) return hipErrorInvalidValue;
-  const int ws = KC > 128 ? 4 : 1, cpl = (kind == 3 && ws == 1 && p.N >= 8192) ? 4 : 1;
+  const bool narrow = kind == 4 && (p.N + 15) / 16 < 256;
+  const int ws = (KC > 128 || narrow) ? 4 : 1, cpl = (kind == 3 && ws == 1 && p.N >= 8192) ? 4 : 1;
   const bool few = p.M <= 4;
   const int ncols = (4 / ws) * 4 * cpl;  // columns per block
   const dim3 grid(unsigned((p.N + ncols - 1) / ncols));

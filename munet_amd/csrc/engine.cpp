@@ -70,6 +70,9 @@ struct Val {
   size_t bytes() const { return numel(shape) * dt_size(dt); }
 };
 
+// OP_CONV a[9]: the layouts it reads and writes
+enum ConvLayout { CONV_NHWC = 0, CONV_NCHW_IN = 1, CONV_NCHW_OUT = 2 };
+
 enum OpKind {
   OP_GEMM, OP_QKV, OP_ATTN, OP_LN, OP_EMBED, OP_EMBED_POS, OP_CONV, OP_CONVT, OP_POOL, OP_UPSAMPLE,
   OP_UNARY, OP_BINARY, OP_SOFTMAX, OP_TO_NHWC, OP_TO_NCHW
@@ -286,6 +289,17 @@ struct EngineImpl {
   // ---------------------------------------------------------------- lowering
   int to_rowmajor4(int x, const std::string &name) {
     if (vals[x].layout != NHWC) return x;
+    // a 1x1 convolution to a few channels that produced x just now (the
+    // output head) writes NCHW itself: x becomes the NCHW value
+    if (!ops.empty()) {
+      Op &pr = ops.back();
+      if (pr.kind == OP_CONV && pr.out.size() == 1 && pr.out[0] == x && pr.a[9] == CONV_NHWC && pr.a[5] == 1 &&
+          pr.a[6] == 1 && pr.a[7] == 0 && vals[x].alias_of < 0 && conv1x1_nchw_ok(dt, int(pr.a[1]), vals[pr.in[0]].row_stride ? vals[pr.in[0]].row_stride : pr.a[1], int(pr.a[4]))) {
+        pr.a[9] = CONV_NCHW_OUT;
+        vals[x].layout = ROWMAJOR;
+        return x;
+      }
+    }
     const Shape s = vals[x].shape;
     int y = new_val(s, vals[x].dt, ROWMAJOR);
     Op &o = emit(OP_TO_NCHW, name + ".to_nchw", {x}, {y});
@@ -425,6 +439,29 @@ struct EngineImpl {
   }
 
   int conv(int x, const std::string &pfx, int iC, int oC, int k, int s, int p, int act, int out_view = -1) {
+    // a 16-bit NCHW image of at most 3 channels into a 3x3 convolution: read
+    // in place by the few-channel kernel (K = 9 C in one MFMA step), which
+    // writes the NHWC activation; no converted copy of the image
+    if (vals[x].layout != NHWC && vals[x].shape.size() == 4 && vals[x].shape[1] == iC &&
+        conv3x3_fewc_ok(dt, iC, k, s, p, oC)) {
+      const Shape xs = vals[x].shape;
+      const int y = out_view >= 0 ? out_view : new_val({xs[0], oC, xs[2], xs[3]}, dt, NHWC);
+      Op &o = emit(OP_CONV, pfx.substr(0, pfx.size() - 1), {x}, {y});
+      o.a[0] = xs[0]; o.a[1] = iC; o.a[2] = xs[2]; o.a[3] = xs[3]; o.a[4] = oC; o.a[5] = k; o.a[6] = s; o.a[7] = p;
+      o.a[8] = iC;
+      o.a[9] = CONV_NCHW_IN;
+      // OIHW rows (K = c 9 + kh 3 + kw) zero-padded to 32
+      const Param &wp = param(pfx + "weight");
+      const size_t es = dt_size(dt), row = size_t(iC) * 9 * es;
+      if (wp.host.size() != size_t(oC) * row) throw Error(pfx + "weight has the wrong size");
+      std::vector<uint8_t> w32(size_t(oC) * 32 * es, 0);
+      for (int c = 0; c < oC; ++c) std::memcpy(&w32[size_t(c) * 32 * es], &wp.host[size_t(c) * row], row);
+      o.w = upload(w32);
+      o.b = bias_or_zero(pfx + "bias", oC);
+      o.act = act;
+      if (act != ACT_NONE) ++fused_epilogues;
+      return y;
+    }
     // an NCHW input with a channel count that is not a whole 16-byte chunk
     // (the image's 3 channels) converts to NHWC padded with zero channels, so
     // the convolution takes the vectorised im2col loader
@@ -630,8 +667,6 @@ struct EngineImpl {
     for (const auto &c : m.at("channels").arr) ch.push_back(c.as_int());
     const int L = int(ch.size());
     int prev = m.at("in_channels").as_int();
-    const int chunk = dt == F32 ? 4 : 8;
-    x = to_nhwc(x, pfx + "input", (prev + chunk - 1) / chunk * chunk);
     std::vector<int> cat(L, -1);
     for (int l = 0; l < L; ++l) {
       const int c = ch[l];
@@ -817,6 +852,27 @@ struct EngineImpl {
                 o.name.c_str());
       break;
     case OP_CONV: {
+      if (o.a[9] == CONV_NCHW_IN) {
+        EpiArgs ep;
+        ep.out = dptr(o.out[0]);
+        const Val &yo = vals[o.out[0]];
+        ep.ldc = yo.row_stride ? yo.row_stride : o.a[4];
+        ep.bias = wptr(o.b);
+        ep.bias_first = 1;
+        ep.act = o.act;
+        hip_check(conv3x3_fewc(dt, dptr(o.in[0]), wptr(o.w), int(o.a[0]), int(o.a[1]), int(o.a[2]), int(o.a[3]),
+                               int(o.a[4]), ep, st),
+                  o.name.c_str());
+        break;
+      }
+      if (o.a[9] == CONV_NCHW_OUT) {
+        const Val &xi = vals[o.in[0]];
+        const long M = o.a[0] * o.a[2] * o.a[3];
+        hip_check(conv1x1_nchw(dt, dptr(o.in[0]), wptr(o.w), wptr(o.b), dptr(o.out[0]), M, int(o.a[2] * o.a[3]),
+                               int(o.a[1]), xi.row_stride ? xi.row_stride : o.a[1], int(o.a[4]), o.act, st),
+                  o.name.c_str());
+        break;
+      }
       ConvArgs cv;
       cv.B = int(o.a[0]); cv.iC = int(o.a[1]); cv.iH = int(o.a[2]); cv.iW = int(o.a[3]);
       cv.kH = cv.kW = int(o.a[5]); cv.s = int(o.a[6]); cv.p = int(o.a[7]);

@@ -128,6 +128,17 @@ hipError_t gemm_pipe_big(int dt, const void *A, const void *Bt, int M, int N, in
 bool gemm_pipe_conv_ok(int dt, const void *x, const void *w, const ConvArgs &cv);
 hipError_t gemm_pipe_conv(int dt, const void *x, const void *w, const ConvArgs &cv, int oC, const EpiArgs &ep,
                           hipStream_t st);
+// A 3x3 stride-1 pad-1 convolution of a 16-bit NCHW image with C <= 3
+// channels into an NHWC activation (w32: the OIHW rows zero-padded to 32;
+// ep: row-major output, bias_first), and a 1x1 convolution of an NHWC
+// activation (iC 32 / 64 / 128 channels, rows of ldx) to oC <= 8 channels
+// written NCHW (w: [oC][iC], bias [oC], act none or ReLU).
+bool conv3x3_fewc_ok(int dt, int C, int k, int s, int p, int oC);
+hipError_t conv3x3_fewc(int dt, const void *x, const void *w32, int B, int C, int H, int W, int oC, const EpiArgs &ep,
+                        hipStream_t st);
+bool conv1x1_nchw_ok(int dt, int iC, long ldx, int oC);
+hipError_t conv1x1_nchw(int dt, const void *x, const void *w, const void *bias, void *out, long M, int HW, int iC,
+                        long ldx, int oC, int act, hipStream_t st);
 hipError_t conv_nhwc(int dt, const void *x, const void *w_ohwi, const ConvArgs &cv, int oC, const EpiArgs &ep,
                      int tile_hint, hipStream_t st);
 // Split-K for small fp32 products (gemm.hip): the slice count for M x N x K

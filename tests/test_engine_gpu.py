@@ -266,6 +266,36 @@ def test_unet_small(orc):
     assert_close(y, ref, synth.F16, what="unet")
 
 
+def _edge_conv_config(dtype, C, oC, n_out, relu_out):
+    layers = [{"type": "Conv2d", "in_channels": C, "out_channels": oC, "kernel_size": 3, "stride": 1, "padding": 1},
+              {"type": "ReLU"},
+              {"type": "Conv2d", "in_channels": oC, "out_channels": n_out, "kernel_size": 1, "stride": 1,
+               "padding": 0}]
+    if relu_out:
+        layers.append({"type": "ReLU"})
+    return {"type": "Sequential", "dtype": dtype, "layers": layers}
+
+
+@pytest.mark.parametrize("dtype,C,oC,n_out,hw,relu_out", [
+    ("bfloat16", 3, 64, 2, (20, 20), False), ("float16", 1, 32, 8, (17, 23), True),
+    ("float16", 2, 128, 3, (16, 16), False), ("bfloat16", 3, 16, 2, (9, 30), False)])
+def test_edge_convolutions(orc, dtype, C, oC, n_out, hw, relu_out):
+    """A 16-bit image of at most 3 channels read in place by the few-channel
+    3x3 kernel (no NCHW -> NHWC copy), and a 1x1 head to at most 8 channels
+    writing NCHW itself (no NHWC -> NCHW copy; 16 input channels keep the
+    general path): ragged pixel counts, a fused ReLU on the NCHW output,
+    against the oracle."""
+    cfg = _edge_conv_config(dtype, C, oC, n_out, relu_out)
+    shape = (2, C) + hw
+    eng, p, x = _build(cfg, shape, "he", seed_scope=f"edge{C}{oC}{n_out}")
+    kinds = [o["kind"] for o in eng.plan()["ops"]]
+    assert "nchw_to_nhwc" not in kinds
+    assert ("nhwc_to_nchw" in kinds) == (oC == 16)
+    y = eng.run(x)
+    assert y.shape == (2, n_out) + hw
+    assert_close(y, omodels.forward(orc, cfg, p, x), synth.DTYPE_CODES[dtype], what=f"edge convs {C}->{oC}->{n_out}")
+
+
 def test_engine_shape_contract():
     cfg = models.mlp_config()
     eng, _p, x = _build(cfg, (64, 784), "mlp")

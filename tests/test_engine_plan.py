@@ -127,6 +127,19 @@ def test_unet_zero_copy_concat():
     assert e.out_shape == (2, 2, 32, 32)
 
 
+def test_unet_plan_reads_the_image_and_writes_the_output_in_place():
+    """A 16-bit UNet: the first convolution reads the NCHW image itself and
+    the 1x1 head writes the NCHW output itself, so no layout conversion runs."""
+    cfg = models.unet_config(channels=(64, 128, 256, 512), out_channels=2)
+    e, p = _plan(cfg, (2, 3, 64, 64))
+    kinds = [o["kind"] for o in p["ops"]]
+    assert "nchw_to_nhwc" not in kinds and "nhwc_to_nchw" not in kinds
+    assert kinds[0] == "conv2d" and kinds[-1] == "conv2d"
+    assert p["values"][p["output"]]["layout"] == 0  # row-major NCHW
+    _check_arena(p)
+    assert e.out_shape == (2, 2, 64, 64)
+
+
 def test_cnn_plan_layouts():
     cfg = models.cnn_config()
     e, p = _plan(cfg, (32, 3, 32, 32))
