@@ -179,6 +179,13 @@ def test_decoder_errors():
         Decoder(e2, 2, 16)
 
 
+def test_decode_full_config_vs_oracle(orc):
+    """Headline architecture (12 layers, d 768, H 12, V 32000, B 4): a
+    24-token prompt and 8 greedy steps against the restatement's textbook
+    decoder on the fed sequence."""
+    _steps_vs_oracle(orc, models.decoder_config(attention="textbook"), 4, 64, "tbfo", T0=24, n=8)
+
+
 def test_decode_full_config_consistent_with_prefill():
     """Headline size (12 layers, d 768, H 12, V 32000, B 4): prefill 1000
     tokens, 24 greedy steps; the engine's own forward of the 1024 fed tokens
