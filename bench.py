@@ -361,6 +361,11 @@ def config_line(torch, key, idx, cpu_batch, steps, warmup, with_cpu):
     x = models.make_input(cfg, shape, init, scope=f"bench_{key}_in")
     eng = Engine(0).load(cfg, params).compile(shape)
     eng.run(x)
+    # a forward here takes 15-600 us: at least 50 untimed and 200 timed
+    # back-to-back graph launches, so that the host's launch path is warm
+    # (the first few dozen hipGraphLaunch calls of a process cost twice the
+    # later ones) and the figure is the steady launch rate
+    steps, warmup = max(steps, 200), max(warmup, 50)
     s = timed_launches(eng, torch, steps, warmup)
     ops = eng.op_times(10)
     peak = PEAK_F32 if dt == synth.F32 else PEAK_BF16
@@ -370,7 +375,7 @@ def config_line(torch, key, idx, cpu_batch, steps, warmup, with_cpu):
     ln = [o for o in ops if o["kind"] == "layer_norm"]
     batch = shape[0]
     row = dict(baseline_config=idx, dtype=synth.DTYPE_NAMES[dt], input_shape=list(shape), ms=s * 1e3,
-               samples_per_s=batch / s,
+               timed_launches=steps, warmup_launches=warmup, samples_per_s=batch / s,
                mfma_frac=(mm_f / mm_t / peak) if mm_t else None,
                mfma_tflops=(mm_f / mm_t / 1e12) if mm_t else None,
                mfma_share_of_forward=mm_t / s,

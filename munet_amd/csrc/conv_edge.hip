@@ -4,9 +4,10 @@
 // nn::Conv2d's bias, src/nn/linear.hpp:39-64):
 //
 // * conv3x3_fewc: a 3x3, stride-1, pad-1 convolution of an NCHW image with
-//   at most 3 channels (K = 9 C <= 32: one MFMA K step) straight into an
-//   NHWC activation, bias + activation fused: the NCHW -> NHWC copy of the
-//   image and the 8-channel zero padding are never written.
+//   at most 3 channels (K = 9 C <= 32: one 16-bit MFMA K step, or two fp32
+//   groups of four) straight into an NHWC activation, bias + activation
+//   fused: the NCHW -> NHWC copy of the image and its zero channel padding
+//   are never written.
 // * conv1x1_nchw: a 1x1 convolution of an NHWC activation to at most 8
 //   channels (the output head) written straight as NCHW: the head's NHWC
 //   output and its conversion are never written.
@@ -90,6 +91,49 @@ __global__ void __launch_bounds__(256) conv3x3_fewc_kernel(const uint16_t *__res
       const uint2 pk = epi_fast_value<DT>(ep, o, bb[t], make_uint2(0, 0));
       if (p < P) *reinterpret_cast<uint2 *>(out + p * ep.ldc + 16 * t + 4 * lg) = pk;
     }
+  }
+}
+
+// The fp32 form (v_mfma_f32_16x16x4f32): lane l holds, per 16-wide K group
+// g of the 32 (9 C <= 32), the 4 values k = 16 g + 4 (l / 16) .. + 3 of its
+// pixel, and the four MFMAs of a group take element j of every lane (K
+// contracted in that permuted order); one wave per 16 pixels, the general
+// fp32 epilogue (bias added to the accumulator, the activation).
+template <int NT>
+__global__ void __launch_bounds__(256) conv3x3_fewc_f32_kernel(const float *__restrict__ x,
+                                                                const float *__restrict__ w, int B, int C, int H, int W,
+                                                                EpiArgs ep) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = lane & 15, q = lane >> 4;
+  uint4 wf[NT][2];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int g = 0; g < 2; ++g) wf[t][g] = *reinterpret_cast<const uint4 *>(w + (16 * t + li) * 32 + 16 * g + 4 * q);
+  const long P = long(B) * H * W, HW = long(H) * W;
+  const long p = (long(blockIdx.x) * 4 + wave) * 16 + li, pc = p < P ? p : P - 1;
+  const int b = int(pc / HW), hw = int(pc - b * HW), y = hw / W, xw = hw - y * W;
+  const float *img = x + long(b) * C * HW;
+  uint4 xv[2];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = 16 * g + 4 * q + j, c = k / 9, r = k - 9 * c;
+      const int yy = y + r / 3 - 1, xx = xw + (r - 3 * (r / 3)) - 1;
+      const bool in = k < 9 * C && unsigned(yy) < unsigned(H) && unsigned(xx) < unsigned(W);
+      v[j] = in ? img[c * HW + long(yy) * W + xx] : 0.f;
+    }
+    xv[g] = make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    Mfma<F32>::step(acc, wf[t][0], xv[0]);
+    Mfma<F32>::step(acc, wf[t][1], xv[1]);
+    float o[4] = {acc[0], acc[1], acc[2], acc[3]};
+    if (p < P) epi_store4<F32>(ep, int(p), 16 * t + 4 * q, 16 * NT, o, 0);
   }
 }
 
@@ -187,7 +231,7 @@ int edge_groups(const char *var, int dflt, int maxv) {
 }
 
 bool conv3x3_fewc_ok(int dt, int C, int k, int s, int p, int oC) {
-  return (dt == F16 || dt == BF16) && C >= 1 && 9 * C <= 32 && k == 3 && s == 1 && p == 1 &&
+  return (dt == F16 || dt == BF16 || dt == F32) && C >= 1 && 9 * C <= 32 && k == 3 && s == 1 && p == 1 &&
          (oC == 16 || oC == 32 || oC == 64 || oC == 128);
 }
 
@@ -198,6 +242,18 @@ hipError_t conv3x3_fewc(int dt, const void *x, const void *w32, int B, int C, in
     return hipErrorInvalidValue;
   const long P = long(B) * H * W;
   if (P <= 0) return hipSuccess;
+  if (dt == F32) {
+    const long blocks = (P + 63) / 64;
+    if (blocks > 0x7fffffffL) return hipErrorInvalidValue;
+    const float *xf = static_cast<const float *>(x), *wf = static_cast<const float *>(w32);
+    switch (oC) {
+    case 16: hipLaunchKernelGGL(conv3x3_fewc_f32_kernel<1>, dim3(unsigned(blocks)), dim3(256), 0, st, xf, wf, B, C, H, W, ep); break;
+    case 32: hipLaunchKernelGGL(conv3x3_fewc_f32_kernel<2>, dim3(unsigned(blocks)), dim3(256), 0, st, xf, wf, B, C, H, W, ep); break;
+    case 64: hipLaunchKernelGGL(conv3x3_fewc_f32_kernel<4>, dim3(unsigned(blocks)), dim3(256), 0, st, xf, wf, B, C, H, W, ep); break;
+    default: hipLaunchKernelGGL(conv3x3_fewc_f32_kernel<8>, dim3(unsigned(blocks)), dim3(256), 0, st, xf, wf, B, C, H, W, ep); break;
+    }
+    return hipGetLastError();
+  }
   static const int G = edge_groups("MUNET_HIP_FEWC_G", 1, 4);
   const long blocks = (P + 64 * G - 1) / (64 * G);
   if (blocks > 0x7fffffffL) return hipErrorInvalidValue;

@@ -247,13 +247,23 @@ struct EngineImpl {
     return reinterpret_cast<const void *>(off + 1);  // resolved after allocation (+1: never null)
   }
   // Linear weight [in, out] -> [out, in] (K-contiguous panels).
-  std::vector<uint8_t> pack_linear(const Param &p, int in_f, int out_f) const {
+  // Linear weight [in, out] -> [out, in].  hwc (C, H, W): the input is a
+  // flattened NHWC activation, its element (h W + w) C + c holding the
+  // logical feature c H W + h W + w, so the K rows are permuted to match.
+  std::vector<uint8_t> pack_linear(const Param &p, int in_f, int out_f, const int *hwc = nullptr) const {
     const size_t es = dt_size(dt);
     if (p.host.size() != size_t(in_f) * out_f * es) throw Error("linear weight has the wrong size");
+    if (hwc && long(hwc[0]) * hwc[1] * hwc[2] != in_f) throw Error("linear weight: flattened input size mismatch");
     std::vector<uint8_t> t(p.host.size());
-    for (int i = 0; i < in_f; ++i)
+    for (int i = 0; i < in_f; ++i) {
+      int src = i;
+      if (hwc) {
+        const int C = hwc[0], HW = hwc[1] * hwc[2], c = i % C, hw = i / C;
+        src = c * HW + hw;
+      }
       for (int o = 0; o < out_f; ++o)
-        std::memcpy(&t[(size_t(o) * in_f + i) * es], &p.host[(size_t(i) * out_f + o) * es], es);
+        std::memcpy(&t[(size_t(o) * in_f + i) * es], &p.host[(size_t(src) * out_f + o) * es], es);
+    }
     return t;
   }
   // Conv weight OIHW -> OHWI.
@@ -406,7 +416,7 @@ struct EngineImpl {
 
   // y = act(x W + b) (+ resid); x [..., in]; ln: a LayerNorm of x folded in
   int linear(int x, const std::string &pfx, int in_f, int out_f, bool has_bias, int act = ACT_NONE, int resid = -1,
-             int out_val = -1, const LnFold *ln = nullptr) {
+             int out_val = -1, const LnFold *ln = nullptr, const int *hwc = nullptr) {
     x = to_rowmajor4(x, pfx);
     const Shape s = vals[x].shape;
     if (s.empty() || s.back() != in_f) throw Error(pfx + ": input " + shape_str(s) + " does not end in " + std::to_string(in_f));
@@ -417,7 +427,7 @@ struct EngineImpl {
     o.a[0] = long(numel(s) / in_f);  // M
     o.a[1] = out_f;                  // N
     o.a[2] = in_f;                   // K
-    std::vector<uint8_t> packed = pack_linear(param(pfx + "weight"), in_f, out_f);
+    std::vector<uint8_t> packed = pack_linear(param(pfx + "weight"), in_f, out_f, hwc);
     if (ln) {
       if (ln->d != in_f) throw Error(pfx + ": folded LayerNorm width mismatch");
       attach_fold(o, ln, packed, in_f, out_f);
@@ -577,7 +587,25 @@ struct EngineImpl {
     const std::string t = m.at("type").as_str();
     if (t == "Sequential") {
       const auto &layers = m.at("layers").arr;
-      for (size_t i = 0; i < layers.size(); ++i) x = lower(layers[i], x, pfx + std::to_string(i) + ".");
+      for (size_t i = 0; i < layers.size(); ++i) {
+        // Flatten of a dense NHWC activation straight into a Linear: the
+        // Linear reads the activation in place as [B, H W C] with its
+        // weight's K rows permuted from the (C, H, W) order (no NCHW copy)
+        const Val &xv = vals[x];
+        if (i + 1 < layers.size() && layers[i].at("type").as_str() == "Flatten" &&
+            layers[i + 1].at("type").as_str() == "Linear" && xv.layout == NHWC && xv.row_stride == 0 &&
+            xv.shape.size() == 4) {
+          const Shape xs = xv.shape;
+          const int hwc[3] = {xs[1], xs[2], xs[3]};
+          const int flat = alias(x, {xs[0], xs[1] * xs[2] * xs[3]});
+          const json::Value &lin = layers[i + 1];
+          x = linear(flat, pfx + std::to_string(i + 1) + ".", lin.at("in_features").as_int(),
+                     lin.at("out_features").as_int(), lin.get_bool("bias", true), ACT_NONE, -1, -1, nullptr, hwc);
+          ++i;
+          continue;
+        }
+        x = lower(layers[i], x, pfx + std::to_string(i) + ".");
+      }
       return x;
     }
     if (t == "Linear")

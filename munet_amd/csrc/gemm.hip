@@ -373,6 +373,9 @@ hipError_t gemm_nt(int dt, const void *A, const void *Bt, int M, int N, int K, l
   // A folded LayerNorm (stats_out / ln_stats) exists only in the pipelined
   // kernels: such a GEMM ignores a forced general-kernel tile, and fails when
   // its operands do not suit the pipelined kernels.
+  // small fp32 products: one workgroup per 16x16 tile, K split over its waves
+  if (tile_hint < 0 && gemm_skinny_ok(dt, A, Bt, M, N, K, lda, ldb, batch, ep))
+    return gemm_skinny(A, Bt, M, N, K, lda, ldb, ep, st);
   const bool pipe = gemm_pipe_ok(dt, A, Bt, M, N, K, lda, ldb, sa, sb);
   const bool fold = ep.stats_out || ep.ln_stats;
   if (pipe && (tile_hint < 0 || tile_hint >= 200 || fold))
@@ -398,6 +401,7 @@ hipError_t gemm_nt(int dt, const void *A, const void *Bt, int M, int N, int K, l
 // (deterministic) and applies the epilogue chain.
 int splitk_count(int dt, int M, int N, int K) {
   if (dt != F32 || M <= 0 || N <= 0 || K < 512) return 1;
+  if (M <= 256 && long((M + 15) / 16) * ((N + 15) / 16) <= 1024 && K % 4 == 0 && K <= 2048) return 1;  // gemm_skinny
   const long tiles = long((M + 63) / 64) * ((N + 63) / 64);
   if (tiles >= 32) return 1;
   int best = 1;

@@ -139,6 +139,13 @@ hipError_t conv3x3_fewc(int dt, const void *x, const void *w32, int B, int C, in
 bool conv1x1_nchw_ok(int dt, int iC, long ldx, int oC);
 hipError_t conv1x1_nchw(int dt, const void *x, const void *w, const void *bias, void *out, long M, int HW, int iC,
                         long ldx, int oC, int act, hipStream_t st);
+// fp32 C = A Bt^T for M <= 256 rows and at most 1024 16x16 output tiles (the
+// small Linears): one workgroup per tile, K split over its waves, summed in
+// wave order; the general epilogue chain.
+bool gemm_skinny_ok(int dt, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch,
+                    const EpiArgs &ep);
+hipError_t gemm_skinny(const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, const EpiArgs &ep,
+                       hipStream_t st);
 hipError_t conv_nhwc(int dt, const void *x, const void *w_ohwi, const ConvArgs &cv, int oC, const EpiArgs &ep,
                      int tile_hint, hipStream_t st);
 // Split-K for small fp32 products (gemm.hip): the slice count for M x N x K

@@ -61,11 +61,11 @@ def test_mlp_full(orc):
 @pytest.mark.parametrize("sizes,batch", [((784, 256, 256, 10), 50), ((512, 200, 36), 64), ((4096, 128, 6), 32),
                                          ((1024, 72, 130), 70)])
 def test_splitk_linears(orc, sizes, batch):
-    """Small fp32 Linears with K >= 512 take split-K (fewer than 32 64x64
-    output tiles): K slices of 784/7, 512/8, 4096/64 and 1024/16 as a batched
-    partial product, then the slice sum and bias + ReLU in a second kernel;
-    ragged M and N tails and Linears below the split threshold included.
-    Against the oracle, and repeated runs give the same bits."""
+    """Small fp32 Linears: up to K = 2048 one workgroup per 16x16 output tile
+    with K split over its waves and summed in wave order (gemm_skinny: K 784,
+    512, 1024, 256, 72, 130), longer K as 64 K slices in a batched partial
+    product plus a slice-sum kernel (4096 -> 128); ragged M and N tails
+    included.  Against the oracle, and repeated runs give the same bits."""
     cfg = models.mlp_config(sizes)
     eng, p, x = _build(cfg, (batch, sizes[0]), "mlp", seed_scope=f"sk{sizes[0]}")
     y = eng.run(x)
@@ -309,19 +309,20 @@ def _edge_conv_config(dtype, C, oC, n_out, relu_out):
 
 @pytest.mark.parametrize("dtype,C,oC,n_out,hw,relu_out", [
     ("bfloat16", 3, 64, 2, (20, 20), False), ("float16", 1, 32, 8, (17, 23), True),
-    ("float16", 2, 128, 3, (16, 16), False), ("bfloat16", 3, 16, 2, (9, 30), False)])
+    ("float16", 2, 128, 3, (16, 16), False), ("bfloat16", 3, 16, 2, (9, 30), False),
+    ("float32", 3, 32, 4, (13, 11), False), ("float32", 2, 64, 2, (16, 16), True)])
 def test_edge_convolutions(orc, dtype, C, oC, n_out, hw, relu_out):
-    """A 16-bit image of at most 3 channels read in place by the few-channel
-    3x3 kernel (no NCHW -> NHWC copy), and a 1x1 head to at most 8 channels
-    writing NCHW itself (no NHWC -> NCHW copy; 16 input channels keep the
-    general path): ragged pixel counts, a fused ReLU on the NCHW output,
-    against the oracle."""
+    """An image of at most 3 channels read in place by the few-channel 3x3
+    kernel (no NCHW -> NHWC copy; fp32 too), and a 16-bit 1x1 head to at
+    most 8 channels writing NCHW itself (no NHWC -> NCHW copy; 16 input
+    channels and fp32 keep the general path): ragged pixel counts, a fused
+    ReLU on the output, against the oracle."""
     cfg = _edge_conv_config(dtype, C, oC, n_out, relu_out)
     shape = (2, C) + hw
     eng, p, x = _build(cfg, shape, "he", seed_scope=f"edge{C}{oC}{n_out}")
     kinds = [o["kind"] for o in eng.plan()["ops"]]
     assert "nchw_to_nhwc" not in kinds
-    assert ("nhwc_to_nchw" in kinds) == (oC == 16)
+    assert ("nhwc_to_nchw" in kinds) == (oC == 16 or dtype == "float32")
     y = eng.run(x)
     assert y.shape == (2, n_out) + hw
     assert_close(y, omodels.forward(orc, cfg, p, x), synth.DTYPE_CODES[dtype], what=f"edge convs {C}->{oC}->{n_out}")

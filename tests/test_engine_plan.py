@@ -141,10 +141,14 @@ def test_unet_plan_reads_the_image_and_writes_the_output_in_place():
 
 
 def test_cnn_plan_layouts():
+    """The CNN runs NHWC end to end with no layout copies: the first
+    convolution reads the NCHW image in place, and the Flatten feeding the
+    first Linear is that Linear reading the NHWC activation with permuted
+    weight rows."""
     cfg = models.cnn_config()
     e, p = _plan(cfg, (32, 3, 32, 32))
     kinds = [o["kind"] for o in p["ops"]]
-    assert kinds[0] == "nchw_to_nhwc" and "nhwc_to_nchw" in kinds
+    assert "nchw_to_nhwc" not in kinds and "nhwc_to_nchw" not in kinds
     assert kinds.count("conv2d") == 2 and kinds.count("max_pool2d") == 2
     _check_arena(p)
     assert e.out_shape == (32, 10)
