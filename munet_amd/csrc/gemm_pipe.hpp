@@ -950,6 +950,14 @@ __device__ __forceinline__ void dma16(const uint16_t *base, uint32_t voff, uint3
                : "memory", "m0");
 }
 
+// One wave instruction: 64 lanes x 16 bytes through a buffer resource into
+// LDS bytes [m0, m0 + 1024): a lane whose offset lies past the resource's end
+// writes zeros (the convolution's padding taps).
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t res, uint32_t voff, uint32_t ldsaddr) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(res), "s"(ldsaddr)
+               : "memory", "m0");
+}
+
 // One wave instruction: 64 lanes x 4 bytes from base + voff into LDS bytes
 // [m0, m0 + 256).
 __device__ __forceinline__ void dma4(const void *base, uint32_t voff, uint32_t ldsaddr) {
@@ -957,10 +965,18 @@ __device__ __forceinline__ void dma4(const void *base, uint32_t voff, uint32_t l
                : "memory", "m0");
 }
 
-template <int DT, int BM, int BN, int WGM, int WGN, int S, int EK>
+// CONV: implicit-GEMM convolution (M = output pixels, N = oC, K = kH kW iC,
+// iC % 64 == 0: slab kt is tap kt / (iC / 64) and 64 consecutive channels)
+// on an NHWC activation A with OHWI weights Bt.  Each lane keeps, per A row
+// it loads, the byte offset of the row's tap (0, 0) chunk and a bit mask of
+// its taps inside the image; a slab's A blocks go straight to LDS through a
+// buffer resource over the activation, padding taps reading an offset past
+// its end (zeros), so the convolution runs the S-stage pipeline of the
+// products.
+template <int DT, int BM, int BN, int WGM, int WGN, int S, int EK, bool CONV = false>
 __global__ void __launch_bounds__(WGM * WGN * 64)
 gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt, int M, int N, int K, long lda,
-                long ldb, long sa, long sb, long sc, EpiArgs ep) {
+                long ldb, long sa, long sb, long sc, EpiArgs ep, ConvArgs cv = ConvArgs{}) {
   typedef PipeGeom<BM, BN, WGM, WGN> G;
   constexpr int NW = G::NW, FM = G::FM, FN = G::FN, BK = 64;
   // 8-row DMA blocks per wave per slab.  EVEN: every wave takes the same
@@ -975,6 +991,7 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
   constexpr int NDMA = EVEN ? ABLK + BBLK : (NB + NW - 1) / NW;
   static_assert(BM % 8 == 0 && BN % 8 == 0, "DMA blocks");
   static_assert(S >= 2 && NDMA * (S - 1) < 64, "stages");
+  static_assert(!CONV || EVEN, "convolution tiles split their DMA blocks evenly");
   constexpr uint32_t STAGE = (BM + BN) * 128;  // bytes per stage
   __shared__ u32x4 lds[S][(BM + BN) * 8];
   __shared__ float2 lnrow[BM];  // folded LayerNorm: row (mean, rstd)
@@ -996,6 +1013,33 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
   uint32_t aoff[ABLK], boff[BBLK];
   uint32_t uoff[EVEN ? 1 : NDMA];
   const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>((lds_void_t *)&lds[0][0]));
+  int32_t cvoff[CONV ? ABLK : 1];
+  uint32_t cvmask[CONV ? ABLK : 1];
+  if constexpr (CONV) {
+#pragma unroll
+    for (int i = 0; i < ABLK; ++i) {
+      const int m = min(m0 + (wave * ABLK + i) * 8 + lr, M - 1);
+      const int ow = m % cv.oW, t2 = m / cv.oW, oh = t2 % cv.oH, b = t2 / cv.oH;
+      const int ih0 = oh * cv.s - cv.p, iw0 = ow * cv.s - cv.p;
+      cvoff[i] = ((b * cv.iH + ih0) * cv.iW + iw0) * int(cv.ldx) * 2 + lc * 16;
+      uint32_t msk = 0;
+      for (int kh = 0; kh < cv.kH; ++kh)
+        for (int kw = 0; kw < cv.kW; ++kw)
+          if (unsigned(ih0 + kh) < unsigned(cv.iH) && unsigned(iw0 + kw) < unsigned(cv.iW)) msk |= 1u << (kh * cv.kW + kw);
+      cvmask[i] = msk;
+    }
+  }
+  const __amdgpu_buffer_rsrc_t xres =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(A), 0, CONV ? cv.B * cv.iH * cv.iW * int(cv.ldx) * 2 : 0,
+                                        0x00020000);
+  const int cblk = CONV ? cv.iC / 64 : 1;  // 64-channel blocks per tap
+  // byte offset of slab kt's tap and channel block from a row's tap (0, 0)
+  // chunk, and the slab's tap (wave-uniform)
+  auto conv_slab = [&](int kt, int &tap) -> int {
+    tap = kt / cblk;
+    const int cic = (kt - tap * cblk) * 64, kh = tap / cv.kW, kw = tap - kh * cv.kW;
+    return ((kh * cv.iW + kw) * int(cv.ldx) + cic) * 2;
+  };
   if constexpr (EVEN) {
 #pragma unroll
     for (int i = 0; i < ABLK; ++i)
@@ -1020,9 +1064,17 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
     if constexpr (!EVEN) {                                                                         \
       const int b_ = min(wave + (T) * NW, NB - 1);                                                 \
       dma16((b_ < NBA ? A : Bt) + (KT_) * BK, uoff[(T) % NDMA], lds0 + (ST) * STAGE + b_ * 1024);  \
-    } else if ((T) < ABLK)                                                                         \
-      dma16(A + (KT_) * BK, aoff[(T) % ABLK], wa + (ST) * STAGE + ((T) % ABLK) * 1024);            \
-    else                                                                                           \
+    } else if ((T) < ABLK) {                                                                       \
+      if constexpr (CONV) {                                                                        \
+        int tap_;                                                                                  \
+        const int so_ = conv_slab((KT_), tap_);                                                    \
+        const uint32_t v_ = ((cvmask[(T) % ABLK] >> tap_) & 1u) ? uint32_t(cvoff[(T) % ABLK] + so_) \
+                                                                : 0x80000000u;                     \
+        dma16_buf(xres, v_, wa + (ST) * STAGE + ((T) % ABLK) * 1024);                              \
+      } else {                                                                                     \
+        dma16(A + (KT_) * BK, aoff[(T) % ABLK], wa + (ST) * STAGE + ((T) % ABLK) * 1024);          \
+      }                                                                                            \
+    } else                                                                                         \
       dma16(Bt + (KT_) * BK, boff[((T) - ABLK) % BBLK], wb + (ST) * STAGE + (((T) - ABLK) % BBLK) * 1024); \
   }
 
@@ -1179,7 +1231,16 @@ void launch_dma(const void *A, const void *Bt, int M, int N, int K, long lda, lo
                 long sc, const EpiArgs &ep, hipStream_t st) {
   const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   hipLaunchKernelGGL((gemm_dma_kernel<DT, BM, BN, WGM, WGN, S, EK>), dim3(tiles, 1, batch), dim3(WGM * WGN * 64), 0,
-                     st, (const uint16_t *)A, (const uint16_t *)Bt, M, N, K, lda, ldb, sa, sb, sc, ep);
+                     st, (const uint16_t *)A, (const uint16_t *)Bt, M, N, K, lda, ldb, sa, sb, sc, ep, ConvArgs{});
+}
+
+// implicit-GEMM convolution on the direct-to-LDS kernel (x NHWC, w OHWI)
+template <int DT, int BM, int BN, int WGM, int WGN, int S>
+void launch_dma_conv(const void *x, const void *w, const ConvArgs &cv, int oC, const EpiArgs &ep, hipStream_t st) {
+  const int M = cv.B * cv.oH * cv.oW, K = cv.kH * cv.kW * cv.iC;
+  const int tiles = ((M + BM - 1) / BM) * ((oC + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm_dma_kernel<DT, BM, BN, WGM, WGN, S, PK_GENERAL, true>), dim3(tiles), dim3(WGM * WGN * 64),
+                     0, st, (const uint16_t *)x, (const uint16_t *)w, M, oC, K, 0L, long(K), 0L, 0L, 0L, ep, cv);
 }
 
 }  // namespace

@@ -12,17 +12,27 @@ namespace mh {
 
 namespace {
 
-// Block tile: 64x64 (four waves of 32x32, 100 VGPRs, so several workgroups
-// per CU hide the im2col gathers).  Measured on MI355X over the UNet's 13
-// convolution shapes (131072 x 64 .. 2048 x 512 output pixels x channels, K
-// 576 .. 4608): fastest or within 2% of the fastest on all but the small
-// grids; 128x64 is up to 40% slower on the deep levels, 128x128 up to 90%
-// slower.  Where 64x64 leaves at most one tile per CU and K <= 2304 (the
-// stride-2 convolutions of the deep levels), 32x64 (four waves of 16x32)
-// doubles the workgroups: 2048 x 256 x 2304 18.3 -> 14.2 us, 8192 x 128 x
-// 1152 12.8 -> 11.5 us; with K = 4608 it was 11% slower.
+// Block tile and kernel per shape, measured on MI355X over the UNet's
+// convolutions (kernel trace, fp16, B 8):
+//  * the 128x128 maps (M = 131072 output pixels): the register-staged 64x64
+//    (four waves of 32x32, 100 VGPRs, several workgroups per CU hiding the
+//    im2col gathers) is fastest (enc0.1 26.3 us, dec0.0 40.1, dec0.1 28.5;
+//    the direct-to-LDS tiles 30.8-68 us);
+//  * 64x64 maps with N >= 128 (M = 32768): direct-to-LDS 64x128 with three
+//    stages (enc1.1 22.4 -> 21.0, dec1.0 37.6 -> 33.8, dec1.1 26.7 -> 25.5);
+//  * the deeper maps (M < 16384), where a 64x64 grid leaves about one tile
+//    per CU and each K step of the register-staged kernel waits a memory
+//    latency: the direct-to-LDS pipeline with four stages, 64x64
+//    (enc3.1 35.6 -> 27.1, enc3.0 19.0 -> 17.5, enc2.1 22.4 -> 22.1), or
+//    32x64 when 64x64 leaves fewer than 256 tiles (down2 18.5 -> 13.2);
+//  * otherwise the register-staged 32x64 where 64x64 leaves at most one tile
+//    per CU and K <= 2304, else 64x64.
+// Every tile gives the same bits (test_conv_pipelined_kernel_bits).
 int conv_tile(int M, int N, int K) {
   const long t64 = long((M + 63) / 64) * ((N + 63) / 64);
+  if (M >= 65536) return 2;
+  if (M >= 16384 && N >= 128) return 8;
+  if (M < 16384) return t64 < 256 ? 6 : 5;
   return t64 <= 256 && K <= 2304 ? 3 : 2;
 }
 
@@ -31,11 +41,17 @@ hipError_t run(const void *x, const void *w, const ConvArgs &cv, int oC, const E
   const int M = cv.B * cv.oH * cv.oW;
   int tile = conv_tile(M, oC, cv.kH * cv.kW * cv.iC);
   // tuning override, read per call: MUNET_HIP_CONV_TILE = 0 128x128, 1 128x64, 2 64x64, 3 32x64, 4 64x32
+  // (register-staged), 5 64x64 four stages, 6 32x64 four stages, 7 64x64 three stages, 8 64x128 three
+  // stages (direct-to-LDS)
   if (const char *e = std::getenv("MUNET_HIP_CONV_TILE")) {
     const int t = std::atoi(e);
-    if (t >= 0 && t <= 4) tile = t;
+    if (t >= 0 && t <= 8) tile = t;
   }
   switch (tile) {
+  case 5: launch_dma_conv<DT, 64, 64, 2, 2, 4>(x, w, cv, oC, ep, st); break;
+  case 6: launch_dma_conv<DT, 32, 64, 2, 2, 4>(x, w, cv, oC, ep, st); break;
+  case 7: launch_dma_conv<DT, 64, 64, 2, 2, 3>(x, w, cv, oC, ep, st); break;
+  case 8: launch_dma_conv<DT, 64, 128, 2, 2, 3>(x, w, cv, oC, ep, st); break;
   case 0: launch_conv<DT, 128, 128, 2, 2>(x, w, cv, oC, ep, st); break;
   case 1: launch_conv<DT, 128, 64, 2, 2>(x, w, cv, oC, ep, st); break;
   case 3: launch_conv<DT, 32, 64, 2, 2>(x, w, cv, oC, ep, st); break;

@@ -339,12 +339,14 @@ def test_conv2d(hip, orc, dt, B, iC, H, W, oC, k, s, p):
                                                    (3, 256, 9, 7, 64, 3, 2, 1, 1), (2, 64, 16, 16, 16, 1, 1, 0, 0),
                                                    (1, 64, 5, 6, 40, 5, 1, 2, 1)])
 def test_conv_pipelined_kernel_bits(hip, dt, B, iC, H, W, oC, k, s, p, act, monkeypatch):
-    """The pipelined implicit-GEMM convolution (iC % 64 == 0) gives the bits
+    """The pipelined implicit-GEMM convolutions (iC % 64 == 0) give the bits
     of the general implicit-GEMM kernel (same MFMA sequence, bias added to the
     fp32 accumulator, one rounding, ReLU) on NHWC inputs, over the block
-    tiles (the automatic choice, and the 32x64 / 64x32 tiles forced),
-    strides, 1x1 and 5x5 filters, ragged pixel counts and padding on every
-    side."""
+    tiles (the automatic choice, the register-staged 32x64 / 64x32 tiles and
+    the direct-to-LDS 64x64 four / three stages, 32x64 four stages and
+    64x128 three stages forced), strides, 1x1 and 5x5 filters, ragged pixel
+    counts and padding on every side (the direct-to-LDS loads of padding
+    taps read past the buffer resource and land as zeros)."""
     x = rand((B, H, W, iC), dt, 120)
     w = rand((oC, iC, k, k), dt, 121, np.sqrt(2.0 / (iC * k * k)))
     b = rand((oC,), dt, 122, 0.1)
@@ -353,7 +355,8 @@ def test_conv_pipelined_kernel_bits(hip, dt, B, iC, H, W, oC, k, s, p, act, monk
     hip.pack_conv_weight(to_device(w, dt), wo, oC, iC, k, k)
     xd, bd = to_device(x, dt), to_device(b, dt)
     outs = {}
-    for name in ("pipelined", "tile3", "tile4", "general"):
+    tiles = ("pipelined", "tile3", "tile4", "tile5", "tile6", "tile7", "tile8")
+    for name in tiles + ("general",):
         monkeypatch.delenv("MUNET_HIP_CONV_KERNEL", raising=False)
         monkeypatch.delenv("MUNET_HIP_CONV_TILE", raising=False)
         if name == "general":
@@ -365,7 +368,7 @@ def test_conv_pipelined_kernel_bits(hip, dt, B, iC, H, W, oC, k, s, p, act, monk
         hip.synchronize()
         outs[name] = to_host(out, dt)
     assert np.all(np.isfinite(dec(outs["pipelined"], dt)))
-    for name in ("pipelined", "tile3", "tile4"):
+    for name in tiles:
         assert np.array_equal(outs[name], outs["general"]), f"{name} conv differs from the general kernel"
 
 
