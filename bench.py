@@ -119,6 +119,31 @@ def probe(eng, torch, name):
     log(f"probe: {name} ({op}) x5 after a forward, copy {COPY_BYTES} bytes")
 
 
+def probe_config(torch, key, op):
+    """--probe for a BASELINE config (--config KEY --probe OP, OP an op name
+    of its plan): one forward, then 5 replayed launches of that op, then the
+    calibration copy, as probe() does for the decoder."""
+    from munet_amd import models
+    from munet_amd.engine import Engine
+    w = models.baseline_workloads()[key]
+    cfg, shape, init = w["config"], w["input_shape"], w["init"]
+    eng = Engine(0).load(cfg, models.init_params(cfg, init, scope=f"bench_{key}")).compile(shape)
+    eng.run(models.make_input(cfg, shape, init, scope=f"bench_{key}_in"))
+    names = [o["name"] for o in eng.plan()["ops"]]
+    if op not in names:
+        sys.exit(f"bench: no op {op!r} in the {key} plan (one of {names})")
+    torch.cuda.synchronize()
+    eng.op_times(5, only=op)
+    torch.cuda.synchronize()
+    a = torch.ones(COPY_BYTES // 2, device="cuda", dtype=torch.bfloat16)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    log(f"probe: {key} {op} x5 after a forward, copy {COPY_BYTES} bytes")
+    eng.close()
+
+
 def measured_traffic(name):
     """HBM bytes per launch of `name` from its committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE summary (profiles/<name>_traffic.md), or None."""
@@ -451,7 +476,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip BASELINE configs 0-3")
-    ap.add_argument("--probe", default=None, help="run one kernel of the forward for rocprofv3 --pmc and exit")
+    ap.add_argument("--probe", default=None, help="run one kernel of the forward for rocprofv3 --pmc and exit "
+                    "(with --config: an op name of that config's plan)")
     ap.add_argument("--config", default=None,
                     help="measure only this BASELINE config (mlp, cnn, encoder_bf16, encoder_fp16, unet, decode), "
                          "print its JSON row and exit (for profiling one config)")
@@ -471,6 +497,9 @@ def main():
 
     if args.config:
         keys = {k: (i, c) for k, i, c in CONFIG_ROWS}
+        if args.probe and args.config in keys:
+            probe_config(torch, args.config, args.probe)
+            return
         if args.config == "decode":
             row = decode_line()
         elif args.config in keys:
@@ -555,9 +584,21 @@ def main():
     kernels = {n: dict(avg_us=round(r["t"] * 1e6, 2), per_forward=r["count"],
                        tflops=round(r["flops"] / r["t"] / 1e12, 1) if r["flops"] else None,
                        gbs=round(r["bytes"] / r["t"] / 1e9, 1) if r["bytes"] else None) for n, r in iso.items()}
+    # memory-bound ops carry their GB/s and HBM fraction both inside the
+    # forward (prefix-graph differences) and alone
+    for n, r in kernels.items():
+        if r["gbs"]:
+            r["hbm_frac"] = round(r["gbs"] * 1e9 / PEAK_HBM, 3)
     in_fwd = {n: dict(avg_us=round(r["t"] * 1e6, 2), per_forward=r["count"], us_per_forward=round(r["per_fwd"] * 1e6, 1),
-                      tflops=round(r["flops"] / r["t"] / 1e12, 1) if r["flops"] and r["t"] > 0 else None)
+                      tflops=round(r["flops"] / r["t"] / 1e12, 1) if r["flops"] and r["t"] > 0 else None,
+                      gbs=round(r["bytes"] / r["t"] / 1e9, 1) if r["bytes"] and r["t"] > 0 else None,
+                      hbm_frac=round(r["bytes"] / r["t"] / PEAK_HBM, 3) if r["bytes"] and r["t"] > 0 else None)
               for n, r in fwd_rows.items()}
+    # the first op's prefix difference is the one-op graph's whole replay
+    # time, graph launch overhead included
+    first = op_category(eng.plan()["ops"][0])
+    if first in in_fwd:
+        in_fwd[first]["note"] = "first op of the forward: includes the graph launch overhead"
     gemm_f = [r for r in fwd_rows.values() if r["flops"] and r["name"] != "attention_causal"]
     gemm_frac_fwd = sum(r["flops"] * r["count"] for r in gemm_f) / sum(r["per_fwd"] for r in gemm_f) / PEAK_BF16
     gemm_i = [r for r in iso.values() if r["flops"] and r["name"] != "attention_causal"]
@@ -603,6 +644,8 @@ def main():
         "gemm_mfma_frac": gemm_frac_fwd,
         "gemm_mfma_frac_isolated": gemm_frac_iso,
         "layernorm_hbm_frac": (ln["bytes"] / ln["t"]) / PEAK_HBM,
+        "layernorm_hbm_frac_in_forward": (ln["bytes"] / fwd_rows["layer_norm"]["t"]) / PEAK_HBM
+        if fwd_rows["layer_norm"]["t"] > 0 else None,
         "layernorm_frac_of_measured_read": (ln["bytes"] / ln["t"]) / peak_read,
         "measured_peaks": {"mfma_bf16_tflops": peak_mfma / 1e12, "hbm_read_gbs": peak_read / 1e9,
                            "hbm_copy_gbs": peak_copy / 1e9},

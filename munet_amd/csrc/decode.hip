@@ -93,16 +93,6 @@ __device__ __forceinline__ uint32_t order_key(float v) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Sum over the 16 lanes of a DPP row (every lane of the row gets it):
-// rotate by 8 and 4 within the row, then the two quad swaps.
-__device__ __forceinline__ float row16_sum(float v) {
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false));  // row_ror:8
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xf, 0xf, false));  // row_ror:4
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false));   // quad [2,3,0,1]
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xb1, 0xf, 0xf, false));   // quad [1,0,3,2]
-  return v;
-}
-
 // acc + the dot product of two 16-byte chunks of 16-bit values (8 pairs), as
 // four packed two-term dot products (v_dot2c_f32_bf16 / _f16: the products
 // of 16-bit values are exact in fp32)

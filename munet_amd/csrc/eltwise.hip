@@ -298,6 +298,65 @@ embedding_vec_kernel(const int32_t *__restrict__ ids, const typename Store<DT>::
   }
 }
 
+// 16-bit rows of D <= 128*NC values, D % 8 == 0: one 16-lane DPP row of
+// lanes per row (four rows per wave), NC 16-byte chunks per lane; the
+// position row's loads go out beside the id's, the table row's once the id
+// has arrived, and the statistics reduce within the DPP row (row16_sum).
+template <int DT, int NC>
+__global__ void __launch_bounds__(256)
+embedding_row16_kernel(const int32_t *__restrict__ ids, const uint16_t *__restrict__ w,
+                       const uint16_t *__restrict__ pos, uint16_t *__restrict__ out, int n, int V, int D, int T,
+                       int *__restrict__ err, float *__restrict__ stats) {
+  const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int rl = threadIdx.x & 15;
+  if (row >= n) return;  // the whole DPP row leaves together
+  const int CH = D / 8;
+  uint4 pq[NC], tq[NC];
+  const uint4 *prow = pos ? reinterpret_cast<const uint4 *>(pos + long(row % T) * D) : nullptr;
+  const int tok = ids[row];
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const int c = rl + 16 * k;
+    pq[k] = prow && c < CH ? prow[c] : make_uint4(0, 0, 0, 0);
+  }
+  const bool ok = tok >= 0 && tok < V;
+  if (!ok && rl == 0) atomicOr(err, 1);
+  const uint4 *src = reinterpret_cast<const uint4 *>(w + long(ok ? tok : 0) * D);
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const int c = rl + 16 * k;
+    tq[k] = ok && c < CH ? src[c] : make_uint4(0, 0, 0, 0);
+  }
+  uint4 *dst = reinterpret_cast<uint4 *>(out + long(row) * D);
+  float r[NC][8];
+  float rsum = 0.f;
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const int c = rl + 16 * k;
+    float v[8], p[8];
+    dec8<DT>(tq[k], v);
+    dec8<DT>(pq[k], p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      r[k][e] = Store<DT>::round(prow ? p[e] + v[e] : v[e]);
+      if (c < CH) rsum += r[k][e];
+    }
+    if (c < CH) dst[c] = enc8<DT>(r[k]);
+  }
+  if (stats) {
+    // the row's LayerNorm statistics over the stored (rounded) values
+    const float mu = row16_sum(rsum) / float(D);
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < NC; ++k)
+      if (rl + 16 * k < CH)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q += (r[k][e] - mu) * (r[k][e] - mu);
+    q = row16_sum(q);
+    if (rl == 0) *reinterpret_cast<float2 *>(stats + 2 * long(row)) = make_float2(mu, q);
+  }
+}
+
 // One wave per row: first index of the maximum (NaN never wins).
 template <int DT>
 __global__ void __launch_bounds__(256)
@@ -480,6 +539,22 @@ hipError_t embedding(int dt, const int32_t *ids, const void *w, const void *pos,
   const bool vec = D % 4 == 0 && D <= 1024 && (uintptr_t)w % (4 * es) == 0 && (uintptr_t)out % (4 * es) == 0 &&
                    (uintptr_t)pos % (4 * es) == 0;
   if (stats && !vec) return hipErrorInvalidValue;  // LayerNorm statistics: vector path only
+  if (dt != F32 && D % 8 == 0 && D <= 1024 && (uintptr_t)w % 16 == 0 && (uintptr_t)out % 16 == 0 &&
+      (uintptr_t)pos % 16 == 0) {
+    const dim3 g16((n + 15) / 16);
+    const uint16_t *W = (const uint16_t *)w, *P = (const uint16_t *)pos;
+    uint16_t *O = (uint16_t *)out;
+#define MH_EMB16(DTV, NC) \
+  case NC: hipLaunchKernelGGL((embedding_row16_kernel<DTV, NC>), g16, dim3(256), 0, st, ids, W, P, O, n, V, D, T, err, stats); break
+#define MH_EMB16_NC(DTV) \
+  switch ((D / 8 + 15) / 16) { MH_EMB16(DTV, 1); MH_EMB16(DTV, 2); MH_EMB16(DTV, 3); MH_EMB16(DTV, 4); \
+                               MH_EMB16(DTV, 5); MH_EMB16(DTV, 6); MH_EMB16(DTV, 7); MH_EMB16(DTV, 8); \
+                               default: return hipErrorInvalidValue; }
+    if (dt == F16) MH_EMB16_NC(F16) else MH_EMB16_NC(BF16)
+#undef MH_EMB16_NC
+#undef MH_EMB16
+    return hipGetLastError();
+  }
   if (vec) {
 #define MH_EMB(DTV, T, NV)                                                                                      \
   hipLaunchKernelGGL((embedding_vec_kernel<DTV, NV>), grid, dim3(256), 0, st, ids, (const T *)w, (const T *)pos, \

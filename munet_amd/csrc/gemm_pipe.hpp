@@ -1032,13 +1032,26 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
   const __amdgpu_buffer_rsrc_t xres =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(A), 0, CONV ? cv.B * cv.iH * cv.iW * int(cv.ldx) * 2 : 0,
                                         0x00020000);
-  const int cblk = CONV ? cv.iC / 64 : 1;  // 64-channel blocks per tap
-  // byte offset of slab kt's tap and channel block from a row's tap (0, 0)
-  // chunk, and the slab's tap (wave-uniform)
-  auto conv_slab = [&](int kt, int &tap) -> int {
-    tap = kt / cblk;
-    const int cic = (kt - tap * cblk) * 64, kh = tap / cv.kW, kw = tap - kh * cv.kW;
-    return ((kh * cv.iW + kw) * int(cv.ldx) + cic) * 2;
+  const int KT = K / BK;
+  // CONV: the slab the next DMAs fetch (wave-uniform): its index, tap (kh,
+  // kw), first channel and byte offset from a row's tap (0, 0) chunk.  The
+  // DMAs fetch slabs in order (the prologue's, then one per step, the last
+  // one again past the end), so the state steps one slab after each slab's
+  // DMAs instead of dividing the slab index every step.
+  int ckt = 0, ckh = 0, ckw = 0, cic = 0, ctap = 0, csoff = 0;
+  auto conv_adv = [&]() {
+    if (ckt + 1 >= KT) return;
+    ++ckt;
+    cic += 64;
+    if (cic == cv.iC) {
+      cic = 0;
+      if (++ckw == cv.kW) {
+        ckw = 0;
+        ++ckh;
+      }
+      ctap = ckh * cv.kW + ckw;
+    }
+    csoff = ((ckh * cv.iW + ckw) * int(cv.ldx) + cic) * 2;
   };
   if constexpr (EVEN) {
 #pragma unroll
@@ -1056,7 +1069,6 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
     }
   }
   const uint32_t wa = lds0 + wave * ABLK * 1024, wb = lds0 + BM * 128 + wave * BBLK * 1024;
-  const int KT = K / BK;
   // DMA instruction t of slab kt into stage st (EVEN: A blocks first; else
   // block min(wave + t NW, NB - 1), whose LDS rows start at 1024 b bytes)
 #define MH_DMA(T, KT_, ST)                                                                         \
@@ -1066,9 +1078,7 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
       dma16((b_ < NBA ? A : Bt) + (KT_) * BK, uoff[(T) % NDMA], lds0 + (ST) * STAGE + b_ * 1024);  \
     } else if ((T) < ABLK) {                                                                       \
       if constexpr (CONV) {                                                                        \
-        int tap_;                                                                                  \
-        const int so_ = conv_slab((KT_), tap_);                                                    \
-        const uint32_t v_ = ((cvmask[(T) % ABLK] >> tap_) & 1u) ? uint32_t(cvoff[(T) % ABLK] + so_) \
+        const uint32_t v_ = ((cvmask[(T) % ABLK] >> ctap) & 1u) ? uint32_t(cvoff[(T) % ABLK] + csoff) \
                                                                 : 0x80000000u;                     \
         dma16_buf(xres, v_, wa + (ST) * STAGE + ((T) % ABLK) * 1024);                              \
       } else {                                                                                     \
@@ -1114,6 +1124,7 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
     const int kt = min(s, KT - 1);
 #pragma unroll
     for (int t = 0; t < NDMA; ++t) MH_DMA(t, kt, s);
+    if constexpr (CONV) conv_adv();
   }
   if constexpr (LATE_PRE) {
     epi.prefetch(ep);
@@ -1170,6 +1181,7 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
       if (t < NDMA) MH_DMA(t, kf_, sf_)                                                            \
       else MH_FRAG(Ls_, c1, t - NDMA, af1, bf1)                                                    \
     }                                                                                              \
+    if constexpr (CONV) conv_adv();                                                                \
     if constexpr (LATE == 0) {                                                                     \
       dma_wait<NDMA * (S - 2)>();                                                                  \
       __syncthreads();                                                                             \

@@ -13,27 +13,28 @@ namespace mh {
 namespace {
 
 // Block tile and kernel per shape, measured on MI355X over the UNet's
-// convolutions (kernel trace, fp16, B 8):
+// convolutions (kernel trace, fp16, B 8; the direct-to-LDS kernel stepping
+// its slab state instead of dividing the slab index every K step):
 //  * the 128x128 maps (M = 131072 output pixels): the register-staged 64x64
-//    (four waves of 32x32, 100 VGPRs, several workgroups per CU hiding the
-//    im2col gathers) is fastest (enc0.1 26.3 us, dec0.0 40.1, dec0.1 28.5;
-//    the direct-to-LDS tiles 30.8-68 us);
+//    (four waves of 32x32, several workgroups per CU hiding the im2col
+//    gathers) is fastest (enc0.1 25.7 us, dec0.0 39.0, dec0.1 28.3; the
+//    direct-to-LDS tiles 27.8-64.7 us);
 //  * 64x64 maps with N >= 128 (M = 32768): direct-to-LDS 64x128 with three
-//    stages (enc1.1 22.4 -> 21.0, dec1.0 37.6 -> 33.8, dec1.1 26.7 -> 25.5);
+//    stages (enc1.1 21.9 -> 19.8, dec1.0 36.3 -> 31.2, dec1.1 26.3 -> 23.9),
+//    with N < 128 (down0) direct-to-LDS 64x64 with three stages (12.6 ->
+//    12.2);
 //  * the deeper maps (M < 16384), where a 64x64 grid leaves about one tile
 //    per CU and each K step of the register-staged kernel waits a memory
-//    latency: the direct-to-LDS pipeline with four stages, 64x64
-//    (enc3.1 35.6 -> 27.1, enc3.0 19.0 -> 17.5, enc2.1 22.4 -> 22.1), or
-//    32x64 when 64x64 leaves fewer than 256 tiles (down2 18.5 -> 13.2);
-//  * otherwise the register-staged 32x64 where 64x64 leaves at most one tile
-//    per CU and K <= 2304, else 64x64.
+//    latency: the direct-to-LDS pipeline with four stages, 64x64 (enc3.1
+//    35.4 -> 23.0, enc2.1 21.9 -> 19.3), or 32x64 when 64x64 leaves fewer
+//    than 256 tiles, or exactly 256 with K <= 2304 (down2 20.8 -> 11.6,
+//    enc3.0 21.1 -> 14.4, down1 14.0 -> 10.9).
 // Every tile gives the same bits (test_conv_pipelined_kernel_bits).
 int conv_tile(int M, int N, int K) {
   const long t64 = long((M + 63) / 64) * ((N + 63) / 64);
   if (M >= 65536) return 2;
-  if (M >= 16384 && N >= 128) return 8;
-  if (M < 16384) return t64 < 256 ? 6 : 5;
-  return t64 <= 256 && K <= 2304 ? 3 : 2;
+  if (M >= 16384) return N >= 128 ? 8 : 7;
+  return t64 < 256 || (t64 == 256 && K <= 2304) ? 6 : 5;
 }
 
 template <int DT>

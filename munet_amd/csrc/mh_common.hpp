@@ -187,6 +187,33 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Sum over the 16 lanes of a DPP row (every lane of the row gets it):
+// rotate by 8 and 4 within the row, then the two quad swaps.  Reads only
+// lanes of the same row, so rows whose lanes have all exited do not matter.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false));  // row_ror:8
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xf, 0xf, false));  // row_ror:4
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false));   // quad [2,3,0,1]
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xb1, 0xf, 0xf, false));   // quad [1,0,3,2]
+  return v;
+}
+
+// Eight 16-bit values of one 16-byte chunk decoded to / encoded from floats.
+template <int DT> __device__ __forceinline__ void dec8(uint4 c, float v[8]) {
+  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = Store<DT>::dec(uint16_t(w[i] & 0xffffu));
+    v[2 * i + 1] = Store<DT>::dec(uint16_t(w[i] >> 16));
+  }
+}
+template <int DT> __device__ __forceinline__ uint4 enc8(const float v[8]) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = uint32_t(Store<DT>::enc(v[2 * i])) | (uint32_t(Store<DT>::enc(v[2 * i + 1])) << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 inline size_t dtype_size(int dt) { return dt_size(dt); }
 
 }  // namespace mh

@@ -3,9 +3,9 @@
 // LayerNorm follows ops::layer_norm (src/core/ops/normalization.cpp:125-224):
 // per row mean, biased variance, (x - mean) / sqrt(var + eps) * w + b, output
 // rounded to the storage dtype.  The reference evaluates it in double on the
-// host; here one wave owns a row, keeps the row in registers, and reduces in
-// fp32 with cross-lane shuffles (two passes over registers, one HBM read and
-// one HBM write per element).
+// host; here one wave (16-bit rows up to 1024 values: one 16-lane DPP row)
+// owns a row, keeps it in registers, and reduces in fp32 across its lanes
+// (two passes over registers, one HBM read and one HBM write per element).
 //
 // Softmax follows CPUBackend::softmax (src/backend/cpu_backend.hpp:587-611):
 // float row max, double sum of exp(x - max), y = exp(x - max) / sum; the
@@ -108,6 +108,65 @@ layernorm_vec_kernel(const typename Store<DT>::T *__restrict__ x, const typename
   }
 }
 
+// 16-bit rows of cols <= 128*NC values, cols % 8 == 0: one 16-lane DPP row
+// of lanes per row (four rows per wave), NC 16-byte chunks per lane, every
+// load of the row (x, w, b) issued before the first reduction; the sums
+// reduce within the DPP row (row16_sum), and the output leaves in 16-byte
+// stores.
+template <int DT, int NC>
+__global__ void __launch_bounds__(256)
+layernorm_row16_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ w, const uint16_t *__restrict__ b,
+                       uint16_t *__restrict__ y, int rows, int cols, float eps) {
+  const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int rl = threadIdx.x & 15;
+  if (row >= rows) return;  // the whole DPP row leaves together
+  const int CH = cols / 8;
+  const uint4 *xr = reinterpret_cast<const uint4 *>(x + long(row) * cols);
+  const uint4 *wc = reinterpret_cast<const uint4 *>(w), *bc = reinterpret_cast<const uint4 *>(b);
+  uint4 xq[NC], wq[NC], bq[NC];
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const int c = rl + 16 * k;
+    const bool in = c < CH;
+    xq[k] = in ? xr[c] : make_uint4(0, 0, 0, 0);
+    wq[k] = in ? wc[c] : make_uint4(0, 0, 0, 0);
+    bq[k] = in ? bc[c] : make_uint4(0, 0, 0, 0);
+  }
+  float v[NC][8];
+  float sum = 0.f;
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    dec8<DT>(xq[k], v[k]);
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) sum += v[k][e] + v[k][e + 1];
+  }
+  const float mean = row16_sum(sum) / float(cols);
+  float var = 0.f;
+#pragma unroll
+  for (int k = 0; k < NC; ++k)
+    if (rl + 16 * k < CH)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = v[k][e] - mean;
+        var += d * d;
+      }
+  var = row16_sum(var) / float(cols);
+  const float inv = 1.0f / sqrtf(var + eps);
+  uint4 *yr = reinterpret_cast<uint4 *>(y + long(row) * cols);
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const int c = rl + 16 * k;
+    if (c < CH) {
+      float wv[8], bv[8], o[8];
+      dec8<DT>(wq[k], wv);
+      dec8<DT>(bq[k], bv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (v[k][e] - mean) * inv * wv[e] + bv[e];
+      yr[c] = enc8<DT>(o);
+    }
+  }
+}
+
 // Long rows: three streaming passes (mean, variance, normalise).
 template <int DT>
 __global__ void __launch_bounds__(256)
@@ -160,6 +219,21 @@ hipError_t ln_dt(const void *x, const void *w, const void *b, void *y, int rows,
   T *Y = (T *)y;
   const bool vec = cols % 4 == 0 && (uintptr_t)x % (4 * sizeof(T)) == 0 && (uintptr_t)y % (4 * sizeof(T)) == 0 &&
                    (uintptr_t)w % (4 * sizeof(T)) == 0 && (uintptr_t)b % (4 * sizeof(T)) == 0;
+  if constexpr (DT != F32) {
+    const bool r16 = cols % 8 == 0 && cols <= 1024 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0 &&
+                     (uintptr_t)w % 16 == 0 && (uintptr_t)b % 16 == 0;
+    if (r16) {
+      const dim3 g16((rows + 15) / 16);
+      switch ((cols / 8 + 15) / 16) {
+#define MH_LN16(NC) \
+  case NC: hipLaunchKernelGGL((layernorm_row16_kernel<DT, NC>), g16, block, 0, st, X, W, B, Y, rows, cols, eps); break
+        MH_LN16(1); MH_LN16(2); MH_LN16(3); MH_LN16(4); MH_LN16(5); MH_LN16(6); MH_LN16(7); MH_LN16(8);
+#undef MH_LN16
+      default: return hipErrorInvalidValue;
+      }
+      return hipGetLastError();
+    }
+  }
   if (vec && cols <= 256) hipLaunchKernelGGL((layernorm_vec_kernel<DT, 1>), grid, block, 0, st, X, W, B, Y, rows, cols, eps);
   else if (vec && cols <= 512) hipLaunchKernelGGL((layernorm_vec_kernel<DT, 2>), grid, block, 0, st, X, W, B, Y, rows, cols, eps);
   else if (vec && cols <= 768) hipLaunchKernelGGL((layernorm_vec_kernel<DT, 3>), grid, block, 0, st, X, W, B, Y, rows, cols, eps);

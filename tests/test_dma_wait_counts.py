@@ -1,7 +1,8 @@
 """Static check of the direct-to-LDS GEMM's first wait (CPU; needs hipcc).
 
 The kernel issues the loads of slabs 0 .. S-2 with inline assembly
-(global_load_lds_dwordx4), after the optional 4-byte loads that touch the
+(global_load_lds_dwordx4; a convolution's A blocks through
+buffer_load_dwordx4 ... lds), after the optional 4-byte loads that touch the
 next GEMM's weights, then, for the fixed epilogue programs, the bias /
 residual prefetch, and waits with ``s_waitcnt vmcnt(N)`` for slab 0.  vmcnt
 counts outstanding vector-memory operations and they complete in order, so
@@ -32,12 +33,13 @@ def _asm(src, tmp_path):
 
 
 def _template_args(name):
-    m = re.search(r"gemm_dma_kernelI((?:Li-?\d+E)+)E", name)
+    # integer arguments, then the convolution flag (Lb0E / Lb1E)
+    m = re.search(r"gemm_dma_kernelI((?:Li-?\d+E)+)(?:Lb[01]E)?E", name)
     return [int(v) for v in re.findall(r"Li(-?\d+)E", m.group(1))]
 
 
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
-@pytest.mark.parametrize("src", ["gemm_pipe_wide.hip", "gemm_pipe_fixed_dma.hip"])
+@pytest.mark.parametrize("src", ["gemm_pipe_wide.hip", "gemm_pipe_fixed_dma.hip", "gemm_pipe_conv.hip"])
 def test_first_slab_wait_covers_slab0(src, tmp_path):
     s = _asm(src, tmp_path)
     checked = 0
@@ -51,7 +53,10 @@ def test_first_slab_wait_covers_slab0(src, tmp_path):
         pro = ins[:first_mfma]
         # the slabs' 16-byte DMAs (the 4-byte loads issued before them touch
         # the next GEMM's weights; being older, they only add to the wait)
-        dma = [i for i, x in enumerate(pro) if x.startswith("global_load_lds_dwordx4")]
+        # (convolutions: the A blocks through the buffer form, padding taps
+        # landing as zeros)
+        dma = [i for i, x in enumerate(pro)
+               if x.startswith("global_load_lds_dwordx4") or (x.startswith("buffer_load_dwordx4") and x.endswith(" lds"))]
         assert dma and len(dma) % (stages - 1) == 0, (name, len(dma))
         ndma = len(dma) // (stages - 1)
         last0 = dma[ndma - 1]  # slab 0's last load

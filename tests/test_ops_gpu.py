@@ -179,8 +179,11 @@ def test_attention_pipelined_kernel_bits(hip, dt, B, T, H, causal, monkeypatch):
 
 
 @pytest.mark.parametrize("dt", DTS)
-@pytest.mark.parametrize("rows,cols", [(64, 768), (33, 512), (5, 100), (3, 2000)])
+@pytest.mark.parametrize("rows,cols", [(64, 768), (33, 512), (5, 100), (3, 2000), (17, 1024), (9, 136), (20, 8)])
 def test_layer_norm(hip, orc, dt, rows, cols):
+    """16-bit rows with cols % 8 == 0 up to 1024 take the 16-lane kernel
+    (ragged chunk counts: 136 / 8 = 17 chunks over 16 lanes), the rest the
+    one-wave kernels."""
     x, w, b = rand((rows, cols), dt, 40, 3.0), rand((cols,), dt, 41), rand((cols,), dt, 42)
     out = empty((rows, cols), dt)
     hip.layer_norm(to_device(x, dt), to_device(w, dt), to_device(b, dt), out, rows, cols, 1e-5)
@@ -276,11 +279,14 @@ def test_masked_fill(hip, orc, dt):
 
 
 @pytest.mark.parametrize("dt", DTS)
-@pytest.mark.parametrize("D", [24, 30, 768, 1100])
+@pytest.mark.parametrize("D", [24, 30, 136, 768, 1024, 1100])
 def test_embedding(hip, orc, dt, D):
-    """D % 4 == 0 and D <= 1024 take the vectorised kernel, the rest the scalar one."""
+    """16-bit rows with D % 8 == 0 up to 1024 take the 16-lane kernel, other
+    rows with D % 4 == 0 up to 1024 the one-wave vector kernel, the rest the
+    scalar one.  A -0.0 in the table keeps its sign without a position table."""
     V, B, T = 50, 3, 7
     w = rand((V, D), dt, 90)
+    w[:, 1] = synth.encode(np.array([-0.0]), dt)[0]
     ids = np.random.default_rng(1).integers(0, V, (B, T)).astype(np.int32)
     out = empty((B * T, D), dt)
     hip.embedding(to_device(ids, I32), to_device(w, dt), out, B * T, V, D)
