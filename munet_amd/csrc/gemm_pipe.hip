@@ -94,6 +94,12 @@ hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long ld
   // two stages (with the late wait for the next slab: forward 1.506 ->
   // 1.491 ms against the register-staged 128x128, 1.497 on the 256x256 tile)
   if (tile < 0 && kind == PK_BIAS_NT && dma) tile = 9;
+  // a transposed convolution (K = iC <= 512, scattered output rows): the
+  // register-staged 64x64, whose many small workgroups hide the load and
+  // store latencies of its few K steps (UNet fp16: up2 14.7 -> 11.1 us, up1
+  // 11.5 -> 10.4, up0 19.1 -> 15.1 against 128x64; the direct-to-LDS 128x128
+  // 20-31 us)
+  if (tile < 0 && ep.mode == EPI_CONVT) tile = 2;
   if (tile == 18 && !(DT == BF16 && dma && head_prog)) tile = -1;
   if (tile < 0 || (kind >= PK_LN_BIAS && !fixed_tile(tile) && tile != 18)) tile = auto_tile(dma, M, N, K, batch);
   if (tile >= 7 && !dma) tile = 0;

@@ -1033,25 +1033,32 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(A), 0, CONV ? cv.B * cv.iH * cv.iW * int(cv.ldx) * 2 : 0,
                                         0x00020000);
   const int KT = K / BK;
-  // CONV: the slab the next DMAs fetch (wave-uniform): its index, tap (kh,
-  // kw), first channel and byte offset from a row's tap (0, 0) chunk.  The
-  // DMAs fetch slabs in order (the prologue's, then one per step, the last
-  // one again past the end), so the state steps one slab after each slab's
-  // DMAs instead of dividing the slab index every step.
+  // Convolution: the slab the next DMAs fetch (wave-uniform): its index,
+  // Bt slab pointer, tap (kh, kw), first channel and byte offset from a
+  // row's tap (0, 0) chunk.  The DMAs fetch slabs in order (the prologue's,
+  // then one per step, the last one again past the end), so the state steps
+  // one slab after each slab's DMAs instead of being recomputed from the
+  // slab index every step (two divisions: by the channel blocks per tap and
+  // by the kernel width).  A plain GEMM computes its slab pointers from the
+  // step index, which takes fewer scalar instructions than carrying them.
   int ckt = 0, ckh = 0, ckw = 0, cic = 0, ctap = 0, csoff = 0;
-  auto conv_adv = [&]() {
-    if (ckt + 1 >= KT) return;
-    ++ckt;
-    cic += 64;
-    if (cic == cv.iC) {
-      cic = 0;
-      if (++ckw == cv.kW) {
-        ckw = 0;
-        ++ckh;
+  const uint16_t *bsl = Bt;
+  auto slab_adv = [&]() {
+    if constexpr (CONV) {
+      if (ckt + 1 >= KT) return;
+      ++ckt;
+      bsl += BK;
+      cic += 64;
+      if (cic == cv.iC) {
+        cic = 0;
+        if (++ckw == cv.kW) {
+          ckw = 0;
+          ++ckh;
+        }
+        ctap = ckh * cv.kW + ckw;
       }
-      ctap = ckh * cv.kW + ckw;
+      csoff = ((ckh * cv.iW + ckw) * int(cv.ldx) + cic) * 2;
     }
-    csoff = ((ckh * cv.iW + ckw) * int(cv.ldx) + cic) * 2;
   };
   if constexpr (EVEN) {
 #pragma unroll
@@ -1085,7 +1092,8 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
         dma16(A + (KT_) * BK, aoff[(T) % ABLK], wa + (ST) * STAGE + ((T) % ABLK) * 1024);          \
       }                                                                                            \
     } else                                                                                         \
-      dma16(Bt + (KT_) * BK, boff[((T) - ABLK) % BBLK], wb + (ST) * STAGE + (((T) - ABLK) % BBLK) * 1024); \
+      dma16(CONV ? bsl : Bt + (KT_) * BK, boff[((T) - ABLK) % BBLK],                               \
+            wb + (ST) * STAGE + (((T) - ABLK) % BBLK) * 1024);                                     \
   }
 
   f32x4 acc[FM][FN];
@@ -1124,7 +1132,7 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
     const int kt = min(s, KT - 1);
 #pragma unroll
     for (int t = 0; t < NDMA; ++t) MH_DMA(t, kt, s);
-    if constexpr (CONV) conv_adv();
+    slab_adv();
   }
   if constexpr (LATE_PRE) {
     epi.prefetch(ep);
@@ -1165,9 +1173,14 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
       BF[((X) - FM) % FN] = (L)[BM * 8 + r * 8 + ((C) ^ (r & 7))];                                 \
     }                                                                                              \
   }
+  // stage of the current step: k % S, carried from step to step when S is
+  // not a power of two (a remainder by 3 costs a multiply-high sequence of
+  // scalar instructions every step)
+  constexpr bool CARRY = (S & (S - 1)) != 0;
+  int stg = 0;
 #define MH_DSTEP(KK, FIRST)                                                                        \
   {                                                                                                \
-    const int s_ = (KK) % S, sn_ = s_ + 1 == S ? 0 : s_ + 1, sf_ = s_ == 0 ? S - 1 : s_ - 1;       \
+    const int s_ = CARRY ? stg : (KK) % S, sn_ = s_ + 1 == S ? 0 : s_ + 1, sf_ = s_ == 0 ? S - 1 : s_ - 1; \
     const int kf_ = min((KK) + S - 1, KT - 1);                                                     \
     const u32x4 *Ls_ = &lds[0][0] + s_ * STAGE4, *Ln_ = &lds[0][0] + sn_ * STAGE4;                 \
     _Pragma("unroll") for (int t = 0; t < NMM; ++t) {                                              \
@@ -1181,7 +1194,7 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
       if (t < NDMA) MH_DMA(t, kf_, sf_)                                                            \
       else MH_FRAG(Ls_, c1, t - NDMA, af1, bf1)                                                    \
     }                                                                                              \
-    if constexpr (CONV) conv_adv();                                                                \
+    slab_adv();                                                                                    \
     if constexpr (LATE == 0) {                                                                     \
       dma_wait<NDMA * (S - 2)>();                                                                  \
       __syncthreads();                                                                             \
@@ -1203,6 +1216,7 @@ gemm_dma_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ Bt,
     if constexpr (LATE == 0) {                                                                     \
       _Pragma("unroll") for (int t = NMM; t < NRD; ++t) MH_FRAG(Ln_, c0f, t, af0, bf0)             \
     }                                                                                              \
+    stg = sn_;                                                                                     \
   }
   MH_DSTEP(0, true);
   for (int k = 1; k < KT; ++k) MH_DSTEP(k, false);
