@@ -25,7 +25,7 @@ PLUGIN = os.path.join(HERE, "libmunet_backend_hip.so")
 ARCH = "gfx950"
 
 KERNEL_SOURCES = ["gemm.hip", "gemm_pipe.hip", "gemm_pipe_fixed_staged.hip", "gemm_pipe_fixed_dma.hip",
-                  "gemm_pipe_wide.hip", "gemm_pipe_big.hip", "gemm_pipe_conv.hip", "gemm_pipe_head.hip", "gemm_dma.hip", "attention.hip", "decode.hip",
+                  "gemm_pipe_wide.hip", "gemm_pipe_conv.hip", "gemm_dma.hip", "attention.hip", "decode.hip",
                   "eltwise.hip", "conv_edge.hip", "gemm_skinny.hip",
                   "norm.hip", "layout.hip", "peak.hip"]
 HOST_SOURCES = ["capi.cpp", "engine.cpp", "artifact.cpp"]

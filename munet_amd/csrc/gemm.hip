@@ -355,17 +355,18 @@ hipError_t gemm_nt(int dt, const void *A, const void *Bt, int M, int N, int K, l
   if (M <= 0 || N <= 0 || batch <= 0) return hipSuccess;
   if (tile_hint < 0) {
     // MUNET_HIP_GEMM_TILE forces a kernel and block tile for tests and tuning:
-    // 0-6 direct-to-LDS kernel, 100-107 general kernel, 200-203, 205-212 and
-    // 214-219 pipelined kernel.  Read at every call so a process can switch it
-    // between calls; any other code is an error.
+    // 0-6 direct-to-LDS kernel, 100-107 general kernel, 200-203, 207-212,
+    // 216, 217 and 219 pipelined kernel.  Read at every call so a process can
+    // switch it between calls; any other code is an error.
     const char *force = std::getenv("MUNET_HIP_GEMM_TILE");
     if (force && *force) {
       tile_hint = std::atoi(force);
       const bool known = (tile_hint >= 0 && tile_hint <= 6) || (tile_hint >= 100 && tile_hint <= 107) ||
-                         (tile_hint >= 200 && tile_hint <= 219 && tile_hint != 204 && tile_hint != 213);
+                         (tile_hint >= 200 && tile_hint <= 203) || (tile_hint >= 207 && tile_hint <= 212) ||
+                         tile_hint == 216 || tile_hint == 217 || tile_hint == 219;
       if (!known)
         throw std::invalid_argument(std::string("MUNET_HIP_GEMM_TILE=") + force +
-                                    " names no GEMM tile (0-6, 100-107, 200-203, 205-212, 214-219)");
+                                    " names no GEMM tile (0-6, 100-107, 200-203, 207-212, 216, 217, 219)");
     }
   }
   // <0: the pipelined 16-bit kernel when the operands allow it, else the

@@ -2,8 +2,8 @@
 // on block tiles up to 128 rows, with the accumulators in ordinary VGPRs
 // (built with -amdgpu-mfma-vgpr-form, see build.py), and the dispatcher that
 // picks the block tile and the epilogue program.  The fixed bf16 programs
-// are instantiated in gemm_pipe_fixed_*.hip, 256-row tiles in
-// gemm_pipe_big.hip.
+// are instantiated in gemm_pipe_fixed_*.hip, the eight-wave tiles in
+// gemm_pipe_wide.hip.
 #include <algorithm>
 #include "gemm_pipe.hpp"
 
@@ -14,9 +14,9 @@ namespace {
 // Width of one wave's tile (columns) for each tile code.
 int pipe_wave_cols(int tile) {
   switch (tile) {
-  case 0: case 6: case 7: case 9: case 15: return 64;
+  case 0: case 7: case 9: return 64;
   case 3: case 8: case 10: case 11: case 17: return 48;
-  case 5: case 14: case 16: return 96;
+  case 16: return 96;
   case 19: return 144;
   default: return 32;  // 1 (128x64), 2 (64x64), 12 (128x64)
   }
@@ -86,10 +86,8 @@ template <int DT>
 hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch, long sa,
                      long sb, long sc, const EpiArgs &ep, int tile, int kind, hipStream_t st) {
   const bool dma = gemm_pipe_dma_ok(A, Bt, M, N, K, lda, ldb);
-  // a folded LayerNorm exists only in the fixed programs, and the 256x256
-  // tile only has the plain, bias and non-temporal bias ones: a forced tile
+  // a folded LayerNorm exists only in the fixed programs: a forced tile
   // without the program takes the automatic choice
-  const bool head_prog = kind == PK_PLAIN || kind == PK_BIAS || kind == PK_BIAS_NT;
   // a large streamed output (the vocabulary head): direct-to-LDS 128x128,
   // two stages (with the late wait for the next slab: forward 1.506 ->
   // 1.491 ms against the register-staged 128x128, 1.497 on the 256x256 tile)
@@ -100,8 +98,7 @@ hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long ld
   // 11.5 -> 10.4, up0 19.1 -> 15.1 against 128x64; the direct-to-LDS 128x128
   // 20-31 us)
   if (tile < 0 && ep.mode == EPI_CONVT) tile = 2;
-  if (tile == 18 && !(DT == BF16 && dma && head_prog)) tile = -1;
-  if (tile < 0 || (kind >= PK_LN_BIAS && !fixed_tile(tile) && tile != 18)) tile = auto_tile(dma, M, N, K, batch);
+  if (tile < 0 || (kind >= PK_LN_BIAS && !fixed_tile(tile))) tile = auto_tile(dma, M, N, K, batch);
   if (tile >= 7 && !dma) tile = 0;
   if (tile == 19 && (M % 128 || N % 288)) tile = auto_tile(dma, M, N, K, batch);
   // LayerNorm partials of stats_cols columns need wave tiles that cover whole
@@ -110,12 +107,9 @@ hipError_t launch_dt(const void *A, const void *Bt, int M, int N, int K, long ld
     tile = ep.stats_cols == 48 ? (dma ? 8 : 3) : ep.stats_cols == 64 ? (dma ? 9 : 0) : 2;
   if (tile == 16 || tile == 17 || tile == 19)
     return gemm_pipe_wide(DT, kind, tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
-  if (tile == 18) return gemm_pipe_head(kind, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
   if (kind > PK_GENERAL && fixed_tile(tile))
     return tile <= 3 ? gemm_pipe_fixed_staged(DT, kind, tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st)
                      : gemm_pipe_fixed_dma(DT, kind, tile, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st);
-  if (tile >= 4 && tile <= 6) return gemm_pipe_big(DT, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile - 4, st);
-  if (tile >= 13) return gemm_pipe_big(DT, A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, tile - 4, st);
   switch (tile) {
   case 0: launch<DT, 128, 128, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;
   case 1: launch<DT, 128, 64, 2, 2>(A, Bt, M, N, K, lda, ldb, batch, sa, sb, sc, ep, st); break;

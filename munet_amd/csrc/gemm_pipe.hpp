@@ -49,8 +49,8 @@
 // 64x64) are issued before the K loop.  The epilogue program is a template
 // parameter (PipeKind).  Instantiated by gemm_pipe.hip (the general program,
 // block tiles up to 128 rows, accumulators in VGPRs), gemm_pipe_fixed_*.hip
-// (the fixed bf16 programs) and gemm_pipe_big.hip (256-row block tiles,
-// accumulators in AGPRs).
+// (the fixed bf16 programs), gemm_pipe_wide.hip (the eight-wave tiles) and
+// gemm_pipe_conv.hip (the convolutions).
 #pragma once
 
 #include "mh_common.hpp"
@@ -1284,9 +1284,5 @@ hipError_t gemm_pipe_wide(int dt, int kind, int tile, const void *A, const void 
                           int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st);
 hipError_t gemm_pipe_fixed_dma(int dt, int kind, int tile, const void *A, const void *Bt, int M, int N, int K, long lda,
                                long ldb, int batch, long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st);
-// Direct-to-LDS 256x256, two stages, AGPR accumulators (gemm_pipe_head.hip,
-// tile 18): the plain, bias and non-temporal bias programs.
-hipError_t gemm_pipe_head(int kind, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch,
-                          long sa, long sb, long sc, const EpiArgs &ep, hipStream_t st);
 
 }  // namespace mh

@@ -109,19 +109,14 @@ hipError_t gemm_dma(int dt, const void *A, const void *Bt, int M, int N, int K, 
                     long sb, long sc, const EpiArgs &ep, int tile, hipStream_t st);
 // Pipelined kernels for 16-bit aligned operands (K % 8 == 0, 16-byte aligned
 // rows); tile: < 0 automatic; register-staged 0 128x128, 1 128x64, 2 64x64,
-// 3 128x96, 5 256x192, 6 256x128; direct-to-LDS (K % 64 == 0, else 128x128
-// register-staged) 7 128x128 3 stages, 8 128x96 4 stages, 9 128x128
-// 2 stages, 10 128x96 2 stages, 11 128x96 3 stages, 12 128x64 3 stages,
-// 14 256x192 2 stages, 15 256x128 3 stages.
+// 3 128x96; direct-to-LDS (K % 64 == 0, else 128x128 register-staged)
+// 7 128x128 3 stages, 8 128x96 4 stages, 9 128x128 2 stages, 10 128x96
+// 2 stages, 11 128x96 3 stages, 12 128x64 3 stages; eight waves 16 256x192
+// 2 stages, 17 128x96 4 stages, 19 128x288 3 stages.
 bool gemm_pipe_ok(int dt, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, long sa, long sb);
 bool gemm_pipe_dma_ok(const void *A, const void *Bt, int M, int N, int K, long lda, long ldb);
 hipError_t gemm_pipe(int dt, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch,
                      long sa, long sb, long sc, const EpiArgs &ep, int tile, hipStream_t st);
-// The 256-row tiles of the pipelined kernels (gemm_pipe_big.hip); tile:
-// 1 256x192, 2 256x128 register-staged; 10 256x192, 11 256x128
-// direct-to-LDS.  Operands already checked by gemm_pipe.
-hipError_t gemm_pipe_big(int dt, const void *A, const void *Bt, int M, int N, int K, long lda, long ldb, int batch,
-                         long sa, long sb, long sc, const EpiArgs &ep, int tile, hipStream_t st);
 // Implicit-GEMM convolution on the register-staged pipelined kernel
 // (gemm_pipe_conv.hip): 16-bit, NHWC x and OHWI w 16-byte aligned, iC % 64
 // == 0, ldx % 8 == 0, at most 32 taps, every byte offset of x below 2^31.

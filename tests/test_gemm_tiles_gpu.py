@@ -14,8 +14,8 @@ pytestmark = pytest.mark.gpu
 
 SHAPES = [(300, 192, 200), (257, 128, 129), (64, 64, 64), (520, 256, 264), (96, 200, 72),
           (130, 320, 96), (70, 448, 136), (33, 40, 48), (530, 136, 392)]
-TILES = [0, 1, 2, 3, 4, 5, 6, 100, 101, 102, 103, 104, 105, 106, 107, 200, 201, 202, 203, 205, 206, 207, 208, 209,
-         210, 211, 212, 214, 215, 216, 217, 218, 219]
+TILES = [0, 1, 2, 3, 4, 5, 6, 100, 101, 102, 103, 104, 105, 106, 107, 200, 201, 202, 203, 207, 208, 209,
+         210, 211, 212, 216, 217, 219]
 
 
 @pytest.mark.parametrize("tile", TILES)
@@ -34,7 +34,7 @@ def test_forced_tile(tile, hip, orc, monkeypatch):
             assert_close(to_host(out, dt), ref, dt, what=f"tile={tile} dt={dt} {M}x{K}x{N}")
 
 
-@pytest.mark.parametrize("tile", [205, 206, 207, 208, 209, 210, 211, 212, 214, 215, 216, 217, 218, 219])
+@pytest.mark.parametrize("tile", [207, 208, 209, 210, 211, 212, 216, 217, 219])
 def test_tiles_bit_identical_to_128(tile, hip, monkeypatch):
     """The 256-row and direct-to-LDS tiles accumulate every output in the
     same K order as the register-staged 128x128 tile (64-wide slabs, two
