@@ -307,7 +307,7 @@ __global__ void __launch_bounds__(256)
 embedding_row16_kernel(const int32_t *__restrict__ ids, const uint16_t *__restrict__ w,
                        const uint16_t *__restrict__ pos, uint16_t *__restrict__ out, int n, int V, int D, int T,
                        int *__restrict__ err, float *__restrict__ stats) {
-  const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int row = blockIdx.x * (blockDim.x >> 4) + (threadIdx.x >> 4);
   const int rl = threadIdx.x & 15;
   if (row >= n) return;  // the whole DPP row leaves together
   const int CH = D / 8;
@@ -337,11 +337,14 @@ embedding_row16_kernel(const int32_t *__restrict__ ids, const uint16_t *__restri
     dec8<DT>(tq[k], v);
     dec8<DT>(pq[k], p);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      r[k][e] = Store<DT>::round(prow ? p[e] + v[e] : v[e]);
-      if (c < CH) rsum += r[k][e];
+    for (int e = 0; e < 8; ++e) r[k][e] = prow ? p[e] + v[e] : v[e];
+    if (c < CH) {
+      const uint4 o = enc8<DT>(r[k]);
+      dst[c] = o;
+      dec8<DT>(o, r[k]);  // the stored (rounded) values
+#pragma unroll
+      for (int e = 0; e < 8; ++e) rsum += r[k][e];
     }
-    if (c < CH) dst[c] = enc8<DT>(r[k]);
   }
   if (stats) {
     // the row's LayerNorm statistics over the stored (rounded) values
@@ -541,11 +544,11 @@ hipError_t embedding(int dt, const int32_t *ids, const void *w, const void *pos,
   if (stats && !vec) return hipErrorInvalidValue;  // LayerNorm statistics: vector path only
   if (dt != F32 && D % 8 == 0 && D <= 1024 && (uintptr_t)w % 16 == 0 && (uintptr_t)out % 16 == 0 &&
       (uintptr_t)pos % 16 == 0) {
-    const dim3 g16((n + 15) / 16);
+    const dim3 g16((n + 3) / 4);  // one wave (four rows) per workgroup
     const uint16_t *W = (const uint16_t *)w, *P = (const uint16_t *)pos;
     uint16_t *O = (uint16_t *)out;
 #define MH_EMB16(DTV, NC) \
-  case NC: hipLaunchKernelGGL((embedding_row16_kernel<DTV, NC>), g16, dim3(256), 0, st, ids, W, P, O, n, V, D, T, err, stats); break
+  case NC: hipLaunchKernelGGL((embedding_row16_kernel<DTV, NC>), g16, dim3(64), 0, st, ids, W, P, O, n, V, D, T, err, stats); break
 #define MH_EMB16_NC(DTV) \
   switch ((D / 8 + 15) / 16) { MH_EMB16(DTV, 1); MH_EMB16(DTV, 2); MH_EMB16(DTV, 3); MH_EMB16(DTV, 4); \
                                MH_EMB16(DTV, 5); MH_EMB16(DTV, 6); MH_EMB16(DTV, 7); MH_EMB16(DTV, 8); \

@@ -207,10 +207,24 @@ template <int DT> __device__ __forceinline__ void dec8(uint4 c, float v[8]) {
     v[2 * i + 1] = Store<DT>::dec(uint16_t(w[i] >> 16));
   }
 }
+// fp16 encodes through round4_f16 (the reference's rounding, the 2-op form
+// unless a value of the wave is outside the normal half range) and packs the
+// representable results exactly: the bits of Store<F16>::enc per value.
 template <int DT> __device__ __forceinline__ uint4 enc8(const float v[8]) {
   uint32_t w[4];
+  if constexpr (DT == F16) {
+    float a[4] = {v[0], v[1], v[2], v[3]}, b[4] = {v[4], v[5], v[6], v[7]};
+    round4_f16(a);
+    round4_f16(b);
+    w[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a[0], a[1]));
+    w[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a[2], a[3]));
+    w[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(b[0], b[1]));
+    w[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(b[2], b[3]));
+  } else {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) w[i] = uint32_t(Store<DT>::enc(v[2 * i])) | (uint32_t(Store<DT>::enc(v[2 * i + 1])) << 16);
+    for (int i = 0; i < 4; ++i)
+      w[i] = uint32_t(Store<DT>::enc(v[2 * i])) | (uint32_t(Store<DT>::enc(v[2 * i + 1])) << 16);
+  }
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 

@@ -117,7 +117,7 @@ template <int DT, int NC>
 __global__ void __launch_bounds__(256)
 layernorm_row16_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ w, const uint16_t *__restrict__ b,
                        uint16_t *__restrict__ y, int rows, int cols, float eps) {
-  const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int row = blockIdx.x * (blockDim.x >> 4) + (threadIdx.x >> 4);
   const int rl = threadIdx.x & 15;
   if (row >= rows) return;  // the whole DPP row leaves together
   const int CH = cols / 8;
@@ -223,10 +223,12 @@ hipError_t ln_dt(const void *x, const void *w, const void *b, void *y, int rows,
     const bool r16 = cols % 8 == 0 && cols <= 1024 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0 &&
                      (uintptr_t)w % 16 == 0 && (uintptr_t)b % 16 == 0;
     if (r16) {
-      const dim3 g16((rows + 15) / 16);
+      // one wave (four rows) per workgroup: at 2048 rows of 512 (the
+      // encoder block) 256-thread workgroups left half the CUs idle
+      const dim3 g16((rows + 3) / 4);
       switch ((cols / 8 + 15) / 16) {
 #define MH_LN16(NC) \
-  case NC: hipLaunchKernelGGL((layernorm_row16_kernel<DT, NC>), g16, block, 0, st, X, W, B, Y, rows, cols, eps); break
+  case NC: hipLaunchKernelGGL((layernorm_row16_kernel<DT, NC>), g16, dim3(64), 0, st, X, W, B, Y, rows, cols, eps); break
         MH_LN16(1); MH_LN16(2); MH_LN16(3); MH_LN16(4); MH_LN16(5); MH_LN16(6); MH_LN16(7); MH_LN16(8);
 #undef MH_LN16
       default: return hipErrorInvalidValue;
