@@ -13,27 +13,27 @@ namespace mh {
 namespace {
 
 // Block tile and kernel per shape, measured on MI355X over the UNet's
-// convolutions (kernel trace, fp16, B 8; the direct-to-LDS kernel stepping
-// its slab state instead of dividing the slab index every K step):
-//  * the 128x128 maps (M = 131072 output pixels): the register-staged 64x64
-//    (four waves of 32x32, several workgroups per CU hiding the im2col
-//    gathers) is fastest (enc0.1 25.7 us, dec0.0 39.0, dec0.1 28.3; the
-//    direct-to-LDS tiles 27.8-64.7 us);
-//  * 64x64 maps with N >= 128 (M = 32768): direct-to-LDS 64x128 with three
-//    stages (enc1.1 21.9 -> 19.8, dec1.0 36.3 -> 31.2, dec1.1 26.3 -> 23.9),
-//    with N < 128 (down0) direct-to-LDS 64x64 with three stages (12.6 ->
-//    12.2);
-//  * the deeper maps (M < 16384), where a 64x64 grid leaves about one tile
-//    per CU and each K step of the register-staged kernel waits a memory
-//    latency: the direct-to-LDS pipeline with four stages, 64x64 (enc3.1
-//    35.4 -> 23.0, enc2.1 21.9 -> 19.3), or 32x64 when 64x64 leaves fewer
-//    than 256 tiles, or exactly 256 with K <= 2304 (down2 20.8 -> 11.6,
-//    enc3.0 21.1 -> 14.4, down1 14.0 -> 10.9).
+// convolutions (kernel trace, fp16, B 8; profiles/unet_forward_kernel_stats.md
+// has the sweeps):
+//  * the 128x128 maps (M = 131072 output pixels): direct-to-LDS 256x64 with
+//    eight waves and two stages (enc0.1 25.7 -> 21.8 us, dec0.0 39.0 -> 31.5,
+//    dec0.1 28.4 -> 24.1 against the register-staged 64x64 four-wave tile);
+//  * the 64x64 maps (M = 32768) and the 32x32 maps with N >= 256: direct-to-LDS
+//    128x64 with eight waves and three stages (enc1.1 19.8 -> 17.4, dec2.0
+//    32.4 -> 28.8, enc2.1 19.3 -> 17.3 against the four-wave 64x128 / 64x64
+//    tiles), or 128x128 with eight waves and three stages for N >= 128 and
+//    K > 1152 (dec1.0 28.4 -> 26.9): eight waves per workgroup share each
+//    weight slab between twice the output pixels;
+//  * the deeper maps, where a larger tile leaves CUs idle: direct-to-LDS with
+//    four waves and four stages, 32x64 when 64x64 leaves fewer than 256 tiles,
+//    or exactly 256 with K <= 2304 (down2 11.6, enc3.0 14.4, down1 10.9 us),
+//    else 64x64 (enc3.1 23.0).
 // Every tile gives the same bits (test_conv_pipelined_kernel_bits).
 int conv_tile(int M, int N, int K) {
   const long t64 = long((M + 63) / 64) * ((N + 63) / 64);
-  if (M >= 65536) return 2;
-  if (M >= 16384) return N >= 128 ? 8 : 7;
+  if (M >= 65536) return 10;
+  if (M >= 16384) return N >= 128 && K > 1152 ? 11 : 9;
+  if (M >= 8192 && N >= 256) return 9;
   return t64 < 256 || (t64 == 256 && K <= 2304) ? 6 : 5;
 }
 
@@ -43,12 +43,16 @@ hipError_t run(const void *x, const void *w, const ConvArgs &cv, int oC, const E
   int tile = conv_tile(M, oC, cv.kH * cv.kW * cv.iC);
   // tuning override, read per call: MUNET_HIP_CONV_TILE = 0 128x128, 1 128x64, 2 64x64, 3 32x64, 4 64x32
   // (register-staged), 5 64x64 four stages, 6 32x64 four stages, 7 64x64 three stages, 8 64x128 three
-  // stages (direct-to-LDS)
+  // stages (direct-to-LDS, four waves), 9 128x64 three stages, 10 256x64 two stages, 11 128x128 three
+  // stages (direct-to-LDS, eight waves)
   if (const char *e = std::getenv("MUNET_HIP_CONV_TILE")) {
     const int t = std::atoi(e);
-    if (t >= 0 && t <= 8) tile = t;
+    if (t >= 0 && t <= 11) tile = t;
   }
   switch (tile) {
+  case 9: launch_dma_conv<DT, 128, 64, 4, 2, 3>(x, w, cv, oC, ep, st); break;
+  case 10: launch_dma_conv<DT, 256, 64, 4, 2, 2>(x, w, cv, oC, ep, st); break;
+  case 11: launch_dma_conv<DT, 128, 128, 4, 2, 3>(x, w, cv, oC, ep, st); break;
   case 5: launch_dma_conv<DT, 64, 64, 2, 2, 4>(x, w, cv, oC, ep, st); break;
   case 6: launch_dma_conv<DT, 32, 64, 2, 2, 4>(x, w, cv, oC, ep, st); break;
   case 7: launch_dma_conv<DT, 64, 64, 2, 2, 3>(x, w, cv, oC, ep, st); break;

@@ -349,8 +349,9 @@ def test_conv_pipelined_kernel_bits(hip, dt, B, iC, H, W, oC, k, s, p, act, monk
     of the general implicit-GEMM kernel (same MFMA sequence, bias added to the
     fp32 accumulator, one rounding, ReLU) on NHWC inputs, over the block
     tiles (the automatic choice, the register-staged 32x64 / 64x32 tiles and
-    the direct-to-LDS 64x64 four / three stages, 32x64 four stages and
-    64x128 three stages forced), strides, 1x1 and 5x5 filters, ragged pixel
+    the direct-to-LDS 64x64 four / three stages, 32x64 four stages, 64x128
+    three stages, and the eight-wave 128x64, 256x64 and 128x128 forced),
+    strides, 1x1 and 5x5 filters, ragged pixel
     counts and padding on every side (the direct-to-LDS loads of padding
     taps read past the buffer resource and land as zeros)."""
     x = rand((B, H, W, iC), dt, 120)
@@ -361,7 +362,7 @@ def test_conv_pipelined_kernel_bits(hip, dt, B, iC, H, W, oC, k, s, p, act, monk
     hip.pack_conv_weight(to_device(w, dt), wo, oC, iC, k, k)
     xd, bd = to_device(x, dt), to_device(b, dt)
     outs = {}
-    tiles = ("pipelined", "tile3", "tile4", "tile5", "tile6", "tile7", "tile8")
+    tiles = ("pipelined",) + tuple(f"tile{t}" for t in range(3, 12))
     for name in tiles + ("general",):
         monkeypatch.delenv("MUNET_HIP_CONV_KERNEL", raising=False)
         monkeypatch.delenv("MUNET_HIP_CONV_TILE", raising=False)
