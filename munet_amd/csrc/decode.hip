@@ -52,20 +52,29 @@ template <int DT> struct Chunk {
 };
 
 // token + position rows of the tokens fed at state[0], one rounding
-// (the prefill's embedding_pos chain)
+// (the prefill's embedding_pos chain): one thread per 16-byte chunk of the
+// B rows, the id and the position loaded together and both rows' chunks as
+// soon as they arrive (a loop of 2-byte loads waited a round trip per trip)
 template <int DT>
 __global__ void __launch_bounds__(256)
 dec_embed_kernel(const int32_t *__restrict__ ids, const typename Store<DT>::T *__restrict__ tok,
                  const typename Store<DT>::T *__restrict__ pos_tab, const int *__restrict__ state,
                  typename Store<DT>::T *__restrict__ out, int B, int V, int D, int *__restrict__ err) {
-  typedef Store<DT> S;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (row >= B) return;
+  typedef Chunk<DT> C;
+  const int DC = D / C::E, i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= B * DC) return;
+  const int row = i / DC, cc = i - row * DC;
   const int t = ids[row], p = state[0];
   const bool ok = t >= 0 && t < V;
-  if (!ok && lane == 0) atomicOr(err, 1);
-  const typename S::T *src = tok + long(ok ? t : 0) * D, *prow = pos_tab + long(p) * D;
-  for (int d = lane; d < D; d += 64) out[long(row) * D + d] = S::enc(S::dec(prow[d]) + (ok ? S::dec(src[d]) : 0.f));
+  if (!ok && cc == 0) atomicOr(err, 1);
+  const uint4 tv = reinterpret_cast<const uint4 *>(tok + long(ok ? t : 0) * D)[cc];
+  const uint4 pv = reinterpret_cast<const uint4 *>(pos_tab + long(p) * D)[cc];
+  float a[C::E], pe[C::E];
+  C::dec(tv, a);
+  C::dec(pv, pe);
+#pragma unroll
+  for (int e = 0; e < C::E; ++e) a[e] = pe[e] + (ok ? a[e] : 0.f);
+  reinterpret_cast<uint4 *>(out)[i] = C::enc(a);
 }
 
 // The Linear output chain for one value (reference rounding per op):
@@ -483,14 +492,18 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
 }
 
 // Attention of the fed tokens over the cached keys 0..pos (the newest key is
-// the query's own position), one block per kSplit keys of head (b, h), the
-// way the prefill's flash kernel runs a key tile: scores
-// s_j = round(round(q.k_j) * scale) (the reference's matmul and scale
-// roundings), the block max m, p_j = round(e^(s_j - m)) (the rounded,
-// unnormalised probabilities the product uses), and the block's shares
-// o = sum_j p_j v_j, l = sum_j p_j into part_o / part_ml for the
-// out-projection's input stage to combine.  Every K and V load of a thread is
-// issued before the first wait.
+// the query's own position), one block per kSplit keys of head (b, h), one
+// wave per 64 of them, the way the prefill's flash kernel runs a key tile:
+// scores s_j = round(round(q.k_j) * scale) (the reference's matmul and scale
+// roundings), the wave's max m, p_j = round(e^(s_j - m)) (the rounded,
+// unnormalised probabilities the product uses) and the wave's shares
+// o = sum_j p_j v_j, l = sum_j p_j; the four waves' shares are rescaled to
+// the block's max and added in wave order, into part_o / part_ml for the
+// out-projection's input stage to combine.
+// Lane layout: eight lanes per key row, lane c = lane & 7 holding dimensions
+// 8c..8c+7 of rows (lane >> 3) + 8i, i = 0..7, of the wave's keys, so every
+// K and V load instruction reads eight whole 128-byte rows (16-bit caches).
+// Every K and V load of a thread is issued before the first wait.
 template <int DT>
 __global__ void __launch_bounds__(kSplit)
 dec_attn_kernel(const typename Store<DT>::T *__restrict__ q, const typename Store<DT>::T *__restrict__ kc,
@@ -498,106 +511,139 @@ dec_attn_kernel(const typename Store<DT>::T *__restrict__ q, const typename Stor
                 float *__restrict__ part_o, float2 *__restrict__ part_ml, int H, int hd, int Lmax, float scale) {
   typedef Store<DT> S;
   typedef typename S::T T;
-  typedef Chunk<DT> C;
-  constexpr int KCH = 64 / C::E;  // 16-byte chunks of a key row (hd <= 64)
-  __shared__ float qs[64];
-  __shared__ float ps[kSplit];
-  __shared__ float red[kSplit / 64];
-  __shared__ float osh[16][65];
+  constexpr int NU = int(sizeof(T)) / 2;  // 16-byte pieces per 8 dimensions
+  constexpr int RW = 8;                   // key rows per lane
+  __shared__ float wml[kSplit / 64][2];
+  __shared__ float wo[kSplit / 64][64];
   const int s = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = bh / H, h = bh - b * H, ns = gridDim.x;
-  const int j0 = s * kSplit;
-  const int kcn = hd / C::E;
+  const int c = lane & 7, rr = lane >> 3;
+  const bool dim_ok = c * 8 < hd;
+  const int cd = dim_ok ? c * 8 : 0;  // (lanes past hd load dimension 0 and are masked)
+  const int jw = s * kSplit + wave * 64;  // the wave's first key
   // The position, q, K and V are loaded together: the cache addresses are
   // clamped to the cache's rows, not to the position, so no load waits for
-  // the position's (a block past the position loads rows it does not use).
-  // Loads complete in issue order, so the scores wait only for the
-  // position, q and K, and V arrives during the softmax.
+  // the position's.  A block past the position computes an empty share
+  // (every key masked) instead of leaving early: an early exit let the
+  // compiler sink the loads below the position's test.
   const int pos = state[0];
-  const T qraw = q[long(b) * H * hd + long(h) * hd + min(tid, hd - 1)];
-  asm volatile("" ::: "memory");
-  // K row of this thread's key, V elements dq..dq+3 of keys jg, jg+16, ...
-  const int j = j0 + tid, jg = tid >> 4, dq = (tid & 15) * 4;
-  uint4 kr[KCH];
-  const uint4 *krow = reinterpret_cast<const uint4 *>(kc + (long(bh) * Lmax + min(j, Lmax - 1)) * hd);
+  uint4 qv[NU];
+  {
+    const uint4 *qp = reinterpret_cast<const uint4 *>(q + long(b) * H * hd + long(h) * hd + cd);
 #pragma unroll
-  for (int c = 0; c < KCH; ++c) kr[c] = krow[min(c, kcn - 1)];  // (chunks past hd are never used)
-  asm volatile("" ::: "memory");
-  typedef typename std::conditional<sizeof(T) == 2, uint2, uint4>::type V4;
-  V4 vr[kSplit / 16];
-  const int dqc = min(dq, hd - 4);
+    for (int u = 0; u < NU; ++u) qv[u] = qp[u];
+  }
+  const T *kb = kc + long(bh) * Lmax * hd, *vb = vc + long(bh) * Lmax * hd;
+  uint4 kr[RW][NU], vr[RW][NU];
 #pragma unroll
-  for (int t = 0; t < kSplit / 16; ++t) {
-    const int jj = min(j0 + jg + 16 * t, Lmax - 1);
-    vr[t] = *reinterpret_cast<const V4 *>(vc + (long(bh) * Lmax + jj) * hd + dqc);
+  for (int i = 0; i < RW; ++i) {
+    const uint4 *kp = reinterpret_cast<const uint4 *>(kb + (min(jw + rr + 8 * i, Lmax - 1) * hd + cd));
+#pragma unroll
+    for (int u = 0; u < NU; ++u) kr[i][u] = kp[u];
   }
-  asm volatile("" ::: "memory");
-  const int L = pos + 1, jn = min(kSplit, L - j0);
-  if (jn <= 0) {  // past the position: an empty share
-    if (tid < hd) part_o[(long(bh) * ns + s) * hd + tid] = 0.f;
-    if (tid == 0) part_ml[long(bh) * ns + s] = make_float2(-INFINITY, 0.f);
-    return;
+#pragma unroll
+  for (int i = 0; i < RW; ++i) {
+    const uint4 *vp = reinterpret_cast<const uint4 *>(vb + (min(jw + rr + 8 * i, Lmax - 1) * hd + cd));
+#pragma unroll
+    for (int u = 0; u < NU; ++u) vr[i][u] = vp[u];
   }
-  if (tid < hd) qs[tid] = S::dec(qraw);
-  lds_barrier();
+  // (every load above is issued before the first arithmetic that waits)
+  __builtin_amdgcn_sched_barrier(0);
+  const int L = pos + 1;
 
-  float sc = -INFINITY;
-  if (tid < jn) {
-    float sum = 0.f;
+  // scores: each lane's 8-dimension partial, summed over the row's 8 lanes
+  // (quad swaps, then the half-row mirror: every lane of the row ends with
+  // the same sum)
+  float qf[8];
+  if constexpr (NU == 1) {
+    dec8<DT>(qv[0], qf);
+  } else {
 #pragma unroll
-    for (int c = 0; c < KCH; ++c)
-      if (c < kcn) {
-        float kv[C::E];
-        C::dec(kr[c], kv);
-#pragma unroll
-        for (int e = 0; e < C::E; ++e) sum = fmaf(qs[c * C::E + e], kv[e], sum);
-      }
-    sc = S::round(S::round(sum) * scale);
-  }
-  float mx = wave_max(sc);
-  if (lane == 0) red[wave] = mx;
-  lds_barrier();
-  mx = red[0];
-#pragma unroll
-  for (int w = 1; w < kSplit / 64; ++w) mx = fmaxf(mx, red[w]);
-  const float p = tid < jn ? S::round(__expf(sc - mx)) : 0.f;
-  ps[tid] = p;
-  const float l = wave_sum(p);
-  lds_barrier();
-  if (lane == 0) red[wave] = l;
-  float o[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int t = 0; t < kSplit / 16; ++t) {
-    const int jj = jg + 16 * t;
-    if (jj < jn) {
-      float v[4];
-      if constexpr (sizeof(T) == 2) {
-        const uint2 w = vr[t];
-        v[0] = S::dec(uint16_t(w.x)); v[1] = S::dec(uint16_t(w.x >> 16));
-        v[2] = S::dec(uint16_t(w.y)); v[3] = S::dec(uint16_t(w.y >> 16));
-      } else {
-        const uint4 w = vr[t];
-        v[0] = __uint_as_float(w.x); v[1] = __uint_as_float(w.y); v[2] = __uint_as_float(w.z); v[3] = __uint_as_float(w.w);
-      }
-      const float pj = ps[jj];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = fmaf(pj, v[e], o[e]);
+    for (int u = 0; u < 2; ++u) {
+      qf[4 * u] = __uint_as_float(qv[u].x); qf[4 * u + 1] = __uint_as_float(qv[u].y);
+      qf[4 * u + 2] = __uint_as_float(qv[u].z); qf[4 * u + 3] = __uint_as_float(qv[u].w);
     }
   }
+  float sc[RW];
+  float mx = -INFINITY;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) osh[jg][(dq + e) & 63] = o[e];
+  for (int i = 0; i < RW; ++i) {
+    float part = 0.f;
+    if constexpr (NU == 1) {
+      part = dot8<DT>(kr[i][0], qv[0], 0.f);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        part = fmaf(qf[4 * u], __uint_as_float(kr[i][u].x), part);
+        part = fmaf(qf[4 * u + 1], __uint_as_float(kr[i][u].y), part);
+        part = fmaf(qf[4 * u + 2], __uint_as_float(kr[i][u].z), part);
+        part = fmaf(qf[4 * u + 3], __uint_as_float(kr[i][u].w), part);
+      }
+    }
+    if (!dim_ok) part = 0.f;
+    part += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(part), 0xb1, 0xf, 0xf, false));   // quad [1,0,3,2]
+    part += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(part), 0x4e, 0xf, 0xf, false));   // quad [2,3,0,1]
+    part += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(part), 0x141, 0xf, 0xf, false));  // half-row mirror
+    const bool valid = jw + rr + 8 * i < L;
+    sc[i] = valid ? S::round(S::round(part) * scale) : -INFINITY;
+    mx = fmaxf(mx, sc[i]);
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  // masked keys (s = -inf) get p = e^-inf = 0, also in a wave with no key at
+  // or before the position (mx = -inf, taken as 0)
+  const float mxs = mx > -INFINITY ? mx : 0.f;
+  float l = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < RW; ++i) {
+    const float p = S::round(__expf(sc[i] - mxs));
+    l += p;
+    float v[8];
+    if constexpr (NU == 1) {
+      dec8<DT>(vr[i][0], v);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        v[4 * u] = __uint_as_float(vr[i][u].x); v[4 * u + 1] = __uint_as_float(vr[i][u].y);
+        v[4 * u + 2] = __uint_as_float(vr[i][u].z); v[4 * u + 3] = __uint_as_float(vr[i][u].w);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = fmaf(p, v[e], o[e]);
+  }
+  // the eight row groups' sums (every lane of a column ends with the same)
+  l += __shfl_xor(l, 8, 64);
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    o[e] += __shfl_xor(o[e], 8, 64);
+    o[e] += __shfl_xor(o[e], 16, 64);
+    o[e] += __shfl_xor(o[e], 32, 64);
+  }
+  if (lane == 0) {
+    wml[wave][0] = mx;
+    wml[wave][1] = l;
+  }
+  if (rr == 0 && dim_ok) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wo[wave][c * 8 + e] = o[e];
+  }
   __syncthreads();
   if (tid < hd) {
-    float t = 0.f;
+    float m = wml[0][0];
 #pragma unroll
-    for (int g = 0; g < 16; ++g) t += osh[g][tid];
-    part_o[(long(bh) * ns + s) * hd + tid] = t;
-  }
-  if (tid == 0) {
-    float lt = 0.f;
+    for (int w = 1; w < kSplit / 64; ++w) m = fmaxf(m, wml[w][0]);
+    float ot = 0.f, lt = 0.f;
 #pragma unroll
-    for (int w = 0; w < kSplit / 64; ++w) lt += red[w];
-    part_ml[long(bh) * ns + s] = make_float2(mx, lt);
+    for (int w = 0; w < kSplit / 64; ++w) {
+      const float f = wml[w][1] > 0.f ? __expf(wml[w][0] - m) : 0.f;
+      ot = fmaf(wo[w][tid], f, ot);
+      lt = fmaf(wml[w][1], f, lt);
+    }
+    part_o[(long(bh) * ns + s) * hd + tid] = ot;
+    if (tid == 0) part_ml[long(bh) * ns + s] = make_float2(m, lt);
   }
 }
 
@@ -640,7 +686,8 @@ kv_store_kernel(const uint4 *__restrict__ k, const uint4 *__restrict__ v, uint4 
 
 hipError_t dec_embed(int dt, const int32_t *ids, const void *tok, const void *pos_tab, const int *state, void *out,
                      int B, int V, int D, int *err, hipStream_t st) {
-  const dim3 grid((B + 3) / 4);
+  if (D % int(16 / dt_size(dt)) != 0) return hipErrorInvalidValue;
+  const dim3 grid(unsigned((size_t(B) * D * dt_size(dt) / 16 + 255) / 256));
   switch (dt) {
   case F32: hipLaunchKernelGGL(dec_embed_kernel<F32>, grid, dim3(256), 0, st, ids, (const float *)tok, (const float *)pos_tab, state, (float *)out, B, V, D, err); break;
   case F16: hipLaunchKernelGGL(dec_embed_kernel<F16>, grid, dim3(256), 0, st, ids, (const uint16_t *)tok, (const uint16_t *)pos_tab, state, (uint16_t *)out, B, V, D, err); break;
@@ -717,7 +764,8 @@ hipError_t dec_linear(int dt, int kind, const DecLinear &p, hipStream_t st) {
 hipError_t dec_attention(int dt, const void *q, const void *kc, const void *vc, const int *state, float *part_o,
                          float2 *part_ml, int B, int H, int hd, int Lmax, float scale, hipStream_t st) {
   const int ns = (Lmax + kSplit - 1) / kSplit;
-  if (hd > 64 || hd % 4 != 0 || hd % int(16 / dt_size(dt)) != 0 || ns > kMaxSplit) return hipErrorInvalidValue;
+  // (eight lanes of 8 dimensions per key row)
+  if (hd > 64 || hd % 8 != 0 || ns > kMaxSplit) return hipErrorInvalidValue;
   const dim3 grid(ns, B * H);
   switch (dt) {
   case F32: hipLaunchKernelGGL(dec_attn_kernel<F32>, grid, dim3(kSplit), 0, st, (const float *)q, (const float *)kc, (const float *)vc, state, part_o, part_ml, H, hd, Lmax, scale); break;

@@ -1569,8 +1569,8 @@ struct mh_decoder {
     if (batch < 1 || batch > 16) throw Error("decoder: batch must be in 1..16");
     if (max_len < 1 || max_len > C) throw Error("decoder: max_len must be in 1..ctx");
     if (max_len > 4096) throw Error("decoder: max_len above 4096 (16 attention blocks of 256 keys)");
-    if (d % H || hd > 64 || hd % 4 || hd % int(ce) || d % int(ce) || ffn % int(ce))
-      throw Error("decoder: d_model, ffn and head_dim must be multiples of 16 bytes, head_dim <= 64");
+    if (d % H || hd > 64 || hd % 8 || hd % int(ce) || d % int(ce) || ffn % int(ce))
+      throw Error("decoder: d_model, ffn and head_dim must be multiples of 16 bytes, head_dim a multiple of 8 and <= 64");
     if (size_t(batch) * std::max(d, ffn) * es > 65536) throw Error("decoder: batch x width exceeds the 64 KiB row stage");
     B = batch;
     Lmax = max_len;
