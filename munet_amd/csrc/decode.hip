@@ -240,6 +240,11 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
   }
 
   // ---- 2. weights: chunks rl + 16 (q + WS i) of each of the row's columns
+  // (loaded without a test: a load under a branch, even a wave-uniform one,
+  // made the compiler's wait counts conservative, so that the input stage
+  // waited for every weight load); the products use slots i < ni, the
+  // chunk slots K needs
+  const int ni = min(KCH, (KC + 16 * WS - 1) / (16 * WS));
   uint4 wv[CPL][KCH];
 #pragma unroll
   for (int cc = 0; cc < CPL; ++cc) {
@@ -284,7 +289,7 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
 #pragma unroll
         for (int e = 0; e < C::E; ++e) sum += v[i][e];
       }
-      const float mean = wave_sum(sum) / float(K);
+      const float mean = wave_sum_dpp(sum) / float(K);
       float var = 0.f;
 #pragma unroll
       for (int i = 0; i < LCH; ++i)
@@ -294,7 +299,7 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
             const float d = v[i][e] - mean;
             var += d * d;
           }
-      var = wave_sum(var) / float(K);
+      var = wave_sum_dpp(var) / float(K);
       const float inv = 1.0f / sqrtf(var + a.eps);
 #pragma unroll
       for (int i = 0; i < LCH; ++i) {
@@ -384,41 +389,80 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
   lds_barrier();
 
   // ---- 5. products, reductions, epilogue
+  // Single-column products over up to 4 rows read every row's input chunks
+  // before the first product: a chunk past K reads a clamped input chunk and
+  // takes it as zeros (its weights are the clamped, finite chunk K - 1), rows
+  // past M read row M - 1 and are never stored (a test per chunk and row put
+  // each read in its own branch, followed by its own wait).  Up to 16 rows:
+  // one row's chunks at a time, rows past M skipped by a wave-uniform test.
   float acc[CPL][MB];
 #pragma unroll
   for (int cc = 0; cc < CPL; ++cc)
 #pragma unroll
     for (int m = 0; m < MB; ++m) acc[cc][m] = 0.f;
-#pragma unroll
-  for (int i = 0; i < KCH; ++i) {
+  auto xload = [&](int i, int mm) -> uint4 {
     const int c = rl + 16 * (q + WS * i);
-    if (c < KC) {
-      if constexpr (DT == F32) {
-        float w[CPL][C::E];
+    const uint4 xv = xs[mm * KC + min(c, KC - 1)];
+    return c < KC ? xv : z4();
+  };
+  auto prod = [&](int i, int m, uint4 x) {
+    if constexpr (DT == F32) {
+      float xv[C::E];
+      C::dec(x, xv);
 #pragma unroll
-        for (int cc = 0; cc < CPL; ++cc) C::dec(wv[cc][i], w[cc]);
+      for (int cc = 0; cc < CPL; ++cc) {
+        float w[C::E];
+        C::dec(wv[cc][i], w);
 #pragma unroll
-        for (int m = 0; m < MB; ++m) {
-          if (m < M) {
-            float xv[C::E];
-            C::dec(xs[m * KC + c], xv);
+        for (int e = 0; e < C::E; ++e) acc[cc][m] = fmaf(w[e], xv[e], acc[cc][m]);
+      }
+    } else {
+      // four packed dot products per chunk and row instead of 16 decodes and
+      // 8 FMAs
 #pragma unroll
-            for (int cc = 0; cc < CPL; ++cc)
+      for (int cc = 0; cc < CPL; ++cc) acc[cc][m] = dot8<DT>(wv[cc][i], x, acc[cc][m]);
+    }
+  };
+  if constexpr (MB == 4 && CPL == 1 && IN != IN_ATTN) {
+    // every row's chunks read before the first product
+    uint4 xr[MB][KCH];
 #pragma unroll
-              for (int e = 0; e < C::E; ++e) acc[cc][m] = fmaf(w[cc][e], xv[e], acc[cc][m]);
-          }
-        }
-      } else {
-        // one wave per SIMD runs this loop: four packed dot products per
-        // chunk and row instead of 16 decodes and 8 FMAs
+    for (int i = 0; i < KCH; ++i)
+      if (i < ni)
 #pragma unroll
-        for (int m = 0; m < MB; ++m) {
-          if (m < M) {
-            const uint4 xr = xs[m * KC + c];
+        for (int m = 0; m < MB; ++m) xr[m][i] = xload(i, min(m, M - 1));
 #pragma unroll
-            for (int cc = 0; cc < CPL; ++cc) acc[cc][m] = dot8<DT>(wv[cc][i], xr, acc[cc][m]);
-          }
-        }
+    for (int i = 0; i < KCH; ++i) {
+      if (i >= ni) break;
+#pragma unroll
+      for (int m = 0; m < MB; ++m) prod(i, m, xr[m][i]);
+    }
+  } else if constexpr (MB == 4) {
+    // the vocabulary head (four columns per row: the batched reads above
+    // would take it past 256 registers, one workgroup per CU) and the
+    // out-projection (two of eight chunk slots used at d 768): one chunk at
+    // a time, lanes past K idle
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int c = rl + 16 * (q + WS * i);
+      if (c < KC) {
+#pragma unroll
+        for (int m = 0; m < MB; ++m)
+          if (m < M) prod(i, m, xs[m * KC + c]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      if (m >= M) break;
+      uint4 xr[KCH];
+#pragma unroll
+      for (int i = 0; i < KCH; ++i)
+        if (i < ni) xr[i] = xload(i, m);
+#pragma unroll
+      for (int i = 0; i < KCH; ++i) {
+        if (i >= ni) break;
+        prod(i, m, xr[i]);
       }
     }
   }
@@ -514,7 +558,7 @@ dec_attn_kernel(const typename Store<DT>::T *__restrict__ q, const typename Stor
   constexpr int NU = int(sizeof(T)) / 2;  // 16-byte pieces per 8 dimensions
   constexpr int RW = 8;                   // key rows per lane
   __shared__ float wml[kSplit / 64][2];
-  __shared__ float wo[kSplit / 64][64];
+  __shared__ float wo[kSplit / 64][4][64];
   const int s = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = bh / H, h = bh - b * H, ns = gridDim.x;
   const int c = lane & 7, rr = lane >> 3;
@@ -588,9 +632,10 @@ dec_attn_kernel(const typename Store<DT>::T *__restrict__ q, const typename Stor
     sc[i] = valid ? S::round(S::round(part) * scale) : -INFINITY;
     mx = fmaxf(mx, sc[i]);
   }
-  mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  // the wave's max: the two row groups of a 16-lane DPP row (rotation by
+  // 8), then the four DPP rows
+  mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mx), 0x128, 0xf, 0xf, false)));
+  mx = rows4_max(mx);
   // masked keys (s = -inf) get p = e^-inf = 0, also in a wave with no key at
   // or before the position (mx = -inf, taken as 0)
   const float mxs = mx > -INFINITY ? mx : 0.f;
@@ -612,23 +657,20 @@ dec_attn_kernel(const typename Store<DT>::T *__restrict__ q, const typename Stor
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = fmaf(p, v[e], o[e]);
   }
-  // the eight row groups' sums (every lane of a column ends with the same)
-  l += __shfl_xor(l, 8, 64);
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
+  // the row groups' sums: the two of each 16-lane DPP row by a rotation by
+  // 8, then l over the four DPP rows; o's four DPP-row partials go to LDS
+  l += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(l), 0x128, 0xf, 0xf, false));
+  l = rows4_sum(l);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    o[e] += __shfl_xor(o[e], 8, 64);
-    o[e] += __shfl_xor(o[e], 16, 64);
-    o[e] += __shfl_xor(o[e], 32, 64);
-  }
+  for (int e = 0; e < 8; ++e)
+    o[e] += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(o[e]), 0x128, 0xf, 0xf, false));
   if (lane == 0) {
     wml[wave][0] = mx;
     wml[wave][1] = l;
   }
-  if (rr == 0 && dim_ok) {
+  if ((lane & 15) < 8 && dim_ok) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) wo[wave][c * 8 + e] = o[e];
+    for (int e = 0; e < 8; ++e) wo[wave][lane >> 4][c * 8 + e] = o[e];
   }
   __syncthreads();
   if (tid < hd) {
@@ -639,7 +681,8 @@ dec_attn_kernel(const typename Store<DT>::T *__restrict__ q, const typename Stor
 #pragma unroll
     for (int w = 0; w < kSplit / 64; ++w) {
       const float f = wml[w][1] > 0.f ? __expf(wml[w][0] - m) : 0.f;
-      ot = fmaf(wo[w][tid], f, ot);
+      const float ow = (wo[w][0][tid] + wo[w][1][tid]) + (wo[w][2][tid] + wo[w][3][tid]);
+      ot = fmaf(ow, f, ot);
       lt = fmaf(wml[w][1], f, lt);
     }
     part_o[(long(bh) * ns + s) * hd + tid] = ot;

@@ -198,6 +198,29 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// The four DPP rows' values read from lanes 0, 16, 32 and 48 (the row's
+// value must already be in its lane 0, 16, 32 or 48); every lane gets the
+// same result.  Every lane of the wave must be active.
+__device__ __forceinline__ float rows4_sum(float v) {
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+__device__ __forceinline__ float rows4_max(float v) {
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// Whole-wave sum without LDS-pipe shuffles: DPP within each 16-lane row,
+// then the four rows through scalar reads (every lane gets the same value).
+// Every lane of the wave must be active.
+__device__ __forceinline__ float wave_sum_dpp(float v) { return rows4_sum(row16_sum(v)); }
+
 // Eight 16-bit values of one 16-byte chunk decoded to / encoded from floats.
 template <int DT> __device__ __forceinline__ void dec8(uint4 c, float v[8]) {
   const uint32_t w[4] = {c.x, c.y, c.z, c.w};
