@@ -120,6 +120,14 @@ template <int DT> __device__ __forceinline__ float dot8(uint4 w, uint4 x, float 
   return acc;
 }
 
+// A 16-byte load with the non-temporal hint (the cached keys and values are
+// read once per step and should not displace the weights in the caches).
+__device__ __forceinline__ uint4 nt_load16(const uint4 *p) {
+  typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+  const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // A zero chunk as a prvalue: `c ? p[i] : zero` with an lvalue zero is a
 // glvalue conditional, compiled as a load through a selected address (a
 // scratch copy of the zero, flat 4-byte loads) instead of a selected value.
@@ -583,13 +591,13 @@ dec_attn_kernel(const typename Store<DT>::T *__restrict__ q, const typename Stor
   for (int i = 0; i < RW; ++i) {
     const uint4 *kp = reinterpret_cast<const uint4 *>(kb + (min(jw + rr + 8 * i, Lmax - 1) * hd + cd));
 #pragma unroll
-    for (int u = 0; u < NU; ++u) kr[i][u] = kp[u];
+    for (int u = 0; u < NU; ++u) kr[i][u] = nt_load16(kp + u);
   }
 #pragma unroll
   for (int i = 0; i < RW; ++i) {
     const uint4 *vp = reinterpret_cast<const uint4 *>(vb + (min(jw + rr + 8 * i, Lmax - 1) * hd + cd));
 #pragma unroll
-    for (int u = 0; u < NU; ++u) vr[i][u] = vp[u];
+    for (int u = 0; u < NU; ++u) vr[i][u] = nt_load16(vp + u);
   }
   // (every load above is issued before the first arithmetic that waits)
   __builtin_amdgcn_sched_barrier(0);
