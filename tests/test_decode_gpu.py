@@ -104,7 +104,8 @@ def test_decode_steps_vs_oracle(orc, dt):
     _steps_vs_oracle(orc, _small(dt), 2, 64, "tbd")
 
 
-@pytest.mark.parametrize("case", ["wide_batch_bf16", "long_cache_f32", "four_wave_f16", "four_wave_f32"])
+@pytest.mark.parametrize("case", ["wide_batch_bf16", "long_cache_f32", "four_wave_f16", "four_wave_f32",
+                                  "head_dim_32_bf16", "head_dim_48_f32_long_prompt"])
 def test_decode_launch_shapes_vs_oracle(orc, case):
     """The step's other launch shapes against the oracle:
     wide_batch_bf16: batch 8 at d 512 (the 16-row kernels, and B*d > 3072,
@@ -114,7 +115,11 @@ def test_decode_launch_shapes_vs_oracle(orc, case):
     the same combine loop);
     four_wave_f16 / four_wave_f32: FFN down with K past 128 chunks (its K
     split over the block's four waves), batches 5 and 3, and a vocabulary of
-    8192 (the head's four-columns-per-row kernel)."""
+    8192 (the head's four-columns-per-row kernel);
+    head_dim_32_bf16 / head_dim_48_f32_long_prompt: heads narrower than the
+    attention kernel's eight lanes of 8 dimensions (lanes past the head
+    dimension masked), the second with a 300-token prompt so that the keys
+    span several waves and two 256-key blocks."""
     if case == "wide_batch_bf16":
         cfg = models.decoder_config(vocab=500, ctx=96, d_model=512, num_heads=8, num_layers=2, ffn=1024,
                                     dtype="bfloat16", attention="textbook")
@@ -123,6 +128,14 @@ def test_decode_launch_shapes_vs_oracle(orc, case):
         cfg = models.decoder_config(vocab=500, ctx=1280, d_model=128, num_heads=2, num_layers=2, ffn=256,
                                     dtype="float32", attention="textbook")
         _steps_vs_oracle(orc, cfg, 2, 1280, "dls_lc")
+    elif case == "head_dim_32_bf16":
+        cfg = models.decoder_config(vocab=500, ctx=96, d_model=128, num_heads=4, num_layers=2, ffn=256,
+                                    dtype="bfloat16", attention="textbook")
+        _steps_vs_oracle(orc, cfg, 2, 64, "dls_hd32")
+    elif case == "head_dim_48_f32_long_prompt":
+        cfg = models.decoder_config(vocab=500, ctx=320, d_model=96, num_heads=2, num_layers=2, ffn=192,
+                                    dtype="float32", attention="textbook")
+        _steps_vs_oracle(orc, cfg, 2, 320, "dls_hd48", T0=300, n=6)
     else:
         dt = "float16" if case.endswith("f16") else "float32"
         cfg = models.decoder_config(vocab=8192, ctx=96, d_model=128, num_heads=2, num_layers=2,
