@@ -137,7 +137,9 @@ int mh_engine_forward_op_times(mh_engine *engine, int reps, char *buf, size_t le
  * prefill.  Greedy decoding: each step feeds one token per sequence. */
 typedef struct mh_decoder mh_decoder;
 /* A decoder over a compiled engine (weights shared with it), `batch`
- * sequences (1..16), positions 0..max_len-1 (max_len <= ctx). */
+ * sequences (1..16), positions 0..max_len-1 (max_len <= ctx, at most 4096);
+ * head_dim a multiple of 8 and at most 64, d_model and ffn rows multiples of
+ * 16 bytes, batch x max(d_model, ffn) values within 64 KiB. */
 int mh_decoder_create(mh_decoder **decoder, mh_engine *engine, int batch, int max_len);
 int mh_decoder_destroy(mh_decoder *decoder);
 /* Prompt ids [batch, T0] (int32) through the engine's forward, filling the
