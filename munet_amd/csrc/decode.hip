@@ -573,11 +573,10 @@ dec_attn_kernel(const typename Store<DT>::T *__restrict__ q, const typename Stor
   const bool dim_ok = c * 8 < hd;
   const int cd = dim_ok ? c * 8 : 0;  // (lanes past hd load dimension 0 and are masked)
   const int jw = s * kSplit + wave * 64;  // the wave's first key
-  // The position, q, K and V are loaded together: the cache addresses are
-  // clamped to the cache's rows, not to the position, so no load waits for
-  // the position's.  A block past the position computes an empty share
-  // (every key masked) instead of leaving early: an early exit let the
-  // compiler sink the loads below the position's test.
+  // The position and q are loaded first; the K and V rows are clamped to the
+  // position, so rows past it re-read the last cached row (cache hits)
+  // instead of streaming rows 0..max_len-1 of every block, and a block past
+  // the position leaves before loading any (an empty share).
   const int pos = state[0];
   uint4 qv[NU];
   {
@@ -585,23 +584,29 @@ dec_attn_kernel(const typename Store<DT>::T *__restrict__ q, const typename Stor
 #pragma unroll
     for (int u = 0; u < NU; ++u) qv[u] = qp[u];
   }
+  const int L = pos + 1;
+  if (s * kSplit >= L) {
+    if (tid < hd) part_o[(long(bh) * ns + s) * hd + tid] = 0.f;
+    if (tid == 0) part_ml[long(bh) * ns + s] = make_float2(-INFINITY, 0.f);
+    return;
+  }
+  const int jlast = min(pos, Lmax - 1);
   const T *kb = kc + long(bh) * Lmax * hd, *vb = vc + long(bh) * Lmax * hd;
   uint4 kr[RW][NU], vr[RW][NU];
 #pragma unroll
   for (int i = 0; i < RW; ++i) {
-    const uint4 *kp = reinterpret_cast<const uint4 *>(kb + (min(jw + rr + 8 * i, Lmax - 1) * hd + cd));
+    const uint4 *kp = reinterpret_cast<const uint4 *>(kb + (min(jw + rr + 8 * i, jlast) * hd + cd));
 #pragma unroll
     for (int u = 0; u < NU; ++u) kr[i][u] = nt_load16(kp + u);
   }
 #pragma unroll
   for (int i = 0; i < RW; ++i) {
-    const uint4 *vp = reinterpret_cast<const uint4 *>(vb + (min(jw + rr + 8 * i, Lmax - 1) * hd + cd));
+    const uint4 *vp = reinterpret_cast<const uint4 *>(vb + (min(jw + rr + 8 * i, jlast) * hd + cd));
 #pragma unroll
     for (int u = 0; u < NU; ++u) vr[i][u] = nt_load16(vp + u);
   }
   // (every load above is issued before the first arithmetic that waits)
   __builtin_amdgcn_sched_barrier(0);
-  const int L = pos + 1;
 
   // scores: each lane's 8-dimension partial, summed over the row's 8 lanes
   // (quad swaps, then the half-row mirror: every lane of the row ends with
