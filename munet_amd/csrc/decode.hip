@@ -11,6 +11,9 @@
 // device memory (state[0]) so one captured graph serves every step:
 //   state[0] = pos: position of the tokens being fed
 //   state[1] = step index into the generated-token buffer
+//   state[2] = 1 while the head's greedy choices (best) are still to be fed
+//              back: the next step's first kernel does it, or, after the
+//              last step of a call, dec_finish_kernel
 // Cache layout: [layer][b][h][Lmax][hd] for K and for V, 16-byte rows of
 // the head dimension contiguous.
 #include <type_traits>
@@ -51,30 +54,59 @@ template <int DT> struct Chunk {
   }
 };
 
-// token + position rows of the tokens fed at state[0], one rounding
-// (the prefill's embedding_pos chain): one thread per 16-byte chunk of the
-// B rows, the id and the position loaded together and both rows' chunks as
-// soon as they arrive (a loop of 2-byte loads waited a round trip per trip)
+// The step's first kernel.  The previous step's greedy choices, when pending
+// (state[2], set by the head), become this step's input tokens and generated
+// tokens: ids[b] and tokens[step][b], best reset, the position and the step
+// index advanced.  Then the token + position rows of the fed tokens, one
+// rounding (the prefill's embedding_pos chain), one thread per 16-byte chunk.
+// One workgroup: every state read happens before its barrier and every state
+// write after it, and the new position reaches the rows through LDS.
 template <int DT>
 __global__ void __launch_bounds__(256)
-dec_embed_kernel(const int32_t *__restrict__ ids, const typename Store<DT>::T *__restrict__ tok,
-                 const typename Store<DT>::T *__restrict__ pos_tab, const int *__restrict__ state,
-                 typename Store<DT>::T *__restrict__ out, int B, int V, int D, int *__restrict__ err) {
+dec_embed_kernel(int32_t *__restrict__ ids, unsigned long long *__restrict__ best, int32_t *__restrict__ tokens,
+                 int *__restrict__ state, const typename Store<DT>::T *__restrict__ tok,
+                 const typename Store<DT>::T *__restrict__ pos_tab, typename Store<DT>::T *__restrict__ out, int B,
+                 int V, int D, int cap, int *__restrict__ err) {
   typedef Chunk<DT> C;
-  const int DC = D / C::E, i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= B * DC) return;
-  const int row = i / DC, cc = i - row * DC;
-  const int t = ids[row], p = state[0];
-  const bool ok = t >= 0 && t < V;
-  if (!ok && cc == 0) atomicOr(err, 1);
-  const uint4 tv = reinterpret_cast<const uint4 *>(tok + long(ok ? t : 0) * D)[cc];
-  const uint4 pv = reinterpret_cast<const uint4 *>(pos_tab + long(p) * D)[cc];
-  float a[C::E], pe[C::E];
-  C::dec(tv, a);
-  C::dec(pv, pe);
+  __shared__ int s_tok[16];
+  __shared__ int s_pos;
+  const int tid = threadIdx.x;
+  const int p0 = state[0], st = state[1], pend = state[2];
+  int t = 0;
+  if (tid < B) {
+    const unsigned long long k = best[tid];
+    const int prev = ids[tid];
+    t = pend ? (k ? int(0xffffffffu - uint32_t(k & 0xffffffffu)) : 0) : prev;
+    s_tok[tid] = t;
+  }
+  if (tid == 0) s_pos = p0 + (pend ? 1 : 0);
+  __syncthreads();
+  if (pend) {
+    if (tid < B) {
+      ids[tid] = t;
+      if (st < cap) tokens[long(st) * B + tid] = t;
+      best[tid] = 0;
+    }
+    if (tid == 0) {
+      state[0] = p0 + 1;
+      state[1] = st + 1;
+      state[2] = 0;
+    }
+  }
+  const int p = s_pos, DC = D / C::E;
+  for (int i = tid; i < B * DC; i += 256) {
+    const int row = i / DC, cc = i - row * DC, tr = s_tok[row];
+    const bool ok = tr >= 0 && tr < V;
+    if (!ok && cc == 0) atomicOr(err, 1);
+    const uint4 tv = reinterpret_cast<const uint4 *>(tok + long(ok ? tr : 0) * D)[cc];
+    const uint4 pv = reinterpret_cast<const uint4 *>(pos_tab + long(p) * D)[cc];
+    float a[C::E], pe[C::E];
+    C::dec(tv, a);
+    C::dec(pv, pe);
 #pragma unroll
-  for (int e = 0; e < C::E; ++e) a[e] = pe[e] + (ok ? a[e] : 0.f);
-  reinterpret_cast<uint4 *>(out)[i] = C::enc(a);
+    for (int e = 0; e < C::E; ++e) a[e] = pe[e] + (ok ? a[e] : 0.f);
+    reinterpret_cast<uint4 *>(out)[i] = C::enc(a);
+  }
 }
 
 // The Linear output chain for one value (reference rounding per op):
@@ -175,6 +207,7 @@ struct DecLinArgs {
   void *out, *kc, *vc;
   unsigned long long *best;
   const int *state;
+  int *pending;
   int M, N, K, E, H, hd, Lmax, nsplit;
   float eps, gelu_c;
 };
@@ -540,6 +573,8 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
       for (int c = 1; c < SLOTS; ++c) k = bk[c][tid] > k ? bk[c][tid] : k;
       if (k) atomicMax(&a.best[tid], k);
     }
+    // the next kernel of the chain feeds the choices back
+    if (blockIdx.x == 0 && tid == 0 && a.pending) *a.pending = 1;
   }
 }
 
@@ -703,14 +738,15 @@ dec_attn_kernel(const typename Store<DT>::T *__restrict__ q, const typename Stor
   }
 }
 
-// The greedy choices folded by the head (best[b]) become the next step's
-// input and the generated tokens; best is reset and the position and step
-// index advance.
+// After the last step of a call: the pending greedy choices (best[b]) become
+// the next input and the generated tokens, best is reset and the position and
+// step index advance (what the next step's first kernel does otherwise).
 __global__ void __launch_bounds__(64)
 dec_finish_kernel(unsigned long long *__restrict__ best, int32_t *__restrict__ ids, int32_t *__restrict__ tokens,
                   int *__restrict__ state, int B, int cap) {
   const int b = threadIdx.x;
-  const int st = state[1];
+  const int p0 = state[0], st = state[1], pend = state[2];
+  if (!pend) return;  // (the same for every thread)
   if (b < B) {
     const unsigned long long k = best[b];
     const int out = k ? int(0xffffffffu - uint32_t(k & 0xffffffffu)) : 0;
@@ -720,8 +756,9 @@ dec_finish_kernel(unsigned long long *__restrict__ best, int32_t *__restrict__ i
   }
   __syncthreads();
   if (b == 0) {
-    state[0] += 1;
+    state[0] = p0 + 1;
     state[1] = st + 1;
+    state[2] = 0;
   }
 }
 
@@ -740,14 +777,13 @@ kv_store_kernel(const uint4 *__restrict__ k, const uint4 *__restrict__ v, uint4 
 
 }  // namespace
 
-hipError_t dec_embed(int dt, const int32_t *ids, const void *tok, const void *pos_tab, const int *state, void *out,
-                     int B, int V, int D, int *err, hipStream_t st) {
-  if (D % int(16 / dt_size(dt)) != 0) return hipErrorInvalidValue;
-  const dim3 grid(unsigned((size_t(B) * D * dt_size(dt) / 16 + 255) / 256));
+hipError_t dec_embed(int dt, int32_t *ids, unsigned long long *best, int32_t *tokens, int *state, const void *tok,
+                     const void *pos_tab, void *out, int B, int V, int D, int cap, int *err, hipStream_t st) {
+  if (B < 1 || B > 16 || D % int(16 / dt_size(dt)) != 0) return hipErrorInvalidValue;
   switch (dt) {
-  case F32: hipLaunchKernelGGL(dec_embed_kernel<F32>, grid, dim3(256), 0, st, ids, (const float *)tok, (const float *)pos_tab, state, (float *)out, B, V, D, err); break;
-  case F16: hipLaunchKernelGGL(dec_embed_kernel<F16>, grid, dim3(256), 0, st, ids, (const uint16_t *)tok, (const uint16_t *)pos_tab, state, (uint16_t *)out, B, V, D, err); break;
-  case BF16: hipLaunchKernelGGL(dec_embed_kernel<BF16>, grid, dim3(256), 0, st, ids, (const uint16_t *)tok, (const uint16_t *)pos_tab, state, (uint16_t *)out, B, V, D, err); break;
+  case F32: hipLaunchKernelGGL(dec_embed_kernel<F32>, dim3(1), dim3(256), 0, st, ids, best, tokens, state, (const float *)tok, (const float *)pos_tab, (float *)out, B, V, D, cap, err); break;
+  case F16: hipLaunchKernelGGL(dec_embed_kernel<F16>, dim3(1), dim3(256), 0, st, ids, best, tokens, state, (const uint16_t *)tok, (const uint16_t *)pos_tab, (uint16_t *)out, B, V, D, cap, err); break;
+  case BF16: hipLaunchKernelGGL(dec_embed_kernel<BF16>, dim3(1), dim3(256), 0, st, ids, best, tokens, state, (const uint16_t *)tok, (const uint16_t *)pos_tab, (uint16_t *)out, B, V, D, cap, err); break;
   default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -763,7 +799,7 @@ hipError_t dec_linear(int dt, int kind, const DecLinear &p, hipStream_t st) {
   const int KC = p.K / ce;
   if (kind == 4 && (p.nsplit < 1 || p.nsplit > kMaxSplit || p.hd % 4 != 0 || p.K % 4 != 0)) return hipErrorInvalidValue;
   DecLinArgs a{p.x, p.w, p.bias, p.ln_w, p.ln_b, p.resid, p.part_o, p.part_ml, p.out, p.kc, p.vc, p.best, p.state,
-               p.M, p.N, p.K, p.E, p.H, p.hd, p.Lmax, p.nsplit, p.eps, p.gelu_c};
+               p.pending, p.M, p.N, p.K, p.E, p.H, p.hd, p.Lmax, p.nsplit, p.eps, p.gelu_c};
   // Launch shape: K up to 128 chunks per column on one wave's 16-lane row
   // (8 chunks per lane), longer K split over the block's four waves (up to
   // 512 chunks); the vocabulary head (N >= 8192, short K) takes 4 columns per

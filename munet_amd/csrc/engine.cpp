@@ -1675,7 +1675,8 @@ struct mh_decoder {
   void enqueue_step() {
     using mh::hip_check;
     const float gelu_c = mh::host_round(dt, 1.702f), scale = mh::host_round(dt, 1.0f / std::sqrt(float(hd)));
-    hip_check(mh::dec_embed(dt, ids, tok, pos_tab, state, x, B, V, d, mh::device_error_flag(), stream), "decode embed");
+    hip_check(mh::dec_embed(dt, ids, best, tokens, state, tok, pos_tab, x, B, V, d, Lmax, mh::device_error_flag(), stream),
+              "decode embed");
     mh::DecLinear p;
     p.state = state; p.M = B; p.E = d; p.H = H; p.hd = hd; p.Lmax = Lmax; p.nsplit = nsplit; p.eps = eps;
     p.gelu_c = gelu_c;
@@ -1699,9 +1700,14 @@ struct mh_decoder {
     }
     mh::DecLinear hd_ = p;  // ln_f + head, greedy choice folded into best
     hd_.x = x; hd_.w = whead; hd_.bias = bhead; hd_.ln_w = lnfw; hd_.ln_b = lnfb; hd_.out = logits; hd_.best = best;
-    hd_.N = V; hd_.K = d;
+    hd_.pending = state + 2; hd_.N = V; hd_.K = d;
     hip_check(mh::dec_linear(dt, 3, hd_, stream), "decode ln_f + head");
-    hip_check(mh::dec_finish(best, ids, tokens, state, B, Lmax, stream), "decode finish");
+  }
+
+  // the last step's pending choices fed back (the next step's first kernel
+  // does it otherwise)
+  void finish() {
+    mh::hip_check(mh::dec_finish(best, ids, tokens, state, B, Lmax, stream), "decode finish");
   }
 
   // Prompt ids [B, T0] through the engine's forward (textbook attention), the
@@ -1738,7 +1744,7 @@ struct mh_decoder {
     // the next input: each sequence's greedy choice at its last position
     for (int b = 0; b < B; ++b)
       hip_check(mh::argmax_rows(dt, out + (size_t(b) * T0 + T0 - 1) * V * es, ids + b, 1, V, e.stream), "prefill argmax");
-    const int st[2] = {T0, 0};
+    const int st[3] = {T0, 0, 0};
     hip_check(hipMemcpyAsync(state, st, sizeof(st), hipMemcpyHostToDevice, e.stream), "decoder state");
     hip_check(hipStreamSynchronize(e.stream), "prefill");
     e.check_error_flag();
@@ -1759,6 +1765,7 @@ struct mh_decoder {
     if (hids) hip_check(hipMemcpyAsync(ids, hids, size_t(B) * 4, hipMemcpyHostToDevice, stream), "decoder ids H2D");
     hip_check(hipEventRecord(ev0, stream), "hipEventRecord");
     hip_check(hipGraphLaunch(exec, stream), "hipGraphLaunch");
+    finish();
     hip_check(hipEventRecord(ev1, stream), "hipEventRecord");
     if (logits_out)
       hip_check(hipMemcpyAsync(logits_out, logits, size_t(B) * V * mh::dt_size(dt), hipMemcpyDeviceToHost, stream),
@@ -1782,6 +1789,7 @@ struct mh_decoder {
     hip_check(hipMemcpyAsync(state + 1, &zero, sizeof(int), hipMemcpyHostToDevice, stream), "decoder state");
     hip_check(hipEventRecord(ev0, stream), "hipEventRecord");
     for (int i = 0; i < n; ++i) hip_check(hipGraphLaunch(exec, stream), "hipGraphLaunch");
+    finish();
     hip_check(hipEventRecord(ev1, stream), "hipEventRecord");
     if (tokens_out)
       hip_check(hipMemcpyAsync(tokens_out, tokens, size_t(n) * B * 4, hipMemcpyDeviceToHost, stream), "tokens D2H");
@@ -1798,7 +1806,7 @@ struct mh_decoder {
     std::ostringstream s;
     s << "{\"batch\":" << B << ",\"max_len\":" << Lmax << ",\"position\":" << pos << ",\"steps\":" << steps
       << ",\"weight_bytes\":" << wbytes << ",\"cache_bytes\":" << cache_bytes << ",\"buffer_bytes\":" << bufbytes
-      << ",\"kernels_per_step\":" << (3 + 5 * L) << ",\"last_step_ms\":" << last_step_ms
+      << ",\"kernels_per_step\":" << (2 + 5 * L) << ",\"last_step_ms\":" << last_step_ms
       << ",\"last_generate_ms\":" << last_generate_ms << ",\"last_prefill_ms\":" << last_prefill_ms
       << ",\"prefill_instances\":" << prefills.size() << "}";
     return s.str();

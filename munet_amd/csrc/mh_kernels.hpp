@@ -156,9 +156,14 @@ hipError_t gemm_splitk(int dt, const void *A, const void *Bt, int M, int N, int 
 hipError_t attention(int dt, const void *q, const void *k, const void *v, void *ctx, int B, int H, int T, int hd,
                      int causal, float scale, int force_generic, hipStream_t st, int textbook = 0);
 
-// KV-cache decode (decode.hip).  state: device ints {pos, step}.
-hipError_t dec_embed(int dt, const int32_t *ids, const void *tok, const void *pos_tab, const int *state, void *out,
-                     int B, int V, int D, int *err, hipStream_t st);
+// KV-cache decode (decode.hip).  state: device ints {pos, step, pending}:
+// the position of the tokens being fed, the index of the next generated
+// token in `tokens`, and 1 while the head's greedy choices in best still have
+// to be fed back.
+// The step's first kernel: pending choices become ids / tokens[step] (best
+// reset, position and step + 1), then the token + position rows of ids.
+hipError_t dec_embed(int dt, int32_t *ids, unsigned long long *best, int32_t *tokens, int *state, const void *tok,
+                     const void *pos_tab, void *out, int B, int V, int D, int cap, int *err, hipStream_t st);
 // One weight-streaming Linear over M <= 16 rows (dec_linear kinds: 0
 // LayerNorm + q/k/v, k and v into the caches at pos; 1 + residual; 2
 // LayerNorm + GELU; 3 LayerNorm + greedy argmax folded into best; 4 the
@@ -171,6 +176,7 @@ struct DecLinear {
   void *out = nullptr, *kc = nullptr, *vc = nullptr;
   unsigned long long *best = nullptr;
   const int *state = nullptr;
+  int *pending = nullptr;  // kind 3: set to 1 once the choices are in best
   int M = 0, N = 0, K = 0, E = 0, H = 1, hd = 1, Lmax = 1, nsplit = 1;
   float eps = 1e-5f, gelu_c = 1.702f;
 };
@@ -179,7 +185,8 @@ hipError_t dec_linear(int dt, int kind, const DecLinear &p, hipStream_t st);
 // part_ml [B*H][blocks] (blocks = ceil(Lmax / 256) <= 16)
 hipError_t dec_attention(int dt, const void *q, const void *kc, const void *vc, const int *state, float *part_o,
                          float2 *part_ml, int B, int H, int hd, int Lmax, float scale, hipStream_t st);
-// best [B] -> ids [B] and tokens[step] (best reset), position and step + 1
+// When choices are pending: best [B] -> ids [B] and tokens[step] (best
+// reset), position and step + 1 (after the last step of a call)
 hipError_t dec_finish(unsigned long long *best, int32_t *ids, int32_t *tokens, int *state, int B, int cap,
                       hipStream_t st);
 hipError_t kv_store(int dt, const void *k, const void *v, void *kc, void *vc, int BH, int T, int hd, int Lmax,
