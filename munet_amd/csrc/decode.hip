@@ -307,6 +307,9 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
     braw[cc] = static_cast<const T *>(a.bias)[nn];
     rraw[cc] = RESID ? static_cast<const T *>(a.resid)[long(mm) * N + nn] : T(0);
   }
+  // the cache position of the k / v stores (read here: loaded in the
+  // epilogue it cost a memory round trip at the end of the kernel)
+  const int kv_pos = OUT == OUT_QKV ? a.state[0] : 0;
   // every load above stays ahead of the input stage's arithmetic
   asm volatile("" ::: "memory");
 
@@ -547,7 +550,7 @@ __global__ void __launch_bounds__(256) dec_linear_kernel(DecLinArgs a) {
           static_cast<T *>(a.out)[long(m) * a.E + e] = y;
         } else {
           T *cache = static_cast<T *>(which == 1 ? a.kc : a.vc);
-          cache[((long(m) * a.H + h) * a.Lmax + a.state[0]) * a.hd + dd] = y;
+          cache[((long(m) * a.H + h) * a.Lmax + kv_pos) * a.hd + dd] = y;
         }
       } else {
         static_cast<T *>(a.out)[long(m) * N + n] = y;
