@@ -169,6 +169,36 @@ def test_decode_explicit_ids_and_generate_repeat_step(orc):
     assert st["batch"] == B and st["position"] == T0 + 1 and st["prefill_instances"] == 1
 
 
+def test_decode_mixed_calls_match_single_steps():
+    """The greedy choices of one call are fed back by the next step's first
+    kernel (or by the flush at the end of a call): prefill, generate(4),
+    step(), step(explicit ids), generate(3), step() give the tokens and
+    positions of the same sequence of single steps."""
+    cfg = _small()
+    p = models.init_params(cfg, "gpt", scope="tbm")
+    B, T0 = 2, 11
+    prompt = models.make_input(cfg, (B, T0), "gpt", scope="tbm_in")
+    eng = Engine(0).load(cfg, p).compile((B, T0))
+    dcd = Decoder(eng, B, 40)
+    t = np.array([42, 7], dtype=np.int32)
+
+    dcd.prefill(prompt, logits=False)
+    ref = [dcd.step()[1] for _ in range(5)]
+    ref.append(dcd.step(t)[1])
+    ref += [dcd.step()[1] for _ in range(4)]
+    assert dcd.position() == T0 + 10
+
+    dcd.prefill(prompt, logits=False)
+    got = list(dcd.generate(4)[0])
+    got.append(dcd.step()[1])
+    assert dcd.position() == T0 + 5
+    got.append(dcd.step(t)[1])
+    got += list(dcd.generate(3)[0])
+    got.append(dcd.step()[1])
+    assert dcd.position() == T0 + 10
+    assert np.array_equal(np.stack(got), np.stack(ref))
+
+
 def test_decoder_errors():
     cfg = _small()
     p = models.init_params(cfg, "gpt", scope="tbe")
