@@ -804,7 +804,7 @@ hipError_t dec_linear(int dt, int kind, const DecLinear &p, hipStream_t st) {
   DecLinArgs a{p.x, p.w, p.bias, p.ln_w, p.ln_b, p.resid, p.part_o, p.part_ml, p.out, p.kc, p.vc, p.best, p.state,
                p.pending, p.M, p.N, p.K, p.E, p.H, p.hd, p.Lmax, p.nsplit, p.eps, p.gelu_c};
   // Launch shape: K up to 128 chunks per column on one wave's 16-lane row
-  // (8 chunks per lane), longer K split over the block's four waves (up to
+  // (up to 8 chunks per lane), longer K split over the block's four waves (up to
   // 512 chunks); the vocabulary head (N >= 8192, short K) takes 4 columns per
   // row so each block amortises its LayerNorm stage over 64 columns.  The
   // out-projection, whose 16-column blocks would leave CUs idle (48 blocks
@@ -820,23 +820,35 @@ hipError_t dec_linear(int dt, int kind, const DecLinear &p, hipStream_t st) {
   const int ncols = (4 / ws) * 4 * cpl;  // columns per block
   const dim3 grid(unsigned((p.N + ncols - 1) / ncols));
   const size_t lds = size_t(p.M) * p.K * es;
-#define MH_DLK(DTV, MB, CPL, WS)                                                                                           \
-  switch (kind) {                                                                                                          \
-  case 0: hipLaunchKernelGGL((dec_linear_kernel<DTV, 8, MB, CPL, WS, IN_LN, OUT_QKV, ACT_NONE, false>), grid, dim3(256), lds, st, a); break;   \
-  case 1: hipLaunchKernelGGL((dec_linear_kernel<DTV, 8, MB, CPL, WS, IN_ROW, OUT_ROW, ACT_NONE, true>), grid, dim3(256), lds, st, a); break;   \
-  case 2: hipLaunchKernelGGL((dec_linear_kernel<DTV, 8, MB, CPL, WS, IN_LN, OUT_ROW, ACT_GELU, false>), grid, dim3(256), lds, st, a); break;   \
-  case 3: hipLaunchKernelGGL((dec_linear_kernel<DTV, 8, MB, CPL, WS, IN_LN, OUT_ARGMAX, ACT_NONE, false>), grid, dim3(256), lds, st, a); break; \
-  case 4: hipLaunchKernelGGL((dec_linear_kernel<DTV, 8, MB, CPL, WS, IN_ATTN, OUT_ROW, ACT_NONE, true>), grid, dim3(256), lds, st, a); break;  \
-  default: return hipErrorInvalidValue;                                                                                    \
+  // weight chunk slots per lane: the K-chunks a lane takes, ceil(KC / (16
+  // ws)), rounded up to 2, 6 or 8 (every slot is loaded, clamped past K: the
+  // out-projection at d 768, two chunks per lane, loaded eight)
+  const int need = (KC + 16 * ws - 1) / (16 * ws), kch = need <= 2 ? 2 : need <= 6 ? 6 : 8;
+#define MH_DLK(DTV, KCV, MB, CPL, WS)                                                                                        \
+  switch (kind) {                                                                                                            \
+  case 0: hipLaunchKernelGGL((dec_linear_kernel<DTV, KCV, MB, CPL, WS, IN_LN, OUT_QKV, ACT_NONE, false>), grid, dim3(256), lds, st, a); break;   \
+  case 1: hipLaunchKernelGGL((dec_linear_kernel<DTV, KCV, MB, CPL, WS, IN_ROW, OUT_ROW, ACT_NONE, true>), grid, dim3(256), lds, st, a); break;   \
+  case 2: hipLaunchKernelGGL((dec_linear_kernel<DTV, KCV, MB, CPL, WS, IN_LN, OUT_ROW, ACT_GELU, false>), grid, dim3(256), lds, st, a); break;   \
+  case 3: hipLaunchKernelGGL((dec_linear_kernel<DTV, KCV, MB, CPL, WS, IN_LN, OUT_ARGMAX, ACT_NONE, false>), grid, dim3(256), lds, st, a); break; \
+  case 4: hipLaunchKernelGGL((dec_linear_kernel<DTV, KCV, MB, CPL, WS, IN_ATTN, OUT_ROW, ACT_NONE, true>), grid, dim3(256), lds, st, a); break;  \
+  default: return hipErrorInvalidValue;                                                                                      \
   }
-#define MH_DLS(DTV, MB)                                                          \
+#define MH_DLW(DTV, KCV, MB)                                                     \
   if (ws == 4) {                                                                 \
-    MH_DLK(DTV, MB, 1, 4)                                                        \
+    MH_DLK(DTV, KCV, MB, 1, 4)                                                   \
   } else if (cpl == 4) {                                                         \
     if (kind != 3) return hipErrorInvalidValue;                                  \
-    hipLaunchKernelGGL((dec_linear_kernel<DTV, 8, MB, 4, 1, IN_LN, OUT_ARGMAX, ACT_NONE, false>), grid, dim3(256), lds, st, a); \
+    hipLaunchKernelGGL((dec_linear_kernel<DTV, KCV, MB, 4, 1, IN_LN, OUT_ARGMAX, ACT_NONE, false>), grid, dim3(256), lds, st, a); \
   } else {                                                                       \
-    MH_DLK(DTV, MB, 1, 1)                                                        \
+    MH_DLK(DTV, KCV, MB, 1, 1)                                                   \
+  }
+#define MH_DLS(DTV, MB)         \
+  if (kch == 2) {               \
+    MH_DLW(DTV, 2, MB)          \
+  } else if (kch == 6) {        \
+    MH_DLW(DTV, 6, MB)          \
+  } else {                      \
+    MH_DLW(DTV, 8, MB)          \
   }
 #define MH_DL(DTV)              \
   if (few) {                    \
@@ -852,6 +864,7 @@ hipError_t dec_linear(int dt, int kind, const DecLinear &p, hipStream_t st) {
   }
 #undef MH_DL
 #undef MH_DLS
+#undef MH_DLW
 #undef MH_DLK
   return hipGetLastError();
 }
