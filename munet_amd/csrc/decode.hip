@@ -8,7 +8,9 @@
 // next B tokens.  M = B rows everywhere, so each Linear is a weight stream:
 // a wave per output column reads the column's K-contiguous weight row once
 // and keeps the B rows of its input in LDS.  The step position lives in
-// device memory (state[0]) so one captured graph serves every step:
+// device memory (state[0]) so a captured graph serves every step (the host
+// keeps one per count of 256-key attention blocks, 1..ceil(max_len / 256),
+// and launches the one whose blocks hold keys 0..pos):
 //   state[0] = pos: position of the tokens being fed
 //   state[1] = step index into the generated-token buffer
 //   state[2] = 1 while the head's greedy choices (best) are still to be fed
@@ -870,10 +872,10 @@ hipError_t dec_linear(int dt, int kind, const DecLinear &p, hipStream_t st) {
 }
 
 hipError_t dec_attention(int dt, const void *q, const void *kc, const void *vc, const int *state, float *part_o,
-                         float2 *part_ml, int B, int H, int hd, int Lmax, float scale, hipStream_t st) {
-  const int ns = (Lmax + kSplit - 1) / kSplit;
+                         float2 *part_ml, int B, int H, int hd, int Lmax, int blocks, float scale, hipStream_t st) {
+  const int ns = blocks;
   // (eight lanes of 8 dimensions per key row)
-  if (hd > 64 || hd % 8 != 0 || ns > kMaxSplit) return hipErrorInvalidValue;
+  if (hd > 64 || hd % 8 != 0 || ns < 1 || ns > kMaxSplit || ns > (Lmax + kSplit - 1) / kSplit) return hipErrorInvalidValue;
   const dim3 grid(ns, B * H);
   switch (dt) {
   case F32: hipLaunchKernelGGL(dec_attn_kernel<F32>, grid, dim3(kSplit), 0, st, (const float *)q, (const float *)kc, (const float *)vc, state, part_o, part_ml, H, hd, Lmax, scale); break;

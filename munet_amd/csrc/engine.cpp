@@ -1509,9 +1509,10 @@ struct mh_engine {
 // attention's keys are not per position, see decode.hip).  The prefill is the
 // engine's own forward for [B, T0] (one compiled instance per T0) with each
 // attention op also storing its k and v into the caches; each decode step is
-// one captured graph of weight-streaming kernels (decode.hip) that feeds B
-// tokens at the device-resident position and writes the B greedy choices
-// back as the next step's input.
+// one launch of a captured graph of weight-streaming kernels (decode.hip)
+// that feeds B tokens at the device-resident position and writes the B
+// greedy choices back as the next step's input (one graph per count of
+// 256-key attention blocks, chosen by the host from the position it tracks).
 struct mh_decoder {
   mh_engine *eng = nullptr;
   int dt = mh::BF16, B = 0, Lmax = 0, L = 0, d = 0, H = 0, hd = 0, ffn = 0, V = 0, C = 0, nsplit = 0;
@@ -1531,8 +1532,13 @@ struct mh_decoder {
   unsigned long long *best = nullptr;
   float *part_o = nullptr;
   float2 *part_ml = nullptr;
-  hipGraph_t graph = nullptr;
-  hipGraphExec_t exec = nullptr;
+  // one step graph per count of active 256-key attention blocks (1..nsplit):
+  // the step at position p runs graph p / 256 (its keys 0..p), so the
+  // attention launches only blocks holding keys and the out-projection
+  // combines only their shares (each of its blocks loads every head's
+  // shares: the load count, not the bytes, sets its input stage's time)
+  std::vector<hipGraph_t> graphs;
+  std::vector<hipGraphExec_t> execs;
   std::map<int, std::unique_ptr<mh::EngineImpl>> prefills;  // by prompt length
   int pos = -1;  // host copy of state[0]; -1 before the first prefill
   double last_step_ms = 0, last_generate_ms = 0, last_prefill_ms = 0;
@@ -1540,8 +1546,10 @@ struct mh_decoder {
 
   ~mh_decoder() {
     prefills.clear();
-    if (exec) (void)hipGraphExecDestroy(exec);
-    if (graph) (void)hipGraphDestroy(graph);
+    for (hipGraphExec_t x : execs)
+      if (x) (void)hipGraphExecDestroy(x);
+    for (hipGraph_t g : graphs)
+      if (g) (void)hipGraphDestroy(g);
     if (wbuf) (void)hipFree(wbuf);
     if (buf) (void)hipFree(buf);
     if (cache) (void)hipFree(cache);
@@ -1655,30 +1663,38 @@ struct mh_decoder {
     hip_check(hipMalloc(&cache, cache_bytes), "hipMalloc(KV cache)");
     hip_check(hipMemset(cache, 0, cache_bytes), "hipMemset(KV cache)");
 
-    // the step graph
-    hip_check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
-    try {
-      enqueue_step();
-    } catch (...) {
-      hipGraph_t g = nullptr;
-      (void)hipStreamEndCapture(stream, &g);
-      if (g) (void)hipGraphDestroy(g);
-      throw;
+    // the step graphs
+    graphs.assign(size_t(nsplit), nullptr);
+    execs.assign(size_t(nsplit), nullptr);
+    for (int nb = 1; nb <= nsplit; ++nb) {
+      hip_check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+      try {
+        enqueue_step(nb);
+      } catch (...) {
+        hipGraph_t g = nullptr;
+        (void)hipStreamEndCapture(stream, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+      }
+      hip_check(hipStreamEndCapture(stream, &graphs[nb - 1]), "hipStreamEndCapture");
+      hip_check(hipGraphInstantiate(&execs[nb - 1], graphs[nb - 1], nullptr, nullptr, 0), "hipGraphInstantiate");
     }
-    hip_check(hipStreamEndCapture(stream, &graph), "hipStreamEndCapture");
-    hip_check(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
   }
+
+  // the step graph for the tokens fed at position p (keys 0..p)
+  hipGraphExec_t exec_at(int p) const { return execs[size_t(std::min(nsplit, p / 256 + 1) - 1)]; }
 
   char *kcache(int l) const { return cache + size_t(l) * layer_bytes; }
   char *vcache(int l) const { return cache + (size_t(L) + l) * layer_bytes; }
 
-  void enqueue_step() {
+  // nb: attention blocks of 256 keys (those holding keys 0..pos)
+  void enqueue_step(int nb) {
     using mh::hip_check;
     const float gelu_c = mh::host_round(dt, 1.702f), scale = mh::host_round(dt, 1.0f / std::sqrt(float(hd)));
     hip_check(mh::dec_embed(dt, ids, best, tokens, state, tok, pos_tab, x, B, V, d, Lmax, mh::device_error_flag(), stream),
               "decode embed");
     mh::DecLinear p;
-    p.state = state; p.M = B; p.E = d; p.H = H; p.hd = hd; p.Lmax = Lmax; p.nsplit = nsplit; p.eps = eps;
+    p.state = state; p.M = B; p.E = d; p.H = H; p.hd = hd; p.Lmax = Lmax; p.nsplit = nb; p.eps = eps;
     p.gelu_c = gelu_c;
     for (int l = 0; l < L; ++l) {
       const LayerW &w = lw[l];
@@ -1686,7 +1702,7 @@ struct mh_decoder {
       a.x = x; a.w = w.wqkv; a.bias = w.bqkv; a.ln_w = w.ln1w; a.ln_b = w.ln1b; a.out = q;
       a.kc = kcache(l); a.vc = vcache(l); a.N = 3 * d; a.K = d;
       hip_check(mh::dec_linear(dt, 0, a, stream), "decode ln1 + qkv");
-      hip_check(mh::dec_attention(dt, q, kcache(l), vcache(l), state, part_o, part_ml, B, H, hd, Lmax, scale, stream),
+      hip_check(mh::dec_attention(dt, q, kcache(l), vcache(l), state, part_o, part_ml, B, H, hd, Lmax, nb, scale, stream),
                 "decode attention");
       mh::DecLinear o = p;  // attention shares -> out_proj + residual
       o.part_o = part_o; o.part_ml = part_ml; o.w = w.wo; o.bias = w.bo; o.resid = x; o.out = x1; o.N = d; o.K = d;
@@ -1764,7 +1780,7 @@ struct mh_decoder {
     require_room(1);
     if (hids) hip_check(hipMemcpyAsync(ids, hids, size_t(B) * 4, hipMemcpyHostToDevice, stream), "decoder ids H2D");
     hip_check(hipEventRecord(ev0, stream), "hipEventRecord");
-    hip_check(hipGraphLaunch(exec, stream), "hipGraphLaunch");
+    hip_check(hipGraphLaunch(exec_at(pos), stream), "hipGraphLaunch");
     finish();
     hip_check(hipEventRecord(ev1, stream), "hipEventRecord");
     if (logits_out)
@@ -1788,7 +1804,7 @@ struct mh_decoder {
     const int zero = 0;
     hip_check(hipMemcpyAsync(state + 1, &zero, sizeof(int), hipMemcpyHostToDevice, stream), "decoder state");
     hip_check(hipEventRecord(ev0, stream), "hipEventRecord");
-    for (int i = 0; i < n; ++i) hip_check(hipGraphLaunch(exec, stream), "hipGraphLaunch");
+    for (int i = 0; i < n; ++i) hip_check(hipGraphLaunch(exec_at(pos + i), stream), "hipGraphLaunch");
     finish();
     hip_check(hipEventRecord(ev1, stream), "hipEventRecord");
     if (tokens_out)
@@ -1806,7 +1822,7 @@ struct mh_decoder {
     std::ostringstream s;
     s << "{\"batch\":" << B << ",\"max_len\":" << Lmax << ",\"position\":" << pos << ",\"steps\":" << steps
       << ",\"weight_bytes\":" << wbytes << ",\"cache_bytes\":" << cache_bytes << ",\"buffer_bytes\":" << bufbytes
-      << ",\"kernels_per_step\":" << (2 + 5 * L) << ",\"last_step_ms\":" << last_step_ms
+      << ",\"kernels_per_step\":" << (2 + 5 * L) << ",\"step_graphs\":" << nsplit << ",\"last_step_ms\":" << last_step_ms
       << ",\"last_generate_ms\":" << last_generate_ms << ",\"last_prefill_ms\":" << last_prefill_ms
       << ",\"prefill_instances\":" << prefills.size() << "}";
     return s.str();

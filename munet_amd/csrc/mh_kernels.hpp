@@ -181,10 +181,11 @@ struct DecLinear {
   float eps = 1e-5f, gelu_c = 1.702f;
 };
 hipError_t dec_linear(int dt, int kind, const DecLinear &p, hipStream_t st);
-// One block per 256 keys of each head: shares part_o [B*H][blocks][hd],
-// part_ml [B*H][blocks] (blocks = ceil(Lmax / 256) <= 16)
+// One block per 256 keys of each head, blocks 0..blocks-1 (keys 0..256
+// blocks - 1, which must hold the position; blocks <= ceil(Lmax / 256) <= 16):
+// shares part_o [B*H][blocks][hd], part_ml [B*H][blocks]
 hipError_t dec_attention(int dt, const void *q, const void *kc, const void *vc, const int *state, float *part_o,
-                         float2 *part_ml, int B, int H, int hd, int Lmax, float scale, hipStream_t st);
+                         float2 *part_ml, int B, int H, int hd, int Lmax, int blocks, float scale, hipStream_t st);
 // When choices are pending: best [B] -> ids [B] and tokens[step] (best
 // reset), position and step + 1 (after the last step of a call)
 hipError_t dec_finish(unsigned long long *best, int32_t *ids, int32_t *tokens, int *state, int B, int cap,

@@ -143,6 +143,27 @@ def test_decode_launch_shapes_vs_oracle(orc, case):
         _steps_vs_oracle(orc, cfg, 5 if dt == "float16" else 3, 64, "dls_" + case)
 
 
+def test_decode_across_key_block_boundary(orc):
+    """The step at position p runs the graph with p // 256 + 1 attention
+    blocks (those holding keys 0..p), the out-projection combining that
+    many shares: steps at positions 250..261 switch graphs at 256, against
+    the oracle, and generate() across the switch repeats the single steps'
+    tokens."""
+    cfg = models.decoder_config(vocab=500, ctx=640, d_model=128, num_heads=2, num_layers=2, ffn=256,
+                                dtype="bfloat16", attention="textbook")
+    _steps_vs_oracle(orc, cfg, 2, 600, "dls_kb", T0=250, n=12)
+    p = models.init_params(cfg, "gpt", scope="dls_kb")
+    prompt = models.make_input(cfg, (2, 250), "gpt", scope="dls_kb_in")
+    eng = Engine(0).load(cfg, p).compile((2, 250))
+    dcd = Decoder(eng, 2, 600)
+    assert dcd.stats()["step_graphs"] == 3
+    dcd.prefill(prompt, logits=False)
+    toks = [dcd.step()[1] for _ in range(12)]
+    dcd.prefill(prompt, logits=False)
+    gen, _ = dcd.generate(12)
+    assert np.array_equal(gen, np.stack(toks))
+
+
 def test_decode_explicit_ids_and_generate_repeat_step(orc):
     """step(ids) feeds the given tokens; generate(n) after the same prefill
     repeats step()'s greedy tokens bit for bit."""
