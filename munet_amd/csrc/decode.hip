@@ -813,8 +813,9 @@ hipError_t dec_linear(int dt, int kind, const DecLinear &p, hipStream_t st) {
   // at d 768), also splits K over four waves: four times the blocks, each
   // streaming a quarter of the bytes (5.19 -> 4.72 us at d 768, B 4).  The
   // LayerNorm-input products do not: four waves per column group slowed
-  // QKV and FFN up from 4.8 to 12.9 us (their input stage holds 8 chunks per
-  // lane for every row).
+  // QKV and FFN up from 4.8 to 12.9 us when their input stage held 8 chunks
+  // per lane for every row, and the step from 0.257 to 0.280 ms with it sized
+  // to K (two chunks): four times the blocks each repeat the LayerNorm stage.
   if (KC > 512) return hipErrorInvalidValue;
   const bool narrow = kind == 4 && (p.N + 15) / 16 < 256;
   const int ws = (KC > 128 || narrow) ? 4 : 1, cpl = (kind == 3 && ws == 1 && p.N >= 8192) ? 4 : 1;
