@@ -111,8 +111,9 @@ def test_decode_launch_shapes_vs_oracle(orc, case):
     wide_batch_bf16: batch 8 at d 512 (the 16-row kernels, and B*d > 3072,
     so the out-projection combines the attention shares in its input-stage
     loop instead of loading them ahead of the weights);
-    long_cache_f32: a 1280-position cache (five 256-key shares per head:
-    the same combine loop);
+    long_cache_f32: a 1280-position cache with a 1100-token prompt (the
+    steps run the five-block graph: five 256-key shares per head, the same
+    combine loop);
     four_wave_f16 / four_wave_f32: FFN down with K past 128 chunks (its K
     split over the block's four waves), batches 5 and 3, and a vocabulary of
     8192 (the head's four-columns-per-row kernel);
@@ -127,7 +128,7 @@ def test_decode_launch_shapes_vs_oracle(orc, case):
     elif case == "long_cache_f32":
         cfg = models.decoder_config(vocab=500, ctx=1280, d_model=128, num_heads=2, num_layers=2, ffn=256,
                                     dtype="float32", attention="textbook")
-        _steps_vs_oracle(orc, cfg, 2, 1280, "dls_lc")
+        _steps_vs_oracle(orc, cfg, 2, 1280, "dls_lc", T0=1100, n=6)
     elif case == "head_dim_32_bf16":
         cfg = models.decoder_config(vocab=500, ctx=96, d_model=128, num_heads=4, num_layers=2, ffn=256,
                                     dtype="bfloat16", attention="textbook")
