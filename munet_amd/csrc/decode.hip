@@ -26,7 +26,7 @@
 namespace mh {
 namespace {
 
-constexpr int kSplit = 256;  // keys per attention block
+constexpr int kSplit = kDecKeyBlock;  // keys per attention block
 
 template <int DT> struct Chunk {
   typedef typename Store<DT>::T T;

@@ -1582,7 +1582,7 @@ struct mh_decoder {
     if (size_t(batch) * std::max(d, ffn) * es > 65536) throw Error("decoder: batch x width exceeds the 64 KiB row stage");
     B = batch;
     Lmax = max_len;
-    nsplit = (Lmax + 255) / 256;
+    nsplit = (Lmax + mh::kDecKeyBlock - 1) / mh::kDecKeyBlock;
 
     // weights, packed as the decode kernels read them ([out, in] rows)
     mh::EngineImpl pk;
@@ -1682,7 +1682,7 @@ struct mh_decoder {
   }
 
   // the step graph for the tokens fed at position p (keys 0..p)
-  hipGraphExec_t exec_at(int p) const { return execs[size_t(std::min(nsplit, p / 256 + 1) - 1)]; }
+  hipGraphExec_t exec_at(int p) const { return execs[size_t(std::min(nsplit, p / mh::kDecKeyBlock + 1) - 1)]; }
 
   char *kcache(int l) const { return cache + size_t(l) * layer_bytes; }
   char *vcache(int l) const { return cache + (size_t(L) + l) * layer_bytes; }

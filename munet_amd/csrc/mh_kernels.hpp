@@ -181,6 +181,8 @@ struct DecLinear {
   float eps = 1e-5f, gelu_c = 1.702f;
 };
 hipError_t dec_linear(int dt, int kind, const DecLinear &p, hipStream_t st);
+// Keys per decode attention block.
+constexpr int kDecKeyBlock = 256;
 // One block per 256 keys of each head, blocks 0..blocks-1 (keys 0..256
 // blocks - 1, which must hold the position; blocks <= ceil(Lmax / 256) <= 16):
 // shares part_o [B*H][blocks][hd], part_ml [B*H][blocks]
