@@ -401,8 +401,7 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
 #pragma unroll
       for (int t = 0; t < FN; ++t)
         if (t <= j && t > j - G16) s += (a.y[t][0] + a.y[t][1]) + (a.y[t][2] + a.y[t][3]);
-      s += __shfl_xor(s, 16);
-      s += __shfl_xor(s, 32);
+      s = xor32_add(xor16_add(s));
       const float mu = s / float(ep.stats_cols);
       float q = 0.f;
 #pragma unroll
@@ -413,8 +412,7 @@ template <int DT, int BM, int BN, int WGM, int WGN, int EK> struct PipeEpi {
             const float dv = __fsub_rn(a.y[t][e], mu);
             q = __fmaf_rn(dv, dv, q);  // explicit: the same rounding in every tile
           }
-      q += __shfl_xor(q, 16);
-      q += __shfl_xor(q, 32);
+      q = xor32_add(xor16_add(q));
       const int g0 = n0 + g.wn * WTN + (j + 1) * 16 - ep.stats_cols;  // first column of the group
       if (g.lg == 0 && m < M && g0 < N)
         *reinterpret_cast<float2 *>(ep.stats_out + 2 * (long(m) * (N / ep.stats_cols) + g0 / ep.stats_cols)) =

@@ -221,6 +221,21 @@ __device__ __forceinline__ float rows4_max(float v) {
 // Every lane of the wave must be active.
 __device__ __forceinline__ float wave_sum_dpp(float v) { return rows4_sum(row16_sum(v)); }
 
+// v[l] + v[l ^ 16] and v[l] + v[l ^ 32] through gfx950's VALU lane swaps
+// instead of __shfl_xor's permute through the LDS pipe: v_permlane16_swap of v
+// with itself leaves v[l] and v[l ^ 16] in its two results at every lane
+// (the odd 16-lane rows of one operand traded with the even rows of the
+// other), v_permlane32_swap v[l] and v[l ^ 32] (the halves traded); the sum
+// of the two is the shuffle sum, bit for bit.  Every lane must be active.
+__device__ __forceinline__ float xor16_add(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_add(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Eight 16-bit values of one 16-byte chunk decoded to / encoded from floats.
 template <int DT> __device__ __forceinline__ void dec8(uint4 c, float v[8]) {
   const uint32_t w[4] = {c.x, c.y, c.z, c.w};
