@@ -740,9 +740,9 @@ flash_attn_pipe_kernel(const uint16_t *__restrict__ Q, const uint16_t *__restric
   auto trip = [&](int t, auto bcc, auto bnc, auto bfc) {
     constexpr int bc = decltype(bcc)::value, bn = decltype(bnc)::value, bf = decltype(bfc)::value;
     // raise the row max only when some lane's own max exceeds it by 2^kRaise
+    // (a wave-uniform branch: every lane runs the lane swaps)
     if (__any(mx * c2 > mrow + kRaise)) {
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = xor32_max(xor16_max(mx));
       const float mnew = fmaxf(mrow, mx * c2);
       const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
       mrow = mnew;

@@ -235,6 +235,15 @@ __device__ __forceinline__ float xor32_add(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+// fmaxf(v[l], v[l ^ 16]) and fmaxf(v[l], v[l ^ 32]) the same way
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 
 // Eight 16-bit values of one 16-byte chunk decoded to / encoded from floats.
 template <int DT> __device__ __forceinline__ void dec8(uint4 c, float v[8]) {
